@@ -1,0 +1,221 @@
+/*
+ * secure_infer for MI355X (gfx950): C-ABI of libsecure_infer.so.
+ *
+ * The library implements the authenticated KV reload (H2D) and writeback
+ * (D2H) data plane of secure_infer: AES-128-GCM records (one per 128-token
+ * block, layer and K/V kind) verified and decrypted (or encrypted and tagged)
+ * on the GPU by hand-written HIP kernels, with the int8/int4 transport codec
+ * and the paged-cache scatter/gather in the same launch sequence.
+ *
+ * Conventions (same as the reference's device ABI, launcher.asc:23-524):
+ *   - every function returns 0 when the work was enqueued and -1 on a null or
+ *     zero argument or a launch failure;
+ *   - all buffer pointers are device addresses unless stated otherwise;
+ *   - work is asynchronous on `stream`; authentication failure is data:
+ *     the record's status word is 0 and its output is all zeros, success
+ *     writes status 1 (ghash.aicpu:637-648, 1051-1068).
+ *
+ * A "record" on the wire is [ciphertext count B][zero pad to 32][tag 16]
+ * [status 16][AAD 64], the reference's H2D wire record
+ * (secure_infer.cpp:6319-6320, 6379-6388, 6529-6537, 6654-6657).
+ */
+#ifndef SECURE_INFER_GPU_H
+#define SECURE_INFER_GPU_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* 1. Kernel-level entry points.  Same argument order and meaning as the
+ *    reference's secure_infer_aicpu_*_do launchers (launcher.asc), with a
+ *    hipStream_t in place of the ACL stream.  `key` (16 B) and `hash_subkey`
+ *    (H = E_K(0^128), 16 B) are device buffers; the library reads them back
+ *    once per call to select its per-key tables, so these calls wait for
+ *    work already queued on `stream`.                                     */
+
+/* launcher.asc:214-241, ghash.aicpu:594-651 */
+int secure_infer_gpu_gcm_decrypt_verify_do(
+    hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+    void* expected_tag, void* plaintext_output, void* status_output,
+    uint64_t bytes, uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2,
+    uint32_t iv_word3);
+
+/* launcher.asc:245-275 */
+int secure_infer_gpu_gcm_decrypt_verify_aad_do(
+    hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+    void* expected_tag, void* plaintext_output, void* status_output,
+    uint64_t bytes, uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2,
+    uint32_t iv_word3, void* aad, uint64_t aad_bytes);
+
+/* launcher.asc:279-308, ghash.aicpu:656-699 */
+int secure_infer_gpu_gcm_encrypt_tag_do(
+    hipStream_t stream, void* plaintext, void* key, void* hash_subkey,
+    void* ciphertext_output, void* tag_output, uint64_t bytes,
+    uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2, uint32_t iv_word3,
+    void* aad, uint64_t aad_bytes);
+
+/* launcher.asc:407-435, ghash.aicpu:780-827 */
+int secure_infer_gpu_gcm_verify_only_aad_do(
+    hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+    void* expected_tag, void* status_output, uint64_t bytes,
+    uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2, uint32_t iv_word3,
+    void* aad, uint64_t aad_bytes);
+
+/* launcher.asc:343-376, ghash.aicpu:705-773 */
+int secure_infer_gpu_gcm_verify_xor_aad_do(
+    hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+    void* expected_tag, void* keystream, void* plaintext_output,
+    void* status_output, uint64_t bytes, uint32_t iv_word0, uint32_t iv_word1,
+    uint32_t iv_word2, uint32_t iv_word3, void* aad, uint64_t aad_bytes);
+
+/* launcher.asc:134-155, ghash.aicpu:517-535 */
+int secure_infer_gpu_aes_ctr_do(
+    hipStream_t stream, void* input, void* key, void* output, uint64_t bytes,
+    uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2, uint32_t iv_word3);
+
+/* launcher.asc:160-179, ghash.aicpu:537-554 */
+int secure_infer_gpu_keystream_do(
+    hipStream_t stream, void* key, void* output, uint64_t bytes,
+    uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2, uint32_t iv_word3);
+
+/* launcher.asc:116-132, ghash.aicpu:1051-1068: zero `bytes` of `data`
+ * unless *status == 1. */
+int secure_infer_gpu_auth_gate_do(hipStream_t stream, void* data, void* status,
+                                  uint64_t bytes);
+
+/* ------------------------------------------------------------------ */
+/* 2. Sessions and layer-level fused entry points.
+ *
+ * A session holds one AES-128 key on the device together with its GHASH
+ * tables (the reference keeps the key device-resident per session,
+ * secure_infer.cpp:449-609).  The IV of record r is
+ *   iv_salt[4] || BE64(session_nonce + ticket) || BE32(2)
+ * (secure_infer_derive_transfer_iv, secure_infer.cpp:274-300).            */
+
+typedef struct si_session si_session;
+
+int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt[4],
+                                    uint64_t session_nonce, uint64_t max_record_bytes,
+                                    si_session** out);
+int secure_infer_gpu_session_destroy(si_session* session);
+/* H = E_K(0^128) of the session (host copy, 16 B). */
+int secure_infer_gpu_session_hash_subkey(const si_session* session, uint8_t out[16]);
+
+/* Codec modes of the KV transport codec (transport_codec.py:9-19). */
+enum {
+    SI_CODEC_NONE = 0, /* bf16 records, ciphertext = raw KV block */
+    SI_CODEC_INT8 = 8,
+    SI_CODEC_INT4 = 4,
+};
+
+/* One layer of authenticated reload: records [0, n_k) are K blocks and
+ * [n_k, nrec) are V blocks; record r decrypts into
+ * cache[kind] + slots[r] * slot_bytes.  Replaces the per-layer swap_blocks
+ * calls of NativeTransfer.single_layer_kv_transfer (native_layerwise.py:94-130)
+ * and the staged decode_into of PipelinedTransfer (pipelined_codec.py:113-139). */
+typedef struct si_reload_desc {
+    const void* wire;         /* device: nrec records of wire_stride bytes      */
+    uint64_t wire_stride;     /* >= align32(bytes) + 96                        */
+    uint64_t bytes;           /* ciphertext bytes per record (count)           */
+    uint32_t nrec;
+    uint32_t n_k;
+    const uint32_t* iv_words; /* device, 4 BE words per record; NULL: derive   */
+    uint64_t ticket_base;     /* ticket of record 0 when iv_words == NULL      */
+    void* cache_k;            /* device paged cache of this layer, kind 0      */
+    void* cache_v;            /* device paged cache of this layer, kind 1      */
+    uint64_t slot_bytes;      /* bytes of one 128-token block in the cache     */
+    uint64_t nslots;          /* slots per cache; out-of-range ids fail closed */
+    const int64_t* slots;     /* device, one slot id per record                */
+    uint32_t codec_bits;      /* SI_CODEC_NONE / INT8 / INT4                   */
+    uint32_t heads;           /* kv heads (codec only)                         */
+    uint32_t head_dim;        /* head dim (codec only)                         */
+    uint32_t layer;           /* layer index (codec header, status)            */
+    void* staging;            /* device scratch, nrec*align32(bytes) (codec)   */
+    uint32_t* fail_count;     /* device u32: += number of failed records; NULL ok */
+} si_reload_desc;
+
+int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* session,
+                                  const si_reload_desc* desc);
+
+/* One layer of writeback: record r gathers cache[kind] + slots[r]*slot_bytes,
+ * optionally quantises it with the transport codec, encrypts it and writes the
+ * ciphertext and tag into its wire record (the AAD must already be there).
+ * Replaces the D2H branch of the reference (secure_infer.cpp:8076-8562 with
+ * gcm_encrypt_tag, ghash.aicpu:656-699) plus transport_codec.encode. */
+typedef struct si_writeback_desc {
+    void* wire;
+    uint64_t wire_stride;
+    uint64_t bytes;           /* plaintext (packet) bytes per record           */
+    uint32_t nrec;
+    uint32_t n_k;
+    const uint32_t* iv_words;
+    uint64_t ticket_base;
+    const void* cache_k;
+    const void* cache_v;
+    uint64_t slot_bytes;
+    uint64_t nslots;
+    const int64_t* slots;
+    uint32_t codec_bits;
+    uint32_t heads;
+    uint32_t head_dim;
+    uint32_t layer;
+    void* staging;            /* device scratch, nrec*align32(bytes) (codec)   */
+    uint32_t* fail_count;     /* device u32: += records with a bad slot id     */
+} si_writeback_desc;
+
+int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* session,
+                                     const si_writeback_desc* desc);
+
+/* Size helpers of the codec packet (transport_codec.py:22-42). */
+uint64_t secure_infer_codec_width(uint32_t bits, uint32_t heads, uint32_t head_dim);
+uint64_t secure_infer_wire_stride(uint64_t bytes);
+
+/* ------------------------------------------------------------------ */
+/* 3. Control plane with the reference's names and semantics.            */
+
+/* secure_infer.cpp:261-272: process-monotonic ticket from 1. */
+uint64_t secure_infer_new_transfer_ticket(void);
+/* secure_infer.cpp:274-300 (GCM counter base 2). Returns 0, or -1 on ticket 0. */
+int secure_infer_derive_transfer_iv(const uint8_t base_iv[16], uint64_t session_nonce,
+                                    uint64_t ticket, uint64_t block_offset,
+                                    uint8_t out_iv[16]);
+/* secure_infer.cpp:1066-1091 (host address ranges -> layer / kind / block). */
+void secure_infer_register_host_range_ex(const void* base, size_t bytes, uint32_t layer_id,
+                                         uint32_t tensor_kind, size_t block_bytes);
+void secure_infer_clear_host_ranges(void);
+/* secure_infer.cpp:730-775: 64-B AAD for a registered host address.
+ * Returns 1 on success, 0 on invalid arguments. */
+int secure_infer_build_gcm_aad(const void* host_ptr, size_t bytes, uint8_t direction,
+                               uint64_t transfer_ticket, uint64_t transfer_offset,
+                               uint64_t session_nonce, uint8_t out[64]);
+/* secure_infer.cpp:777-789: 1 if the ticket was not seen before, else 0. */
+int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket);
+
+/* secure_infer.cpp:5883-5903: layer-group brackets (thread-local). */
+int secure_infer_h2d_layer_group_begin(size_t expected);
+int secure_infer_h2d_layer_group_end(void);
+
+/* secure_infer.cpp:7303-7333: 0 if every record submitted for `layer` since
+ * the last wait authenticated, -1 otherwise.  Waits for the layer's work. */
+int secure_infer_recovery_wait_layer_authentication(uint32_t layer);
+/* Registers a reload of `layer` whose per-record statuses land in the device
+ * u32 `fail_count` once `event` completes (library-internal bookkeeping used
+ * by the Python layer driver). */
+int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event,
+                                      const uint32_t* fail_count);
+
+/* Library build / device information. */
+const char* secure_infer_gpu_version(void);
+/* Tuning: maximum rows (blocks per thread) of one workgroup chunk, 1..256
+ * (default 16).  No reference counterpart; used by the benchmark sweep. */
+int secure_infer_gpu_set_chunk_rows(int jmax);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,791 @@
+// libsecure_infer.so host side: per-key GCM contexts, sessions, ticket / IV /
+// AAD bookkeeping and the C-ABI declared in include/secure_infer_gpu.h.
+#include "secure_infer_gpu.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "si_device.h"
+#include "si_kernels.h"
+
+namespace {
+
+// ---------------------------------------------------------------- AES (host)
+// FIPS-197; the S-box is derived from GF(2^8) inversion and the affine map.
+
+uint8_t gf8_mul(uint8_t a, uint8_t b)
+{
+    uint8_t r = 0;
+    while (b) {
+        if (b & 1) r ^= a;
+        a = uint8_t((a << 1) ^ ((a & 0x80) ? 0x1b : 0));
+        b >>= 1;
+    }
+    return r;
+}
+
+struct Sbox {
+    uint8_t s[256];
+    Sbox()
+    {
+        for (int x = 0; x < 256; ++x) {
+            uint8_t inv = 0;
+            if (x) {
+                uint8_t p = uint8_t(x), acc = 1;
+                for (int e = 254; e; e >>= 1) {
+                    if (e & 1) acc = gf8_mul(acc, p);
+                    p = gf8_mul(p, p);
+                }
+                inv = acc;
+            }
+            uint8_t b = inv, r = inv;
+            for (int k = 1; k <= 4; ++k) {
+                b = uint8_t((b << 1) | (b >> 7));
+                r ^= b;
+            }
+            s[x] = uint8_t(r ^ 0x63);
+        }
+    }
+};
+const Sbox& sbox()
+{
+    static const Sbox s;
+    return s;
+}
+
+void aes_expand(const uint8_t key[16], uint8_t rk[176])
+{
+    const uint8_t* S = sbox().s;
+    memcpy(rk, key, 16);
+    uint8_t rcon = 1;
+    for (int i = 4; i < 44; ++i) {
+        uint8_t t[4];
+        memcpy(t, rk + 4 * (i - 1), 4);
+        if ((i & 3) == 0) {
+            const uint8_t f = t[0];
+            t[0] = uint8_t(S[t[1]] ^ rcon);
+            t[1] = S[t[2]];
+            t[2] = S[t[3]];
+            t[3] = S[f];
+            rcon = gf8_mul(rcon, 2);
+        }
+        for (int j = 0; j < 4; ++j) rk[4 * i + j] = uint8_t(rk[4 * (i - 4) + j] ^ t[j]);
+    }
+}
+
+void aes_encrypt(const uint8_t rk[176], const uint8_t in[16], uint8_t out[16])
+{
+    const uint8_t* S = sbox().s;
+    uint8_t s[16], t[16];
+    for (int i = 0; i < 16; ++i) s[i] = uint8_t(in[i] ^ rk[i]);
+    for (int round = 1; round <= 10; ++round) {
+        for (int c = 0; c < 4; ++c)
+            for (int r = 0; r < 4; ++r) t[r + 4 * c] = S[s[r + 4 * ((c + r) & 3)]];
+        if (round < 10) {
+            for (int c = 0; c < 4; ++c) {
+                const uint8_t* a = t + 4 * c;
+                s[4 * c + 0] = uint8_t(gf8_mul(a[0], 2) ^ gf8_mul(a[1], 3) ^ a[2] ^ a[3]);
+                s[4 * c + 1] = uint8_t(a[0] ^ gf8_mul(a[1], 2) ^ gf8_mul(a[2], 3) ^ a[3]);
+                s[4 * c + 2] = uint8_t(a[0] ^ a[1] ^ gf8_mul(a[2], 2) ^ gf8_mul(a[3], 3));
+                s[4 * c + 3] = uint8_t(gf8_mul(a[0], 3) ^ a[1] ^ a[2] ^ gf8_mul(a[3], 2));
+            }
+        } else {
+            memcpy(s, t, 16);
+        }
+        for (int i = 0; i < 16; ++i) s[i] ^= rk[16 * round + i];
+    }
+    memcpy(out, s, 16);
+}
+
+uint32_t le32(const uint8_t* p) { return uint32_t(p[0]) | uint32_t(p[1]) << 8 | uint32_t(p[2]) << 16 | uint32_t(p[3]) << 24; }
+uint32_t be32(const uint8_t* p) { return uint32_t(p[0]) << 24 | uint32_t(p[1]) << 16 | uint32_t(p[2]) << 8 | uint32_t(p[3]); }
+void put_be32(uint8_t* p, uint32_t v) { p[0] = uint8_t(v >> 24); p[1] = uint8_t(v >> 16); p[2] = uint8_t(v >> 8); p[3] = uint8_t(v); }
+void put_be64(uint8_t* p, uint64_t v) { for (int i = 0; i < 8; ++i) p[i] = uint8_t(v >> (56 - 8 * i)); }
+
+// ---------------------------------------------------------------- GF(2^128) (host)
+// Elements as 16 bytes in GCM order (bit 0 = MSB of byte 0 = x^0).
+
+struct Blk {
+    uint8_t b[16];
+};
+
+Blk gf_mul(const Blk& x, const Blk& y)
+{
+    // right-shift multiply (SP 800-38D Algorithm 1) on two 64-bit halves
+    uint64_t vh = 0, vl = 0, zh = 0, zl = 0;
+    for (int i = 0; i < 8; ++i) {
+        vh = vh << 8 | y.b[i];
+        vl = vl << 8 | y.b[8 + i];
+    }
+    for (int i = 0; i < 128; ++i) {
+        if ((x.b[i >> 3] >> (7 - (i & 7))) & 1) {
+            zh ^= vh;
+            zl ^= vl;
+        }
+        const uint64_t lsb = vl & 1;
+        vl = (vl >> 1) | (vh << 63);
+        vh >>= 1;
+        if (lsb) vh ^= 0xe100000000000000ull;
+    }
+    Blk z;
+    for (int i = 0; i < 8; ++i) {
+        z.b[i] = uint8_t(zh >> (56 - 8 * i));
+        z.b[8 + i] = uint8_t(zl >> (56 - 8 * i));
+    }
+    return z;
+}
+
+// Fast multiply by one fixed element with 16 per-nibble-position tables.
+struct FixedMul {
+    Blk t[32][16];
+    explicit FixedMul(const Blk& h)
+    {
+        for (int p = 0; p < 32; ++p)
+            for (int v = 0; v < 16; ++v) {
+                Blk x{};
+                x.b[p >> 1] = uint8_t((p & 1) ? v << 4 : v);
+                t[p][v] = gf_mul(x, h);
+            }
+    }
+    Blk operator()(const Blk& x) const
+    {
+        Blk z{};
+        for (int p = 0; p < 32; ++p) {
+            const int v = (x.b[p >> 1] >> ((p & 1) * 4)) & 15;
+            for (int k = 0; k < 16; ++k) z.b[k] ^= t[p][v].b[k];
+        }
+        return z;
+    }
+};
+
+// ---------------------------------------------------------------- contexts
+
+struct DevCtx {
+    si::GcmCtx* dev = nullptr;
+    uint32_t npow = 0;
+    uint8_t key[16];
+    uint8_t h[16];
+    ~DevCtx()
+    {
+        if (dev) (void)hipFree(dev);
+    }
+};
+
+std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], uint32_t npow)
+{
+    std::vector<uint8_t> img(sizeof(si::GcmCtx) + size_t(npow) * 16, 0);
+    auto* c = reinterpret_cast<si::GcmCtx*>(img.data());
+    uint8_t rk[176];
+    aes_expand(key, rk);
+    for (int i = 0; i < 44; ++i) {
+        c->rk[i] = le32(rk + 4 * i);
+        c->rk16[i] = (c->rk[i] << 16) | (c->rk[i] >> 16);
+    }
+    const uint8_t* S = sbox().s;
+    for (int x = 0; x < 256; ++x) {
+        const uint32_t s = S[x], s2 = gf8_mul(uint8_t(s), 2), s3 = gf8_mul(uint8_t(s), 3);
+        c->te0[x] = s2 | (s << 8) | (s << 16) | (s3 << 24);
+    }
+    for (int k = 0; k < 4; ++k) c->h[k] = le32(h + 4 * k);
+    c->npow = npow;
+    Blk hb;
+    memcpy(hb.b, h, 16);
+    const FixedMul mh(hb);
+    Blk p{};
+    p.b[0] = 0x80;  // H^0 = 1
+    auto* pow = reinterpret_cast<uint8_t*>(c + 1);
+    Blk ht{};
+    for (uint32_t e = 0; e < npow; ++e) {
+        memcpy(pow + 16 * size_t(e), p.b, 16);
+        if (e == SI_T) ht = p;
+        p = mh(p);
+    }
+    if (npow <= SI_T) {
+        ht = Blk{};
+        ht.b[0] = 0x80;
+        for (int e = 0; e < SI_T; ++e) ht = mh(ht);
+    }
+    const FixedMul mt(ht);
+    for (int pos = 0; pos < 32; ++pos)
+        for (int v = 0; v < 16; ++v) {
+            const Blk& e = mt.t[pos][v];
+            c->gh4[pos * 16 + v] = make_uint4(le32(e.b), le32(e.b + 4), le32(e.b + 8), le32(e.b + 12));
+        }
+    auto out = std::make_unique<DevCtx>();
+    if (hipMalloc(&out->dev, img.size()) != hipSuccess) return nullptr;
+    if (hipMemcpy(out->dev, img.data(), img.size(), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    out->npow = npow;
+    memcpy(out->key, key, 16);
+    memcpy(out->h, h, 16);
+    return out;
+}
+
+int g_jmax = 16;
+
+si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
+{
+    si::Sched s{};
+    s.nrec = nrec;
+    s.bytes = bytes;
+    s.aad_bytes = uint32_t(aad_bytes);
+    s.a = uint32_t((aad_bytes + 15) / 16);
+    s.n = uint32_t((bytes + 15) / 16);
+    const uint64_t m = uint64_t(s.a) + s.n + 1;
+    const uint64_t chmax = uint64_t(SI_T) * uint64_t(g_jmax);
+    s.nc = uint32_t((m + chmax - 1) / chmax);
+    s.j = uint32_t((m + uint64_t(s.nc) * SI_T - 1) / (uint64_t(s.nc) * SI_T));
+    return s;
+}
+
+uint32_t npow_for(uint64_t bytes, uint64_t aad_bytes)
+{
+    return uint32_t((aad_bytes + 15) / 16 + (bytes + 15) / 16 + 1 + SI_T + 16);
+}
+
+std::mutex g_lock;
+std::vector<std::unique_ptr<DevCtx>> g_ctx_cache;  // compat entry points, keyed by (key, H)
+
+// Per-stream accumulator workspaces.
+struct Workspace {
+    si::RecAcc* acc = nullptr;
+    size_t cap = 0;
+};
+std::unordered_map<hipStream_t, Workspace> g_ws;
+
+si::RecAcc* workspace(hipStream_t stream, size_t nrec)
+{
+    Workspace& w = g_ws[stream];
+    if (w.cap >= nrec) return w.acc;
+    if (w.acc) {
+        if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+        (void)hipFree(w.acc);
+        w.acc = nullptr;
+        w.cap = 0;
+    }
+    size_t cap = 256;
+    while (cap < nrec) cap *= 2;
+    if (hipMalloc(&w.acc, cap * sizeof(si::RecAcc)) != hipSuccess) return nullptr;
+    if (hipMemset(w.acc, 0, cap * sizeof(si::RecAcc)) != hipSuccess) return nullptr;
+    w.cap = cap;
+    return w.acc;
+}
+
+DevCtx* ctx_for_device_key(hipStream_t stream, const void* key, const void* h, uint32_t npow)
+{
+    uint8_t kb[16], hb[16] = {0};
+    if (hipMemcpyAsync(kb, key, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+    if (h && hipMemcpyAsync(hb, h, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    for (auto& c : g_ctx_cache)
+        if (!memcmp(c->key, kb, 16) && !memcmp(c->h, hb, 16) && c->npow >= npow) return c.get();
+    auto c = build_ctx(kb, hb, npow);
+    if (!c) return nullptr;
+    if (g_ctx_cache.size() >= 8) {
+        if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+        g_ctx_cache.erase(g_ctx_cache.begin());
+    }
+    g_ctx_cache.push_back(std::move(c));
+    return g_ctx_cache.back().get();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int run_single(int mode, hipStream_t stream, void* src, void* key, void* h, void* tag, void* dst,
+               void* status, const void* ks, uint64_t bytes, const uint32_t iv[4], void* aad,
+               uint64_t aad_bytes)
+{
+    std::lock_guard<std::mutex> g(g_lock);
+    DevCtx* c = ctx_for_device_key(stream, key, h, npow_for(bytes, aad_bytes));
+    if (!c) return -1;
+    si::RecAcc* acc = workspace(stream, 1);
+    if (!acc) return -1;
+    si::RecBatch b{};
+    b.single = 1;
+    b.src = static_cast<const uint8_t*>(src);
+    b.dst = static_cast<uint8_t*>(dst);
+    b.aad = static_cast<const uint8_t*>(aad);
+    b.tag = static_cast<uint8_t*>(tag);
+    b.status = static_cast<uint32_t*>(status);
+    b.ks = static_cast<const uint8_t*>(ks);
+    for (int k = 0; k < 4; ++k) b.iv[k] = iv[k];
+    const si::Sched s = make_sched(1, bytes, aad_bytes);
+    const bool al = aligned16(src) && (!dst || aligned16(dst)) && (!ks || aligned16(ks));
+    return si::launch_gcm(mode, stream, c->dev, b, s, acc, al) == hipSuccess ? 0 : -1;
+}
+
+// ---------------------------------------------------------------- control plane state
+
+std::atomic<uint64_t> g_next_ticket{1};
+
+struct HostRange {
+    uintptr_t begin, end;
+    uint32_t layer, kind;
+    size_t block_bytes;
+};
+std::mutex g_ranges_lock;
+std::vector<HostRange> g_ranges;
+
+std::mutex g_replay_lock;
+std::unordered_set<uint64_t> g_replay;
+
+thread_local int64_t t_group_expected = -1;
+
+struct TrackedLayer {
+    hipEvent_t event;
+    const uint32_t* fail_count;
+};
+std::mutex g_track_lock;
+std::multimap<uint32_t, TrackedLayer> g_tracked;
+
+}  // namespace
+
+// ---------------------------------------------------------------- sessions
+
+struct si_session {
+    std::unique_ptr<DevCtx> ctx;
+    uint32_t salt_word;
+    uint64_t session_nonce;
+    uint64_t max_record_bytes;
+};
+
+extern "C" {
+
+const char* secure_infer_gpu_version(void)
+{
+    return "secure_infer_amd 0.1 (gfx950, AES-128-GCM T-table/LDS, 4-bit GHASH tables)";
+}
+
+int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt[4],
+                                    uint64_t session_nonce, uint64_t max_record_bytes,
+                                    si_session** out)
+{
+    if (!key || !iv_salt || !out || max_record_bytes == 0) return -1;
+    uint8_t rk[176], h[16], zero[16] = {0};
+    aes_expand(key, rk);
+    aes_encrypt(rk, zero, h);
+    auto s = std::make_unique<si_session>();
+    s->ctx = build_ctx(key, h, npow_for(max_record_bytes, 64));
+    if (!s->ctx) return -1;
+    s->salt_word = be32(iv_salt);
+    s->session_nonce = session_nonce;
+    s->max_record_bytes = max_record_bytes;
+    *out = s.release();
+    return 0;
+}
+
+int secure_infer_gpu_session_destroy(si_session* s)
+{
+    if (!s) return -1;
+    (void)hipDeviceSynchronize();
+    delete s;
+    return 0;
+}
+
+int secure_infer_gpu_session_hash_subkey(const si_session* s, uint8_t out[16])
+{
+    if (!s || !out) return -1;
+    memcpy(out, s->ctx->h, 16);
+    return 0;
+}
+
+uint64_t secure_infer_codec_width(uint32_t bits, uint32_t heads, uint32_t head_dim)
+{
+    const uint64_t qb = 128ull * heads * head_dim * bits / 8;
+    const uint64_t sb = 2ull * heads * head_dim * 4;
+    return (qb + 2 * sb + 16 + 15) / 16 * 16;
+}
+
+uint64_t secure_infer_wire_stride(uint64_t bytes)
+{
+    return ((bytes + 31) & ~uint64_t(31)) + 96;
+}
+
+static int layer_common(const si_session* s, uint64_t bytes, uint32_t nrec, uint32_t n_k,
+                        uint64_t nslots, uint64_t wire_stride, const void* wire, const int64_t* slots,
+                        uint32_t codec, uint32_t heads, uint32_t dim, const void* staging,
+                        uint64_t slot_bytes)
+{
+    if (!s || !wire || !slots || nrec == 0 || n_k > nrec || bytes == 0) return -1;
+    if (nslots == 0) return -1;
+    if (bytes > s->max_record_bytes) return -1;
+    if (wire_stride < secure_infer_wire_stride(bytes) || (wire_stride & 15)) return -1;
+    if (!aligned16(wire)) return -1;
+    if (codec != SI_CODEC_NONE && codec != SI_CODEC_INT8 && codec != SI_CODEC_INT4) return -1;
+    if (codec != SI_CODEC_NONE) {
+        if (!staging || !aligned16(staging) || heads == 0 || dim == 0 || dim % 64) return -1;
+        if (bytes != secure_infer_codec_width(codec, heads, dim)) return -1;
+        if (slot_bytes < 128ull * heads * dim * 2) return -1;
+    } else if (slot_bytes < bytes) {
+        return -1;
+    }
+    return 0;
+}
+
+static void fill_layer_ivs(const si_session* s, si::RecBatch& b, const uint32_t* ivs, uint64_t ticket_base)
+{
+    b.ivs = ivs;
+    b.iv[0] = s->salt_word;
+    b.iv[3] = 2;
+    b.nonce_base = s->session_nonce + ticket_base;
+}
+
+int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_reload_desc* d)
+{
+    if (!d) return -1;
+    if (layer_common(s, d->bytes, d->nrec, d->n_k, d->nslots, d->wire_stride, d->wire, d->slots, d->codec_bits,
+                     d->heads, d->head_dim, d->staging, d->slot_bytes))
+        return -1;
+    if (!d->cache_k && d->n_k) return -1;
+    if (!d->cache_v && d->n_k < d->nrec) return -1;
+    if (!d->iv_words && d->ticket_base == 0) return -1;
+    std::lock_guard<std::mutex> g(g_lock);
+    si::RecAcc* acc = workspace(stream, d->nrec);
+    if (!acc) return -1;
+    si::RecBatch b{};
+    b.single = 0;
+    b.encrypt = 0;
+    b.wire = static_cast<const uint8_t*>(d->wire);
+    b.wire_stride = d->wire_stride;
+    b.tag_off = (d->bytes + 31) & ~uint64_t(31);
+    b.status_off = b.tag_off + 16;
+    b.aad_off = b.tag_off + 32;
+    b.cache[0] = static_cast<uint8_t*>(d->cache_k);
+    b.cache[1] = static_cast<uint8_t*>(d->cache_v);
+    b.slot_bytes = d->slot_bytes;
+    b.slots = d->slots;
+    b.nslots = int64_t(d->nslots);
+    b.n_k = d->n_k;
+    fill_layer_ivs(s, b, d->iv_words, d->ticket_base);
+    b.fail_count = d->fail_count;
+    const bool codec = d->codec_bits != SI_CODEC_NONE;
+    if (codec) {
+        b.staging = static_cast<uint8_t*>(d->staging);
+        b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
+    }
+    const si::Sched sc = make_sched(d->nrec, d->bytes, 64);
+    const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
+    if (si::launch_gcm(0, stream, s->ctx->dev, b, sc, acc, al) != hipSuccess) return -1;
+    if (codec) {
+        si::CodecBatch cb{};
+        cb.nrec = d->nrec;
+        cb.n_k = d->n_k;
+        cb.bits = d->codec_bits;
+        cb.heads = d->heads;
+        cb.dim = d->head_dim;
+        cb.layer = d->layer;
+        cb.cache[0] = static_cast<uint8_t*>(d->cache_k);
+        cb.cache[1] = static_cast<uint8_t*>(d->cache_v);
+        cb.slot_bytes = d->slot_bytes;
+        cb.slots = d->slots;
+        cb.nslots = int64_t(d->nslots);
+        cb.staging = static_cast<uint8_t*>(d->staging);
+        cb.staging_stride = b.staging_stride;
+        cb.qbytes = 128ull * d->heads * d->head_dim * d->codec_bits / 8;
+        cb.sbytes = 2ull * d->heads * d->head_dim * 4;
+        cb.width = d->bytes;
+        if (si::launch_dequant_scatter(stream, cb) != hipSuccess) return -1;
+    }
+    return 0;
+}
+
+int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si_writeback_desc* d)
+{
+    if (!d) return -1;
+    if (layer_common(s, d->bytes, d->nrec, d->n_k, d->nslots, d->wire_stride, d->wire, d->slots, d->codec_bits,
+                     d->heads, d->head_dim, d->staging, d->slot_bytes))
+        return -1;
+    if (!d->cache_k && d->n_k) return -1;
+    if (!d->cache_v && d->n_k < d->nrec) return -1;
+    if (!d->iv_words && d->ticket_base == 0) return -1;
+    std::lock_guard<std::mutex> g(g_lock);
+    si::RecAcc* acc = workspace(stream, d->nrec);
+    if (!acc) return -1;
+    const bool codec = d->codec_bits != SI_CODEC_NONE;
+    si::RecBatch b{};
+    b.single = 0;
+    b.encrypt = 1;
+    b.wire = static_cast<const uint8_t*>(d->wire);
+    b.wire_stride = d->wire_stride;
+    b.tag_off = (d->bytes + 31) & ~uint64_t(31);
+    b.status_off = b.tag_off + 16;
+    b.aad_off = b.tag_off + 32;
+    b.cache[0] = static_cast<uint8_t*>(const_cast<void*>(d->cache_k));
+    b.cache[1] = static_cast<uint8_t*>(const_cast<void*>(d->cache_v));
+    b.slot_bytes = d->slot_bytes;
+    b.slots = d->slots;
+    b.nslots = int64_t(d->nslots);
+    b.n_k = d->n_k;
+    b.fail_count = d->fail_count;
+    fill_layer_ivs(s, b, d->iv_words, d->ticket_base);
+    if (codec) {
+        b.staging = static_cast<uint8_t*>(d->staging);
+        b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
+        si::CodecBatch cb{};
+        cb.nrec = d->nrec;
+        cb.n_k = d->n_k;
+        cb.bits = d->codec_bits;
+        cb.heads = d->heads;
+        cb.dim = d->head_dim;
+        cb.layer = d->layer;
+        cb.cache[0] = b.cache[0];
+        cb.cache[1] = b.cache[1];
+        cb.slot_bytes = d->slot_bytes;
+        cb.slots = d->slots;
+        cb.nslots = int64_t(d->nslots);
+        cb.staging = b.staging;
+        cb.staging_stride = b.staging_stride;
+        cb.qbytes = 128ull * d->heads * d->head_dim * d->codec_bits / 8;
+        cb.sbytes = 2ull * d->heads * d->head_dim * 4;
+        cb.width = d->bytes;
+        if (si::launch_gather_quant(stream, cb) != hipSuccess) return -1;
+    }
+    const si::Sched sc = make_sched(d->nrec, d->bytes, 64);
+    const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
+    return si::launch_gcm(1, stream, s->ctx->dev, b, sc, acc, al) == hipSuccess ? 0 : -1;
+}
+
+// ---------------------------------------------------------------- kernel-level mirrors
+
+int secure_infer_gpu_gcm_decrypt_verify_aad_do(hipStream_t stream, void* ciphertext, void* key,
+                                               void* hash_subkey, void* expected_tag,
+                                               void* plaintext_output, void* status_output,
+                                               uint64_t bytes, uint32_t iv0, uint32_t iv1,
+                                               uint32_t iv2, uint32_t iv3, void* aad,
+                                               uint64_t aad_bytes)
+{
+    if (!ciphertext || !key || !hash_subkey || !expected_tag || !plaintext_output || !status_output ||
+        bytes == 0 || (aad_bytes != 0 && !aad))
+        return -1;
+    const uint32_t iv[4] = {iv0, iv1, iv2, iv3};
+    return run_single(0, stream, ciphertext, key, hash_subkey, expected_tag, plaintext_output,
+                      status_output, nullptr, bytes, iv, aad, aad_bytes);
+}
+
+int secure_infer_gpu_gcm_decrypt_verify_do(hipStream_t stream, void* ciphertext, void* key,
+                                           void* hash_subkey, void* expected_tag,
+                                           void* plaintext_output, void* status_output,
+                                           uint64_t bytes, uint32_t iv0, uint32_t iv1,
+                                           uint32_t iv2, uint32_t iv3)
+{
+    return secure_infer_gpu_gcm_decrypt_verify_aad_do(stream, ciphertext, key, hash_subkey,
+                                                      expected_tag, plaintext_output,
+                                                      status_output, bytes, iv0, iv1, iv2, iv3,
+                                                      nullptr, 0);
+}
+
+int secure_infer_gpu_gcm_encrypt_tag_do(hipStream_t stream, void* plaintext, void* key,
+                                        void* hash_subkey, void* ciphertext_output,
+                                        void* tag_output, uint64_t bytes, uint32_t iv0,
+                                        uint32_t iv1, uint32_t iv2, uint32_t iv3, void* aad,
+                                        uint64_t aad_bytes)
+{
+    if (!plaintext || !key || !hash_subkey || !ciphertext_output || !tag_output || bytes == 0 ||
+        (aad_bytes != 0 && !aad))
+        return -1;
+    const uint32_t iv[4] = {iv0, iv1, iv2, iv3};
+    return run_single(1, stream, plaintext, key, hash_subkey, tag_output, ciphertext_output,
+                      nullptr, nullptr, bytes, iv, aad, aad_bytes);
+}
+
+int secure_infer_gpu_gcm_verify_only_aad_do(hipStream_t stream, void* ciphertext, void* key,
+                                            void* hash_subkey, void* expected_tag,
+                                            void* status_output, uint64_t bytes, uint32_t iv0,
+                                            uint32_t iv1, uint32_t iv2, uint32_t iv3, void* aad,
+                                            uint64_t aad_bytes)
+{
+    if (!ciphertext || !key || !hash_subkey || !expected_tag || !status_output || bytes == 0 ||
+        (aad_bytes != 0 && !aad))
+        return -1;
+    const uint32_t iv[4] = {iv0, iv1, iv2, iv3};
+    return run_single(2, stream, ciphertext, key, hash_subkey, expected_tag, nullptr,
+                      status_output, nullptr, bytes, iv, aad, aad_bytes);
+}
+
+int secure_infer_gpu_gcm_verify_xor_aad_do(hipStream_t stream, void* ciphertext, void* key,
+                                           void* hash_subkey, void* expected_tag, void* keystream,
+                                           void* plaintext_output, void* status_output,
+                                           uint64_t bytes, uint32_t iv0, uint32_t iv1,
+                                           uint32_t iv2, uint32_t iv3, void* aad,
+                                           uint64_t aad_bytes)
+{
+    if (!ciphertext || !key || !hash_subkey || !expected_tag || !keystream || !plaintext_output ||
+        !status_output || bytes == 0 || (aad_bytes != 0 && !aad))
+        return -1;
+    const uint32_t iv[4] = {iv0, iv1, iv2, iv3};
+    return run_single(3, stream, ciphertext, key, hash_subkey, expected_tag, plaintext_output,
+                      status_output, keystream, bytes, iv, aad, aad_bytes);
+}
+
+static int run_ctr(hipStream_t stream, const void* in, void* key, void* out, uint64_t bytes,
+                   const uint32_t iv[4])
+{
+    std::lock_guard<std::mutex> g(g_lock);
+    DevCtx* c = ctx_for_device_key(stream, key, nullptr, 1);
+    if (!c) return -1;
+    return si::launch_ctr(stream, c->dev, static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out),
+                          bytes, iv) == hipSuccess ? 0 : -1;
+}
+
+int secure_infer_gpu_aes_ctr_do(hipStream_t stream, void* input, void* key, void* output,
+                                uint64_t bytes, uint32_t iv0, uint32_t iv1, uint32_t iv2,
+                                uint32_t iv3)
+{
+    if (!input || !key || !output || bytes == 0) return -1;
+    const uint32_t iv[4] = {iv0, iv1, iv2, iv3};
+    return run_ctr(stream, input, key, output, bytes, iv);
+}
+
+int secure_infer_gpu_keystream_do(hipStream_t stream, void* key, void* output, uint64_t bytes,
+                                  uint32_t iv0, uint32_t iv1, uint32_t iv2, uint32_t iv3)
+{
+    if (!key || !output || bytes == 0) return -1;
+    const uint32_t iv[4] = {iv0, iv1, iv2, iv3};
+    return run_ctr(stream, nullptr, key, output, bytes, iv);
+}
+
+int secure_infer_gpu_auth_gate_do(hipStream_t stream, void* data, void* status, uint64_t bytes)
+{
+    if (!data || !status) return -1;
+    return si::launch_auth_gate(stream, static_cast<uint8_t*>(data),
+                                static_cast<const uint32_t*>(status), bytes) == hipSuccess ? 0 : -1;
+}
+
+// ---------------------------------------------------------------- control plane
+
+uint64_t secure_infer_new_transfer_ticket(void)
+{
+    const uint64_t t = g_next_ticket.fetch_add(1, std::memory_order_relaxed);
+    if (t == 0) {
+        fprintf(stderr, "[secure_infer] transfer ticket space exhausted\n");
+        abort();
+    }
+    return t;
+}
+
+int secure_infer_derive_transfer_iv(const uint8_t base_iv[16], uint64_t session_nonce,
+                                    uint64_t ticket, uint64_t block_offset, uint8_t out_iv[16])
+{
+    if (!base_iv || !out_iv || ticket == 0 || block_offset > UINT32_MAX - 2u) return -1;
+    memcpy(out_iv, base_iv, 16);
+    put_be64(out_iv + 4, session_nonce + ticket);
+    put_be32(out_iv + 12, uint32_t(block_offset + 2));
+    return 0;
+}
+
+void secure_infer_register_host_range_ex(const void* base, size_t bytes, uint32_t layer_id,
+                                         uint32_t tensor_kind, size_t block_bytes)
+{
+    if (!base || bytes == 0) return;
+    std::lock_guard<std::mutex> g(g_ranges_lock);
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+    g_ranges.push_back(HostRange{b, b + bytes, layer_id, tensor_kind, block_bytes});
+}
+
+void secure_infer_clear_host_ranges(void)
+{
+    std::lock_guard<std::mutex> g(g_ranges_lock);
+    g_ranges.clear();
+}
+
+int secure_infer_build_gcm_aad(const void* host_ptr, size_t bytes, uint8_t direction,
+                               uint64_t transfer_ticket, uint64_t transfer_offset,
+                               uint64_t session_nonce, uint8_t out[64])
+{
+    if (!out || !host_ptr || bytes == 0 || transfer_ticket == 0 || (direction != 1 && direction != 2))
+        return 0;
+    const uintptr_t begin = reinterpret_cast<uintptr_t>(host_ptr);
+    uint32_t layer = UINT32_MAX, kind = UINT32_MAX;
+    uint64_t block_id = begin, offset = 0;
+    {
+        std::lock_guard<std::mutex> g(g_ranges_lock);
+        for (const HostRange& r : g_ranges) {
+            if (begin < r.begin || begin + bytes > r.end) continue;
+            const uint64_t rel = begin - r.begin;
+            const uint64_t stride = r.block_bytes ? r.block_bytes : 1;
+            layer = r.layer;
+            kind = r.kind;
+            block_id = rel / stride;
+            offset = rel % stride;
+            break;
+        }
+    }
+    memset(out, 0, 64);
+    out[0] = 'S'; out[1] = 'F'; out[2] = 'A'; out[3] = 'D';
+    out[4] = 1;
+    out[5] = direction;
+    out[6] = uint8_t(kind & 0xff);
+    put_be32(out + 8, layer);
+    put_be64(out + 12, block_id);
+    put_be64(out + 20, offset);
+    put_be64(out + 28, bytes);
+    put_be64(out + 36, transfer_ticket);
+    put_be64(out + 44, transfer_offset);
+    put_be64(out + 52, session_nonce);
+    return 1;
+}
+
+int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket)
+{
+    if (transfer_ticket == 0) return 1;
+    std::lock_guard<std::mutex> g(g_replay_lock);
+    return g_replay.insert(transfer_ticket).second ? 1 : 0;
+}
+
+int secure_infer_h2d_layer_group_begin(size_t expected)
+{
+    if (t_group_expected >= 0) return -1;
+    t_group_expected = int64_t(expected);
+    return 0;
+}
+
+int secure_infer_h2d_layer_group_end(void)
+{
+    if (t_group_expected < 0) return -1;
+    t_group_expected = -1;
+    return 0;
+}
+
+int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event, const uint32_t* fail_count)
+{
+    if (!event || !fail_count) return -1;
+    std::lock_guard<std::mutex> g(g_track_lock);
+    g_tracked.emplace(layer, TrackedLayer{event, fail_count});
+    return 0;
+}
+
+int secure_infer_recovery_wait_layer_authentication(uint32_t layer)
+{
+    std::vector<TrackedLayer> recs;
+    {
+        std::lock_guard<std::mutex> g(g_track_lock);
+        auto range = g_tracked.equal_range(layer);
+        for (auto it = range.first; it != range.second; ++it) recs.push_back(it->second);
+        g_tracked.erase(range.first, range.second);
+    }
+    int rc = 0;
+    for (const TrackedLayer& t : recs) {
+        if (hipEventSynchronize(t.event) != hipSuccess) return -1;
+        uint32_t fails = 1;
+        if (hipMemcpy(&fails, t.fail_count, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+        if (fails != 0) rc = -1;
+    }
+    return rc;
+}
+
+int secure_infer_gpu_set_chunk_rows(int jmax)
+{
+    if (jmax < 1 || jmax > 256) return -1;
+    g_jmax = jmax;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,245 @@
+// Device primitives for AES-128-GCM on gfx950 (CDNA4).
+//
+// Data layout conventions used by every kernel:
+//   * AES state and round keys are four little-endian column words, i.e. the
+//     16-byte block loaded from memory as four dwords.  Column j's byte r is
+//     state row r.  Te0[x] = {2s, s, s, 3s} (s = S(x)) packs MixColumns' first
+//     column; Te1 = rotl8(Te0); the other two are rotl16 of these.
+//   * GF(2^128) elements for GHASH are kept in memory byte order (four LE
+//     dwords) wherever only XORs and table lookups touch them; the generic
+//     multiply converts to big-endian words (bit 0 = MSB of byte 0 = x^0).
+//
+// LDS tables (per workgroup):
+//   AES  : entry e, table t in {Te0, Te1}, copy c in [0, 32): 32-bit word at
+//          byte address e*256 + t*128 + c*4.  Lane l reads copy (l & 31), so a
+//          wave64 lookup touches each of the 32 banks once per half-wave.  The
+//          address is produced by ONE v_perm_b32: byte1 <- state byte, byte0 <-
+//          the lane's copy offset.
+//   GHASH: 4-bit per-position tables of H^T (T = threads per workgroup):
+//          position p (nibble p of the block, p = 0..31), value v: 16 bytes at
+//          p*256 + v*16.  Y*H^T = XOR_p table[p][nibble_p(Y)].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SI_T 256  // threads per workgroup of the GCM kernels
+
+namespace si {
+
+// Per-key context in device memory, built on the host.
+struct GcmCtx {
+    uint32_t rk[44];      // AES-128 round keys, LE column words
+    uint32_t rk16[44];    // rotl16(rk)
+    uint32_t te0[256];    // Te0
+    uint32_t h[4];        // H, memory byte order
+    uint32_t npow;        // entries of the power table that follows
+    uint32_t reserved[3];
+    uint4 gh4[32 * 16];   // 4-bit tables of H^SI_T
+    // followed by uint4 hpow[npow]: hpow[e] = H^e in memory byte order
+};
+
+// One record's cross-workgroup GHASH accumulator; zero between launches
+// (the finalising workgroup resets it).
+struct RecAcc {
+    uint32_t w[4];
+    uint32_t count;
+    uint32_t reserved[3];
+};
+
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c)
+{
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
+__device__ __forceinline__ uint32_t rotl16(uint32_t x)
+{
+    return __builtin_amdgcn_alignbit(x, x, 16);
+}
+
+__device__ __forceinline__ uint32_t bswap32(uint32_t x)
+{
+    return __builtin_amdgcn_perm(x, x, 0x00010203u);
+}
+
+// ---------------------------------------------------------------- AES
+
+// Lane-specific byte offsets of the lane's copy of Te0 / Te1.
+struct AesLane {
+    uint32_t b0, b1;
+};
+
+__device__ __forceinline__ AesLane aes_lane(uint32_t lane)
+{
+    AesLane l;
+    l.b0 = (lane & 31u) * 4u;
+    l.b1 = 128u + (lane & 31u) * 4u;
+    return l;
+}
+
+// Table word for byte k of state word w: one v_perm_b32 builds the address.
+template <int K>
+__device__ __forceinline__ uint32_t te(const uint32_t* lds, uint32_t w, uint32_t base)
+{
+    constexpr uint32_t sel = 0x0c0c0000u | ((4u + K) << 8);
+    const uint32_t addr = __builtin_amdgcn_perm(w, base, sel);
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + addr);
+}
+
+// Fills the AES region (64 KiB) from Te0; all threads of the block take part.
+__device__ __forceinline__ void aes_fill_lds(uint32_t* lds, const uint32_t* __restrict__ te0,
+                                             uint32_t tid, uint32_t nthreads)
+{
+    // 4096 uint4 slots: slot s -> entry s/16, 16-byte column s%16 (columns 0..7
+    // hold Te0 copies, 8..15 hold Te1 copies).  Consecutive threads write
+    // consecutive columns, so the stores are bank-conflict free.
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    for (uint32_t s = tid; s < 4096u; s += nthreads) {
+        const uint32_t e = s >> 4;
+        uint32_t v = te0[e];
+        if (s & 8u) v = __builtin_amdgcn_alignbit(v, v, 24);  // rotl8
+        dst[s] = make_uint4(v, v, v, v);
+    }
+}
+
+// E_K(counter block) with the three nonce words already XORed with rk[0..2].
+__device__ __forceinline__ void aes_ctr_block(const uint32_t* lds, AesLane l,
+                                              const GcmCtx* __restrict__ ctx, uint32_t n0,
+                                              uint32_t n1, uint32_t n2, uint32_t ctr,
+                                              uint32_t out[4])
+{
+    uint32_t s0 = n0, s1 = n1, s2 = n2, s3 = bswap32(ctr) ^ ctx->rk[3];
+#pragma unroll
+    for (int r = 1; r <= 9; ++r) {
+        const uint32_t t0 = xor3(te<0>(lds, s0, l.b0), te<1>(lds, s1, l.b1),
+                                 rotl16(xor3(te<2>(lds, s2, l.b0), te<3>(lds, s3, l.b1),
+                                             ctx->rk16[4 * r + 0])));
+        const uint32_t t1 = xor3(te<0>(lds, s1, l.b0), te<1>(lds, s2, l.b1),
+                                 rotl16(xor3(te<2>(lds, s3, l.b0), te<3>(lds, s0, l.b1),
+                                             ctx->rk16[4 * r + 1])));
+        const uint32_t t2 = xor3(te<0>(lds, s2, l.b0), te<1>(lds, s3, l.b1),
+                                 rotl16(xor3(te<2>(lds, s0, l.b0), te<3>(lds, s1, l.b1),
+                                             ctx->rk16[4 * r + 2])));
+        const uint32_t t3 = xor3(te<0>(lds, s3, l.b0), te<1>(lds, s0, l.b1),
+                                 rotl16(xor3(te<2>(lds, s1, l.b0), te<3>(lds, s2, l.b1),
+                                             ctx->rk16[4 * r + 3])));
+        s0 = t0; s1 = t1; s2 = t2; s3 = t3;
+    }
+    // Last round: S-box bytes sit in byte 1 of Te0 and byte 2 of Te1.
+    // (lo | hi) ^ rk : bitop3 truth table 0x56.
+#define SI_LAST(J, A, B, C, D)                                                            \
+    out[J] = __builtin_amdgcn_bitop3_b32(                                                  \
+        __builtin_amdgcn_perm(te<0>(lds, A, l.b0), te<1>(lds, B, l.b1), 0x0c0c0205u),     \
+        __builtin_amdgcn_perm(te<2>(lds, C, l.b0), te<3>(lds, D, l.b1), 0x02050c0cu),     \
+        ctx->rk[40 + J], 0x56)
+    SI_LAST(0, s0, s1, s2, s3);
+    SI_LAST(1, s1, s2, s3, s0);
+    SI_LAST(2, s2, s3, s0, s1);
+    SI_LAST(3, s3, s0, s1, s2);
+#undef SI_LAST
+}
+
+// ---------------------------------------------------------------- GHASH
+
+// y <- y * H^T with the 4-bit per-position tables in LDS.
+__device__ __forceinline__ void gh_mul_table(const uint4* gh, uint32_t y[4])
+{
+    uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+    const char* base = reinterpret_cast<const char*>(gh);
+#pragma unroll
+    for (int p = 0; p < 32; p += 2) {
+        const uint32_t w = y[p >> 3];
+        const int q = p & 7;
+        // nibble q of w sits at bits [4q, 4q+4); its table offset is nibble*16.
+        const uint32_t o0 = q == 0 ? ((w << 4) & 0xf0u) : ((w >> (4 * q - 4)) & 0xf0u);
+        const uint32_t o1 = (w >> (4 * q)) & 0xf0u;
+        const uint4 v0 = *reinterpret_cast<const uint4*>(base + p * 256 + o0);
+        const uint4 v1 = *reinterpret_cast<const uint4*>(base + (p + 1) * 256 + o1);
+        a0 = xor3(a0, v0.x, v1.x);
+        a1 = xor3(a1, v0.y, v1.y);
+        a2 = xor3(a2, v0.z, v1.z);
+        a3 = xor3(a3, v0.w, v1.w);
+    }
+    y[0] = a0; y[1] = a1; y[2] = a2; y[3] = a3;
+}
+
+// Big-endian-word GF(2^128) helpers (bit 0 = MSB of word 0 = x^0).
+__device__ __forceinline__ void be_mulx(uint32_t a[4])
+{
+    const uint32_t carry = a[3] & 1u;
+    a[3] = __builtin_amdgcn_alignbit(a[2], a[3], 1);
+    a[2] = __builtin_amdgcn_alignbit(a[1], a[2], 1);
+    a[1] = __builtin_amdgcn_alignbit(a[0], a[1], 1);
+    a[0] = (a[0] >> 1) ^ ((0u - carry) & 0xe1000000u);
+}
+
+// z = x * y for per-lane x, y (memory byte order in and out).  Shoup's 4-bit
+// method with the lane's 16-entry table of multiples of y in LDS:
+// tbl + (v * stride + lane_slot) * 16 bytes, v = 0..15.
+__device__ __forceinline__ void gh_mul_generic(const uint32_t x_mem[4], const uint32_t y_mem[4],
+                                               uint4* tbl, uint32_t slot, uint32_t stride,
+                                               uint32_t z_mem[4])
+{
+    uint32_t m8[4] = {bswap32(y_mem[0]), bswap32(y_mem[1]), bswap32(y_mem[2]), bswap32(y_mem[3])};
+    uint32_t m4[4] = {m8[0], m8[1], m8[2], m8[3]};
+    be_mulx(m4);
+    uint32_t m2[4] = {m4[0], m4[1], m4[2], m4[3]};
+    be_mulx(m2);
+    uint32_t m1[4] = {m2[0], m2[1], m2[2], m2[3]};
+    be_mulx(m1);
+#pragma unroll
+    for (uint32_t v = 0; v < 16; ++v) {
+        uint32_t e[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t t = 0;
+            if (v & 8u) t ^= m8[k];
+            if (v & 4u) t ^= m4[k];
+            if (v & 2u) t ^= m2[k];
+            if (v & 1u) t ^= m1[k];
+            e[k] = t;
+        }
+        tbl[v * stride + slot] = make_uint4(e[0], e[1], e[2], e[3]);
+    }
+    const uint32_t xb[4] = {bswap32(x_mem[0]), bswap32(x_mem[1]), bswap32(x_mem[2]),
+                            bswap32(x_mem[3])};
+    // Horner over the nibbles of x from the last (x^124..x^127) to the first.
+    uint32_t a[4];
+    {
+        const uint4 t = tbl[(xb[3] & 0xfu) * stride + slot];
+        a[0] = t.x; a[1] = t.y; a[2] = t.z; a[3] = t.w;
+    }
+#pragma unroll
+    for (int j = 30; j >= 0; --j) {
+        const uint32_t nib = (xb[j >> 3] >> (28 - 4 * (j & 7))) & 0xfu;
+        // a <- a * x^4: shift right by 4 and fold the 4 bits that left x^127
+        // back in: x^(128+i) = x^i (x^7 + x^2 + x + 1), i.e. the 16-bit
+        // reduction value clmul(rem, 0x1c20) placed in the top half-word.
+        const uint32_t rem = a[3] & 0xfu;
+        a[3] = __builtin_amdgcn_alignbit(a[2], a[3], 4);
+        a[2] = __builtin_amdgcn_alignbit(a[1], a[2], 4);
+        a[1] = __builtin_amdgcn_alignbit(a[0], a[1], 4);
+        const uint32_t red = (rem << 21) ^ xor3(rem << 26, rem << 27, rem << 28);
+        const uint4 t = tbl[nib * stride + slot];
+        a[0] = xor3(a[0] >> 4, red, t.x);
+        a[1] ^= t.y;
+        a[2] ^= t.z;
+        a[3] ^= t.w;
+    }
+    z_mem[0] = bswap32(a[0]);
+    z_mem[1] = bswap32(a[1]);
+    z_mem[2] = bswap32(a[2]);
+    z_mem[3] = bswap32(a[3]);
+}
+
+// XOR-reduce four words across a wave64.
+__device__ __forceinline__ void wave_xor4(uint32_t v[4])
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] ^= __shfl_xor(v[k], off, 64);
+    }
+}
+
+}  // namespace si

@@ -1,0 +1,74 @@
+// Host-visible launch interface of the HIP kernels (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace si {
+
+struct GcmCtx;
+struct RecAcc;
+
+// A batch of records.  single != 0: one record with explicit pointers
+// (src/dst/aad/tag/status/ks/iv).  Otherwise records r = 0..nrec-1 live in a
+// wire buffer (stride wire_stride) and map to paged-cache slots.
+struct RecBatch {
+    int single;
+    int encrypt;  // layer form: 1 = writeback (cache -> wire), 0 = reload
+    // single-record form
+    const uint8_t* src;
+    uint8_t* dst;
+    const uint8_t* aad;
+    uint8_t* tag;
+    uint32_t* status;
+    const uint8_t* ks;
+    uint32_t iv[4];  // single: full IV; layer: iv[0] = salt word, iv[3] = counter start
+    // layer form
+    const uint8_t* wire;
+    uint64_t wire_stride;
+    uint64_t tag_off, status_off, aad_off;
+    uint8_t* cache[2];
+    uint64_t slot_bytes;
+    const int64_t* slots;
+    int64_t nslots;        // slot ids outside [0, nslots) fail the record, nothing is touched
+    uint32_t n_k;
+    const uint32_t* ivs;   // 4 words per record, or null: derive from nonce_base + r
+    uint64_t nonce_base;   // session_nonce + ticket of record 0
+    uint8_t* staging;      // codec: plaintext packets go here instead of the cache
+    uint64_t staging_stride;
+    uint32_t* fail_count;
+};
+
+// Work decomposition shared by all records of a batch (uniform sizes).
+struct Sched {
+    uint32_t nrec;       // records
+    uint32_t nc;         // chunks per record
+    uint32_t j;          // rows per chunk (blocks per thread)
+    uint32_t a;          // AAD blocks
+    uint32_t n;          // payload blocks
+    uint32_t aad_bytes;
+    uint64_t bytes;      // payload bytes
+};
+
+hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
+                      const Sched& s, RecAcc* acc, bool aligned);
+hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, uint8_t* out,
+                      uint64_t bytes, const uint32_t iv[4]);
+hipError_t launch_auth_gate(hipStream_t stream, uint8_t* data, const uint32_t* status,
+                            uint64_t bytes);
+
+// Codec kernels (si_codec.hip).
+struct CodecBatch {
+    uint32_t nrec, n_k, bits, heads, dim, layer;
+    uint8_t* cache[2];
+    uint64_t slot_bytes;
+    const int64_t* slots;
+    int64_t nslots;
+    uint8_t* staging;       // packets, one per record
+    uint64_t staging_stride;
+    uint64_t qbytes, sbytes, width;
+};
+hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b);
+hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b);
+
+}  // namespace si

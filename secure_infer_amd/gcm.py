@@ -1,0 +1,356 @@
+"""Python face of libsecure_infer.so on PyTorch-ROCm tensors.
+
+* Kernel-level calls mirror the reference's device launchers
+  (secure_infer/native/kernels/aicpu/launcher.asc) one record at a time.
+* ``GcmSession`` owns a device-resident AES-128 key with its GHASH tables and
+  runs the fused per-layer reload / writeback kernels.
+* ``NativeTransfer`` mirrors ``native_layerwise.NativeTransfer`` (per-layer
+  authenticated reload into the paged cache, native_layerwise.py:85-130) and
+  the per-layer authentication wait the reuse schedulers block on
+  (``secure_infer_recovery_wait_layer_authentication``, secure_infer.cpp:7303).
+
+All tensors handed to the library are CUDA (HIP) tensors; every call is
+asynchronous on the given (default: current) stream.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import struct
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+AAD_BYTES = 64
+SI_CODEC_NONE, SI_CODEC_INT8, SI_CODEC_INT4 = 0, 8, 4
+
+
+def lib():
+    return _lib.load()
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else ct.c_void_p(t.data_ptr())
+
+
+def _stream(stream) -> ct.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ct.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed (rc={rc})")
+
+
+def _dev(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ------------------------------------------------------------------ wire layout
+
+def wire_tag_offset(nbytes: int) -> int:
+    """Ciphertext area of a wire record is padded to 32 B (secure_infer.cpp:6319-6320)."""
+    return (nbytes + 31) & ~31
+
+
+def wire_stride(nbytes: int) -> int:
+    """[ct pad32][tag 16][status 16][AAD 64] (secure_infer.cpp:6379-6388)."""
+    return int(lib().secure_infer_wire_stride(nbytes))
+
+
+def codec_width(bits: int, heads: int, head_dim: int) -> int:
+    return int(lib().secure_infer_codec_width(bits, heads, head_dim))
+
+
+# ------------------------------------------------------------------ control plane
+
+def new_transfer_ticket() -> int:
+    return int(lib().secure_infer_new_transfer_ticket())
+
+
+def derive_transfer_iv(base_iv: bytes, ticket: int, block_offset: int = 0,
+                       session_nonce: int = 0) -> bytes:
+    out = (ct.c_uint8 * 16)()
+    base = (ct.c_uint8 * 16).from_buffer_copy(bytes(base_iv).ljust(16, b"\0"))
+    _check(lib().secure_infer_derive_transfer_iv(base, session_nonce, ticket, block_offset, out),
+           "derive_transfer_iv")
+    return bytes(out)
+
+
+def iv_words(iv: bytes) -> tuple[int, int, int, int]:
+    """pack_inline_iv: four big-endian words (secure_infer.cpp:2083-2093)."""
+    return struct.unpack(">IIII", bytes(iv[:16]))
+
+
+def register_host_range(tensor: torch.Tensor, layer_id: int, tensor_kind: int) -> None:
+    """_register_host_range (npu_predict.py:384-408)."""
+    block_bytes = tensor[0].numel() * tensor.element_size() if tensor.ndim and tensor.shape[0] else 0
+    lib().secure_infer_register_host_range_ex(ct.c_void_p(tensor.data_ptr()),
+                                              tensor.numel() * tensor.element_size(),
+                                              layer_id, tensor_kind, block_bytes)
+
+
+def clear_host_ranges() -> None:
+    lib().secure_infer_clear_host_ranges()
+
+
+def build_gcm_aad(host_ptr: int, nbytes: int, direction: int, ticket: int,
+                  transfer_offset: int = 0, session_nonce: int = 0) -> bytes:
+    out = (ct.c_uint8 * 64)()
+    ok = lib().secure_infer_build_gcm_aad(ct.c_void_p(host_ptr), nbytes, direction, ticket,
+                                          transfer_offset, session_nonce, out)
+    if ok != 1:
+        raise ValueError("invalid AAD request")
+    return bytes(out)
+
+
+def replay_reserve(ticket: int) -> bool:
+    return lib().secure_infer_gcm_replay_reserve(ticket) == 1
+
+
+# ------------------------------------------------------------------ kernel-level mirrors
+
+def gcm_decrypt_verify(ciphertext, key, hash_subkey, expected_tag, plaintext_out, status_out,
+                       iv, aad=None, nbytes=None, stream=None) -> None:
+    """secure_infer_aicpu_gcm_decrypt_verify[_aad]_do (launcher.asc:214-275)."""
+    n = ciphertext.numel() if nbytes is None else nbytes
+    a = 0 if aad is None else aad.numel()
+    _check(lib().secure_infer_gpu_gcm_decrypt_verify_aad_do(
+        _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
+        _p(plaintext_out), _p(status_out), n, *iv, _p(aad), a), "gcm_decrypt_verify")
+
+
+def gcm_encrypt_tag(plaintext, key, hash_subkey, ciphertext_out, tag_out, iv, aad=None,
+                    nbytes=None, stream=None) -> None:
+    """secure_infer_aicpu_gcm_encrypt_tag_do (launcher.asc:279-308)."""
+    n = plaintext.numel() if nbytes is None else nbytes
+    a = 0 if aad is None else aad.numel()
+    _check(lib().secure_infer_gpu_gcm_encrypt_tag_do(
+        _stream(stream), _p(plaintext), _p(key), _p(hash_subkey), _p(ciphertext_out), _p(tag_out),
+        n, *iv, _p(aad), a), "gcm_encrypt_tag")
+
+
+def gcm_verify_only(ciphertext, key, hash_subkey, expected_tag, status_out, iv, aad=None,
+                    stream=None) -> None:
+    """secure_infer_aicpu_gcm_verify_only_aad_do (launcher.asc:407-435)."""
+    a = 0 if aad is None else aad.numel()
+    _check(lib().secure_infer_gpu_gcm_verify_only_aad_do(
+        _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
+        _p(status_out), ciphertext.numel(), *iv, _p(aad), a), "gcm_verify_only")
+
+
+def gcm_verify_xor(ciphertext, key, hash_subkey, expected_tag, keystream, plaintext_out,
+                   status_out, iv, aad=None, stream=None) -> None:
+    """secure_infer_aicpu_gcm_verify_xor_aad_do (launcher.asc:343-376)."""
+    a = 0 if aad is None else aad.numel()
+    _check(lib().secure_infer_gpu_gcm_verify_xor_aad_do(
+        _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
+        _p(keystream), _p(plaintext_out), _p(status_out), ciphertext.numel(), *iv, _p(aad), a),
+        "gcm_verify_xor")
+
+
+def aes_ctr(inp, key, out, iv, stream=None) -> None:
+    """secure_infer_aicpu_aes_ctr_do (launcher.asc:134-155)."""
+    _check(lib().secure_infer_gpu_aes_ctr_do(_stream(stream), _p(inp), _p(key), _p(out),
+                                             inp.numel(), *iv), "aes_ctr")
+
+
+def keystream(key, out, iv, stream=None) -> None:
+    """secure_infer_aicpu_keystream_do (launcher.asc:160-179)."""
+    _check(lib().secure_infer_gpu_keystream_do(_stream(stream), _p(key), _p(out), out.numel(), *iv),
+           "keystream")
+
+
+def auth_gate(data, status, stream=None) -> None:
+    """secure_infer_aicpu_auth_gate_do (launcher.asc:116-132)."""
+    _check(lib().secure_infer_gpu_auth_gate_do(_stream(stream), _p(data), _p(status),
+                                               data.numel() * data.element_size()), "auth_gate")
+
+
+# ------------------------------------------------------------------ sessions
+
+@dataclass
+class LayerShape:
+    """Geometry of one layer's records: `nblocks` 128-token blocks per kind."""
+    heads: int
+    head_dim: int
+    codec_bits: int = SI_CODEC_NONE
+
+    @property
+    def block_bytes(self) -> int:
+        return 128 * self.heads * self.head_dim * 2
+
+    @property
+    def record_bytes(self) -> int:
+        if self.codec_bits == SI_CODEC_NONE:
+            return self.block_bytes
+        return codec_width(self.codec_bits, self.heads, self.head_dim)
+
+
+class GcmSession:
+    """One AES-128-GCM session: key and GHASH tables resident on the device.
+
+    IV of the record with ticket t: salt[4] || BE64(session_nonce + t) || BE32(2)
+    (secure_infer_derive_transfer_iv, secure_infer.cpp:274-300).
+    """
+
+    def __init__(self, key: bytes, iv_salt: bytes, session_nonce: int = 0,
+                 max_record_bytes: int = 1 << 20):
+        if len(key) < 16 or len(iv_salt) < 4:
+            raise ValueError("key needs 16 bytes and iv_salt 4 bytes")
+        self.key = bytes(key[:16])
+        self.iv_salt = bytes(iv_salt[:4])
+        self.session_nonce = int(session_nonce)
+        self.max_record_bytes = int(max_record_bytes)
+        h = ct.c_void_p()
+        kb = (ct.c_uint8 * 16).from_buffer_copy(self.key)
+        sb = (ct.c_uint8 * 4).from_buffer_copy(self.iv_salt)
+        _check(lib().secure_infer_gpu_session_create(kb, sb, self.session_nonce,
+                                                     self.max_record_bytes, ct.byref(h)),
+               "session_create")
+        self._h = h
+        out = (ct.c_uint8 * 16)()
+        _check(lib().secure_infer_gpu_session_hash_subkey(self._h, out), "hash_subkey")
+        self.hash_subkey = bytes(out)
+
+    def close(self) -> None:
+        if self._h:
+            lib().secure_infer_gpu_session_destroy(self._h)
+            self._h = ct.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def base_iv(self) -> bytes:
+        return self.iv_salt + bytes(12)
+
+    def record_iv(self, ticket: int) -> tuple[int, int, int, int]:
+        return iv_words(derive_transfer_iv(self.base_iv(), ticket, 0, self.session_nonce))
+
+    def reload_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
+                     cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
+                     ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
+                     codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
+                     layer: int = 0, staging: torch.Tensor | None = None,
+                     fail_count: torch.Tensor | None = None, stream=None) -> None:
+        for t, name in ((wire, "wire"), (cache_k, "cache_k"), (cache_v, "cache_v"),
+                        (slots, "slots")):
+            _dev(t, name)
+        if slots.dtype != torch.int64 or slots.numel() < nrec:
+            raise ValueError("slots must be int64 with one entry per record")
+        stride = wire_stride(nbytes)
+        if wire.numel() * wire.element_size() < nrec * stride:
+            raise ValueError("wire buffer too small")
+        if codec_bits and (staging is None or staging.numel() * staging.element_size()
+                           < nrec * wire_tag_offset(nbytes)):
+            raise ValueError("codec reload needs a staging buffer of nrec*align32(bytes)")
+        d = _lib.SiReloadDesc(
+            wire=wire.data_ptr(), wire_stride=stride, bytes=nbytes, nrec=nrec, n_k=n_k,
+            iv_words=None if iv_words_dev is None else iv_words_dev.data_ptr(),
+            ticket_base=ticket_base, cache_k=cache_k.data_ptr(), cache_v=cache_v.data_ptr(),
+            slot_bytes=cache_k[0].numel() * cache_k.element_size(),
+            nslots=min(cache_k.shape[0], cache_v.shape[0]), slots=slots.data_ptr(),
+            codec_bits=codec_bits, heads=heads, head_dim=head_dim, layer=layer,
+            staging=None if staging is None else staging.data_ptr(),
+            fail_count=None if fail_count is None else fail_count.data_ptr())
+        _check(lib().secure_infer_gpu_reload_layer(_stream(stream), self._h, ct.byref(d)),
+               "reload_layer")
+
+    def writeback_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
+                        cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
+                        ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
+                        codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
+                        layer: int = 0, staging: torch.Tensor | None = None,
+                        fail_count: torch.Tensor | None = None, stream=None) -> None:
+        for t, name in ((wire, "wire"), (cache_k, "cache_k"), (cache_v, "cache_v"),
+                        (slots, "slots")):
+            _dev(t, name)
+        stride = wire_stride(nbytes)
+        if wire.numel() * wire.element_size() < nrec * stride:
+            raise ValueError("wire buffer too small")
+        if codec_bits and staging is None:
+            raise ValueError("codec writeback needs a staging buffer")
+        d = _lib.SiWritebackDesc(
+            wire=wire.data_ptr(), wire_stride=stride, bytes=nbytes, nrec=nrec, n_k=n_k,
+            iv_words=None if iv_words_dev is None else iv_words_dev.data_ptr(),
+            ticket_base=ticket_base, cache_k=cache_k.data_ptr(), cache_v=cache_v.data_ptr(),
+            slot_bytes=cache_k[0].numel() * cache_k.element_size(),
+            nslots=min(cache_k.shape[0], cache_v.shape[0]), slots=slots.data_ptr(),
+            codec_bits=codec_bits, heads=heads, head_dim=head_dim, layer=layer,
+            staging=None if staging is None else staging.data_ptr(),
+            fail_count=None if fail_count is None else fail_count.data_ptr())
+        _check(lib().secure_infer_gpu_writeback_layer(_stream(stream), self._h, ct.byref(d)),
+               "writeback_layer")
+
+
+def set_chunk_rows(jmax: int) -> None:
+    _check(lib().secure_infer_gpu_set_chunk_rows(jmax), "set_chunk_rows")
+
+
+class NativeTransfer:
+    """Per-layer authenticated reload driver (native_layerwise.py:85-130).
+
+    ``single_layer_kv_transfer((wire, mapping), (cache_k, cache_v))`` reloads
+    one layer: ``wire`` holds 2*N device wire records (K blocks then V blocks,
+    tickets ``ticket_base .. ticket_base+2N-1``), ``mapping`` is the [N, 2]
+    int64 (cpu_block, gpu_slot) table of vLLM's swap_blocks.  The whole layer
+    is one fused launch bracketed by the layer-group calls; the layer's
+    authentication result is then available through ``wait_layer``.
+    """
+
+    def __init__(self, session: GcmSession, shape: LayerShape, stream=None):
+        self.session = session
+        self.shape = shape
+        self.stream = stream
+        self.layer = 0
+        self._fail = {}
+        self._events = {}
+        self._staging = None
+
+    def single_layer_kv_transfer(self, payload, destination, ticket_base: int) -> None:
+        wire, mapping = payload
+        cache_k, cache_v = destination
+        n = int(mapping.shape[0])
+        slots = mapping[:, 1].to(device=cache_k.device, dtype=torch.int64)
+        slots = torch.cat([slots, slots]).contiguous()
+        nbytes = self.shape.record_bytes
+        staging = None
+        if self.shape.codec_bits:
+            need = 2 * n * wire_tag_offset(nbytes)
+            if self._staging is None or self._staging.numel() < need:
+                self._staging = torch.empty(need, dtype=torch.uint8, device=cache_k.device)
+            staging = self._staging
+        fail = torch.zeros(1, dtype=torch.int32, device=cache_k.device)
+        _check(lib().secure_infer_h2d_layer_group_begin(2 * n), "h2d_layer_group_begin")
+        try:
+            self.session.reload_layer(wire, nbytes, 2 * n, n, cache_k, cache_v, slots,
+                                      ticket_base=ticket_base,
+                                      codec_bits=self.shape.codec_bits, heads=self.shape.heads,
+                                      head_dim=self.shape.head_dim, layer=self.layer,
+                                      staging=staging, fail_count=fail, stream=self.stream)
+        finally:
+            _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
+        ev = torch.cuda.Event()
+        ev.record(self.stream if self.stream is not None else torch.cuda.current_stream())
+        self._fail[self.layer] = fail
+        self._events[self.layer] = ev
+        _check(lib().secure_infer_recovery_track_layer(self.layer, ct.c_void_p(ev.cuda_event),
+                                                       ct.c_void_p(fail.data_ptr())),
+               "recovery_track_layer")
+        self.layer += 1
+
+    def wait_layer(self, layer: int) -> int:
+        """0 if every record of `layer` authenticated, -1 otherwise."""
+        rc = int(lib().secure_infer_recovery_wait_layer_authentication(layer))
+        self._fail.pop(layer, None)
+        self._events.pop(layer, None)
+        return rc

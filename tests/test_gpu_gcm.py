@@ -1,0 +1,281 @@
+"""GPU parity tests: the HIP path through the C-ABI against the oracle and
+OpenSSL (the reference's host AES-128-GCM) on the same key, IV and inputs.
+
+Integer / byte work: every comparison is bit-exact.  Ported from the
+reference's device known-answer test (tests/crypto_smoke.py: sizes 16, 31,
+32768, 262144 B, 64-B AAD; device encrypt == host AES-GCM, host encrypt ->
+device decrypt, keystream + verify_xor) plus fail-closed tamper cases.
+"""
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+import secure_infer_amd as si
+from oracle import oracle as O
+from tests import wire as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rand_bytes(rng, n):
+    return rng.integers(0, 256, n, dtype=np.uint8)
+
+
+SIZES = [16, 31, 1000, 32768, 40976, 147472, 262144]
+
+
+@pytest.mark.parametrize("n", SIZES)
+def test_kernel_mirrors_match_openssl(n):
+    rng = np.random.default_rng(n)
+    key, iv12, aad = rand_bytes(rng, 16), rand_bytes(rng, 12), rand_bytes(rng, 64)
+    pt = rand_bytes(rng, n)
+    ref_ct, ref_tag = O.ossl_gcm_encrypt(key.tobytes(), iv12.tobytes(), aad, pt)
+    h = np.frombuffer(O.hash_subkey(key.tobytes()), np.uint8)
+    iv = struct.unpack(">III", iv12.tobytes()) + (2,)
+    dk, dh, da, dp = dev(key), dev(h), dev(aad), dev(pt)
+    c = torch.empty_like(dp)
+    tag = torch.zeros(16, dtype=torch.uint8, device=DEV)
+    si.gcm_encrypt_tag(dp, dk, dh, c, tag, iv, aad=da)
+    assert np.array_equal(host(c), ref_ct), "device encryption mismatch"
+    assert host(tag).tobytes() == ref_tag
+
+    dc, dt = dev(ref_ct), dev(np.frombuffer(ref_tag, np.uint8))
+    out = torch.zeros_like(dc)
+    st = torch.full((1,), 7, dtype=torch.int32, device=DEV)
+    si.gcm_decrypt_verify(dc, dk, dh, dt, out, st, iv, aad=da)
+    assert int(host(st)[0]) == 1 and np.array_equal(host(out), pt)
+
+    ks = torch.empty_like(dc)
+    si.keystream(dk, ks, iv)
+    assert np.array_equal(host(ks), O.keystream(key.tobytes(), iv, n))
+    out2 = torch.zeros_like(dc)
+    st2 = torch.zeros(1, dtype=torch.int32, device=DEV)
+    si.gcm_verify_xor(dc, dk, dh, dt, ks, out2, st2, iv, aad=da)
+    assert int(host(st2)[0]) == 1 and np.array_equal(host(out2), pt)
+
+    st3 = torch.zeros(1, dtype=torch.int32, device=DEV)
+    si.gcm_verify_only(dc, dk, dh, dt, st3, iv, aad=da)
+    assert int(host(st3)[0]) == 1
+
+    back = torch.empty_like(dc)
+    si.aes_ctr(dc, dk, back, iv)
+    assert np.array_equal(host(back), pt)
+
+
+def test_no_aad_and_unaligned_buffers():
+    rng = np.random.default_rng(5)
+    n = 4099
+    key, pt = rand_bytes(rng, 16), rand_bytes(rng, n)
+    iv = (0x11223344, 0x55667788, 0x99AABBCC, 2)
+    ref_ct, ref_tag = O.ossl_gcm_encrypt(key.tobytes(), O.iv12_from_words(iv), b"", pt)
+    h = np.frombuffer(O.hash_subkey(key.tobytes()), np.uint8)
+    dk, dh = dev(key), dev(h)
+    big = torch.zeros(n + 3, dtype=torch.uint8, device=DEV)
+    big[1:n + 1] = dev(pt)
+    cbig = torch.zeros(n + 5, dtype=torch.uint8, device=DEV)
+    tag = torch.zeros(16, dtype=torch.uint8, device=DEV)
+    si.gcm_encrypt_tag(big[1:n + 1], dk, dh, cbig[3:n + 3], tag, iv, nbytes=n)
+    assert np.array_equal(host(cbig)[3:n + 3], ref_ct) and host(tag).tobytes() == ref_tag
+    out = torch.zeros(n + 7, dtype=torch.uint8, device=DEV)
+    st = torch.zeros(1, dtype=torch.int32, device=DEV)
+    si.gcm_decrypt_verify(cbig[3:n + 3], dk, dh, tag, out[5:n + 5], st, iv, nbytes=n)
+    o = host(out)
+    assert int(host(st)[0]) == 1 and np.array_equal(o[5:n + 5], pt)
+    assert not o[:5].any() and not o[n + 5:].any()
+
+
+@pytest.mark.parametrize("where", ["ct_first", "ct_last", "tag", "aad"])
+def test_tampered_record_fails_closed(where):
+    rng = np.random.default_rng(11)
+    n = 262144
+    key, aad, pt = rand_bytes(rng, 16), rand_bytes(rng, 64), rand_bytes(rng, n)
+    iv = (0xA1B2C3D4, 0, 77, 2)
+    ct_, tag = O.ossl_gcm_encrypt(key.tobytes(), O.iv12_from_words(iv), aad, pt)
+    tag = bytearray(tag)
+    if where == "ct_first":
+        ct_[0] ^= 1
+    elif where == "ct_last":
+        ct_[-1] ^= 0x80
+    elif where == "tag":
+        tag[15] ^= 4
+    else:
+        aad = aad.copy()
+        aad[63] ^= 2
+    h = np.frombuffer(O.hash_subkey(key.tobytes()), np.uint8)
+    out = torch.full((n,), 0x5A, dtype=torch.uint8, device=DEV)
+    st = torch.full((1,), 9, dtype=torch.int32, device=DEV)
+    si.gcm_decrypt_verify(dev(ct_), dev(key), dev(h), dev(np.frombuffer(bytes(tag), np.uint8)), out, st,
+                          iv, aad=dev(aad))
+    assert int(host(st)[0]) == 0
+    assert not host(out).any()
+    ref_st, _ = O.gcm_decrypt_verify(key.tobytes(), h.tobytes(), iv, aad, ct_, bytes(tag))
+    assert ref_st == 0
+
+
+def test_auth_gate():
+    data = torch.full((1000,), 3, dtype=torch.uint8, device=DEV)
+    ok = torch.ones(1, dtype=torch.int32, device=DEV)
+    si.auth_gate(data, ok)
+    assert host(data).min() == 3
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    si.auth_gate(data, bad)
+    assert not host(data).any()
+
+
+# ---------------------------------------------------------------- layer level
+
+KEY = bytes(range(100, 116))
+SALT = bytes.fromhex("c0ffee01")
+
+
+def make_caches(nslots, heads, dim, fill=0x3C):
+    k = torch.full((nslots, 128, heads, dim), 0, dtype=torch.int16, device=DEV)
+    v = torch.full((nslots, 128, heads, dim), 0, dtype=torch.int16, device=DEV)
+    k.view(torch.uint8).fill_(fill)
+    v.view(torch.uint8).fill_(fill)
+    return k, v
+
+
+@pytest.mark.parametrize("chunk_rows", [16, 1, 3, 64])
+def test_reload_layer_bf16(chunk_rows):
+    rng = np.random.default_rng(21)
+    heads, dim, nb, nslots, layer = 8, 128, 6, 32, 4
+    blocks = W.bf16_blocks(rng, 2 * nb, heads, dim)
+    payloads = [b.view(np.uint8).reshape(-1) for b in blocks]
+    kinds = [0] * nb + [1] * nb
+    cpu_ids = list(rng.permutation(100)[:nb]) * 2
+    ticket0 = 1000
+    wire = W.build_wire(KEY, SALT, payloads, kinds, layer, cpu_ids, ticket0)
+    wire[3 * W.stride(payloads[0].size) + 100] ^= 0x20  # record 3 (a K block) tampered
+    slots_np = rng.permutation(nslots)[:nb].astype(np.int64)
+    slots = dev(np.concatenate([slots_np, slots_np]))
+    ck, cv = make_caches(nslots, heads, dim)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=payloads[0].size)
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    si.set_chunk_rows(chunk_rows)
+    try:
+        dw = dev(wire)
+        sess.reload_layer(dw, payloads[0].size, 2 * nb, nb, ck, cv, slots, ticket_base=ticket0,
+                          fail_count=fail)
+        kk, vv, ww = host(ck), host(cv), host(dw)
+    finally:
+        si.set_chunk_rows(16)
+    st = W.stride(payloads[0].size)
+    toff = W.align32(payloads[0].size)
+    statuses = [int(ww[r * st + toff + 16:r * st + toff + 20].view(np.uint32)[0]) for r in range(2 * nb)]
+    assert statuses == [1, 1, 1, 0, 1, 1] + [1] * nb
+    assert int(host(fail)[0]) == 1
+    used = set(slots_np.tolist())
+    for i in range(nb):
+        s = slots_np[i]
+        if i == 3:
+            assert not kk[s].any()
+        else:
+            assert np.array_equal(kk[s].view(np.uint16), blocks[i])
+        assert np.array_equal(vv[s].view(np.uint16), blocks[nb + i])
+    for s in range(nslots):
+        if s not in used:
+            assert np.all(kk[s].view(np.uint8) == 0x3C) and np.all(vv[s].view(np.uint8) == 0x3C)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_reload_layer_codec(bits):
+    rng = np.random.default_rng(31 + bits)
+    heads, dim, nb, nslots, layer = 4, 128, 5, 16, 2
+    blocks = W.bf16_blocks(rng, 2 * nb, heads, dim)
+    kinds = [0] * nb + [1] * nb
+    packets = [O.codec_encode(blocks[r], bits, kinds[r], layer) for r in range(2 * nb)]
+    n = packets[0].size
+    assert n == si.codec_width(bits, heads, dim)
+    ticket0 = 5000
+    wire = W.build_wire(KEY, SALT, packets, kinds, layer, list(range(2 * nb)), ticket0)
+    wire[(nb + 1) * W.stride(n) + n - 1] ^= 1  # V record 1: flip last ciphertext byte
+    slots_np = rng.permutation(nslots)[:nb].astype(np.int64)
+    ck, cv = make_caches(nslots, heads, dim)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    staging = torch.zeros(2 * nb * W.align32(n), dtype=torch.uint8, device=DEV)
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    sess.reload_layer(dev(wire), n, 2 * nb, nb, ck, cv, dev(np.concatenate([slots_np, slots_np])),
+                      ticket_base=ticket0, codec_bits=bits, heads=heads, head_dim=dim, layer=layer,
+                      staging=staging, fail_count=fail)
+    kk, vv = host(ck), host(cv)
+    assert int(host(fail)[0]) == 1
+    for i in range(nb):
+        s = slots_np[i]
+        assert np.array_equal(kk[s].view(np.uint16), O.codec_decode(packets[i], heads, dim, bits, 0))
+        if i == 1:
+            assert not vv[s].any()
+        else:
+            assert np.array_equal(vv[s].view(np.uint16),
+                                  O.codec_decode(packets[nb + i], heads, dim, bits, 1))
+
+
+@pytest.mark.parametrize("bits", [0, 8, 4])
+def test_writeback_layer(bits):
+    rng = np.random.default_rng(41 + bits)
+    heads, dim, nb, nslots, layer = 8, 128, 4, 16, 7
+    ck, cv = make_caches(nslots, heads, dim)
+    data = O.f32_to_bf16(rng.standard_normal((2, nslots, 128, heads, dim), dtype=np.float32))
+    ck.copy_(dev(data[0].view(np.int16)))
+    cv.copy_(dev(data[1].view(np.int16)))
+    slots_np = rng.permutation(nslots)[:nb].astype(np.int64)
+    kinds = [0] * nb + [1] * nb
+    if bits:
+        plain = [O.codec_encode(data[kinds[r]][slots_np[r % nb]], bits, kinds[r], layer)
+                 for r in range(2 * nb)]
+    else:
+        plain = [data[kinds[r]][slots_np[r % nb]].view(np.uint8).reshape(-1) for r in range(2 * nb)]
+    n = plain[0].size
+    ticket0 = 9000
+    wire = W.wire_aads(KEY, SALT, n, kinds, layer, list(range(2 * nb)), ticket0)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    staging = torch.zeros(2 * nb * W.align32(n), dtype=torch.uint8, device=DEV) if bits else None
+    dw = dev(wire)
+    sess.writeback_layer(dw, n, 2 * nb, nb, ck, cv, dev(np.concatenate([slots_np, slots_np])),
+                         ticket_base=ticket0, codec_bits=bits, heads=heads, head_dim=dim,
+                         layer=layer, staging=staging)
+    ww = host(dw)
+    expect = W.build_wire(KEY, SALT, plain, kinds, layer, list(range(2 * nb)), ticket0, direction=2)
+    st, toff = W.stride(n), W.align32(n)
+    for r in range(2 * nb):
+        o = r * st
+        assert np.array_equal(ww[o:o + n], expect[o:o + n]), f"record {r} ciphertext"
+        assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
+
+
+def test_native_transfer_wait_layer():
+    rng = np.random.default_rng(51)
+    heads, dim, nb, nslots = 2, 128, 3, 8
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=shape.record_bytes)
+    ck, cv = make_caches(nslots, heads, dim)
+    mapping = torch.tensor([[10, 5], [11, 2], [12, 7]], dtype=torch.int64)
+    nt = si.NativeTransfer(sess, shape)
+    tickets = []
+    for layer in range(2):
+        blocks = W.bf16_blocks(rng, 2 * nb, heads, dim)
+        t0 = 20000 + 100 * layer
+        wire = W.build_wire(KEY, SALT, [b.view(np.uint8).reshape(-1) for b in blocks],
+                            [0] * nb + [1] * nb, layer, [10, 11, 12] * 2, t0)
+        if layer == 1:
+            wire[W.align32(shape.record_bytes)] ^= 1  # tag of record 0
+        nt.single_layer_kv_transfer((dev(wire), mapping), (ck, cv), ticket_base=t0)
+        tickets.append(blocks)
+    assert nt.wait_layer(0) == 0
+    assert nt.wait_layer(1) == -1
+    kk = host(ck)
+    assert not kk[5].any()  # layer 1 record 0 (K block -> slot 5) withheld
+    assert np.array_equal(kk[2].view(np.uint16), tickets[1][1])
