@@ -95,7 +95,7 @@ def cpu_baseline(wire_host: np.ndarray, stride: int, nbytes: int, nrec: int, n_k
     t_end = time.time() + budget_s
     while time.time() < t_end or len(times) < 5:
         times.append(run(threads) / 1e9)
-        if len(times) >= 200:
+        if len(times) >= 20000:
             break
     t1 = [run(1) / 1e9 for _ in range(3)]
     med = float(np.median(times))
@@ -117,6 +117,8 @@ def main():
     ap.add_argument("--chunk-rows", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (PMC byte calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: records are independent and need no exchange; "
@@ -125,6 +127,16 @@ def main():
 
     import torch
     import secure_infer_amd as si
+
+    if args.copy_mb:
+        n = args.copy_mb << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 5}), flush=True)
+        return
 
     cfg = CONFIGS[args.config]
     L, H, D, NB, NS, bits = cfg["layers"], cfg["heads"], cfg["dim"], cfg["blocks"], cfg["slots"], cfg["bits"]

@@ -203,22 +203,29 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
     Blk p{};
     p.b[0] = 0x80;  // H^0 = 1
     auto* pow = reinterpret_cast<uint8_t*>(c + 1);
-    Blk ht{};
+    Blk ht{}, ht2{};
     for (uint32_t e = 0; e < npow; ++e) {
         memcpy(pow + 16 * size_t(e), p.b, 16);
         if (e == SI_T) ht = p;
+        if (e == 2 * SI_T) ht2 = p;
         p = mh(p);
     }
-    if (npow <= SI_T) {
-        ht = Blk{};
-        ht.b[0] = 0x80;
-        for (int e = 0; e < SI_T; ++e) ht = mh(ht);
+    if (npow <= 2 * SI_T) {
+        Blk q{};
+        q.b[0] = 0x80;
+        for (int e = 1; e <= 2 * SI_T; ++e) {
+            q = mh(q);
+            if (e == SI_T) ht = q;
+        }
+        ht2 = q;
     }
-    const FixedMul mt(ht);
+    const FixedMul mt(ht), mt2(ht2);
     for (int pos = 0; pos < 32; ++pos)
         for (int v = 0; v < 16; ++v) {
             const Blk& e = mt.t[pos][v];
             c->gh4[pos * 16 + v] = make_uint4(le32(e.b), le32(e.b + 4), le32(e.b + 8), le32(e.b + 12));
+            const Blk& f = mt2.t[pos][v];
+            c->gh4b[pos * 16 + v] = make_uint4(le32(f.b), le32(f.b + 4), le32(f.b + 8), le32(f.b + 12));
         }
     auto out = std::make_unique<DevCtx>();
     if (hipMalloc(&out->dev, img.size()) != hipSuccess) return nullptr;

@@ -15,9 +15,9 @@
 //          wave64 lookup touches each of the 32 banks once per half-wave.  The
 //          address is produced by ONE v_perm_b32: byte1 <- state byte, byte0 <-
 //          the lane's copy offset.
-//   GHASH: 4-bit per-position tables of H^T (T = threads per workgroup):
-//          position p (nibble p of the block, p = 0..31), value v: 16 bytes at
-//          p*256 + v*16.  Y*H^T = XOR_p table[p][nibble_p(Y)].
+//   GHASH: 4-bit per-position tables of H^T and H^2T (T = threads per
+//          workgroup): position p (nibble p of the block, p = 0..31), value v:
+//          16 bytes at p*256 + v*16.  Y*H^T = XOR_p table[p][nibble_p(Y)].
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -36,6 +36,7 @@ struct GcmCtx {
     uint32_t npow;        // entries of the power table that follows
     uint32_t reserved[3];
     uint4 gh4[32 * 16];   // 4-bit tables of H^SI_T
+    uint4 gh4b[32 * 16];  // 4-bit tables of H^(2*SI_T)
     // followed by uint4 hpow[npow]: hpow[e] = H^e in memory byte order
 };
 
@@ -77,13 +78,22 @@ __device__ __forceinline__ AesLane aes_lane(uint32_t lane)
     return l;
 }
 
-// Table word for byte k of state word w: one v_perm_b32 builds the address.
+// Table word for byte k of state word w: one v_perm_b32 builds the address
+// (byte 1 <- the state byte, byte 0 <- the lane's copy offset).
 template <int K>
 __device__ __forceinline__ uint32_t te(const uint32_t* lds, uint32_t w, uint32_t base)
 {
     constexpr uint32_t sel = 0x0c0c0000u | ((4u + K) << 8);
     const uint32_t addr = __builtin_amdgcn_perm(w, base, sel);
     return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + addr);
+}
+
+// Te_K[byte K of w] for K = 0..3 (Te2, Te3 are rotl16 of Te0, Te1).
+template <int K>
+__device__ __forceinline__ uint32_t te_full(const uint32_t* lds, uint32_t w, AesLane l)
+{
+    const uint32_t v = te<K>(lds, w, (K & 1) ? l.b1 : l.b0);
+    return K >= 2 ? rotl16(v) : v;
 }
 
 // Fills the AES region (64 KiB) from Te0; all threads of the block take part.
@@ -102,27 +112,47 @@ __device__ __forceinline__ void aes_fill_lds(uint32_t* lds, const uint32_t* __re
     }
 }
 
-// E_K(counter block) with the three nonce words already XORed with rk[0..2].
-__device__ __forceinline__ void aes_ctr_block(const uint32_t* lds, AesLane l,
-                                              const GcmCtx* __restrict__ ctx, uint32_t n0,
-                                              uint32_t n1, uint32_t n2, uint32_t ctr,
-                                              uint32_t out[4])
+// Round keys held in VGPRs for the whole kernel: rk16 of rounds 1..9 and the
+// plain last-round key.  Loaded through an opaque per-lane zero so the compiler
+// keeps them in vector registers instead of reloading scalars in the loop.
+struct AesKeys {
+    uint32_t rk3;
+    uint32_t r16[36];   // rk16[4..39]
+    uint32_t last[4];   // rk[40..43]
+};
+
+__device__ __forceinline__ void load_keys(const GcmCtx* __restrict__ ctx, AesKeys& k)
 {
-    uint32_t s0 = n0, s1 = n1, s2 = n2, s3 = bswap32(ctr) ^ ctx->rk[3];
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    const uint4* p16 = reinterpret_cast<const uint4*>(ctx->rk16 + 4) + z;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+        const uint4 q = p16[i];
+        k.r16[4 * i] = q.x; k.r16[4 * i + 1] = q.y; k.r16[4 * i + 2] = q.z; k.r16[4 * i + 3] = q.w;
+    }
+    const uint4 q = reinterpret_cast<const uint4*>(ctx->rk + 40)[z];
+    k.last[0] = q.x; k.last[1] = q.y; k.last[2] = q.z; k.last[3] = q.w;
+    k.rk3 = ctx->rk[3 + z];
+}
+
+// Rounds `r0`..9 and the last round from state s.
+__device__ __forceinline__ void aes_rounds(const uint32_t* lds, AesLane l, const AesKeys& k,
+                                           int r0, uint32_t s0, uint32_t s1, uint32_t s2,
+                                           uint32_t s3, uint32_t out[4])
+{
 #pragma unroll
     for (int r = 1; r <= 9; ++r) {
+        if (r < r0) continue;
+        const uint32_t* rk = k.r16 + 4 * (r - 1);
         const uint32_t t0 = xor3(te<0>(lds, s0, l.b0), te<1>(lds, s1, l.b1),
-                                 rotl16(xor3(te<2>(lds, s2, l.b0), te<3>(lds, s3, l.b1),
-                                             ctx->rk16[4 * r + 0])));
+                                 rotl16(xor3(te<2>(lds, s2, l.b0), te<3>(lds, s3, l.b1), rk[0])));
         const uint32_t t1 = xor3(te<0>(lds, s1, l.b0), te<1>(lds, s2, l.b1),
-                                 rotl16(xor3(te<2>(lds, s3, l.b0), te<3>(lds, s0, l.b1),
-                                             ctx->rk16[4 * r + 1])));
+                                 rotl16(xor3(te<2>(lds, s3, l.b0), te<3>(lds, s0, l.b1), rk[1])));
         const uint32_t t2 = xor3(te<0>(lds, s2, l.b0), te<1>(lds, s3, l.b1),
-                                 rotl16(xor3(te<2>(lds, s0, l.b0), te<3>(lds, s1, l.b1),
-                                             ctx->rk16[4 * r + 2])));
+                                 rotl16(xor3(te<2>(lds, s0, l.b0), te<3>(lds, s1, l.b1), rk[2])));
         const uint32_t t3 = xor3(te<0>(lds, s3, l.b0), te<1>(lds, s0, l.b1),
-                                 rotl16(xor3(te<2>(lds, s1, l.b0), te<3>(lds, s2, l.b1),
-                                             ctx->rk16[4 * r + 3])));
+                                 rotl16(xor3(te<2>(lds, s1, l.b0), te<3>(lds, s2, l.b1), rk[3])));
         s0 = t0; s1 = t1; s2 = t2; s3 = t3;
     }
     // Last round: S-box bytes sit in byte 1 of Te0 and byte 2 of Te1.
@@ -131,7 +161,7 @@ __device__ __forceinline__ void aes_ctr_block(const uint32_t* lds, AesLane l,
     out[J] = __builtin_amdgcn_bitop3_b32(                                                  \
         __builtin_amdgcn_perm(te<0>(lds, A, l.b0), te<1>(lds, B, l.b1), 0x0c0c0205u),     \
         __builtin_amdgcn_perm(te<2>(lds, C, l.b0), te<3>(lds, D, l.b1), 0x02050c0cu),     \
-        ctx->rk[40 + J], 0x56)
+        k.last[J], 0x56)
     SI_LAST(0, s0, s1, s2, s3);
     SI_LAST(1, s1, s2, s3, s0);
     SI_LAST(2, s2, s3, s0, s1);
@@ -139,28 +169,94 @@ __device__ __forceinline__ void aes_ctr_block(const uint32_t* lds, AesLane l,
 #undef SI_LAST
 }
 
+// E_K(counter block) with the three nonce words already XORed with rk[0..2].
+__device__ __forceinline__ void aes_ctr_block(const uint32_t* lds, AesLane l, const AesKeys& k,
+                                              uint32_t n0, uint32_t n1, uint32_t n2, uint32_t ctr,
+                                              uint32_t out[4])
+{
+    aes_rounds(lds, l, k, 1, n0, n1, n2, bswap32(ctr) ^ k.rk3, out);
+}
+
+// Counter-mode cache of rounds 1 and 2 (valid while counter bytes 12..13 stay
+// fixed and byte 15 is the same for all of a thread's blocks, i.e. its blocks
+// are 256*q apart).  With state word 3 = bswap(ctr) ^ rk3 the only byte that
+// moves between the thread's blocks is s3.b2 (counter byte 14); round 1 then
+// reduces to one lookup and round 2 to four:
+//   t1 = U1 ^ Te2[s3.b2],  v = C ^ {Te1[t1.b1], Te0[t1.b0], Te3[t1.b3], Te2[t1.b2]}.
+struct CtrCache {
+    uint32_t u1, c0, c1, c2, c3;
+};
+
+__device__ __forceinline__ CtrCache ctr_cache(const uint32_t* lds, AesLane l,
+                                              const GcmCtx* __restrict__ ctx, uint32_t n0,
+                                              uint32_t n1, uint32_t n2, uint32_t s3)
+{
+    const uint32_t* rk = ctx->rk;
+    const uint32_t u0 = te_full<0>(lds, n0, l) ^ te_full<1>(lds, n1, l) ^ te_full<2>(lds, n2, l) ^
+                        te_full<3>(lds, s3, l) ^ rk[4];
+    const uint32_t u2 = te_full<0>(lds, n2, l) ^ te_full<1>(lds, s3, l) ^ te_full<2>(lds, n0, l) ^
+                        te_full<3>(lds, n1, l) ^ rk[6];
+    const uint32_t u3 = te_full<0>(lds, s3, l) ^ te_full<1>(lds, n0, l) ^ te_full<2>(lds, n1, l) ^
+                        te_full<3>(lds, n2, l) ^ rk[7];
+    CtrCache c;
+    c.u1 = te_full<0>(lds, n1, l) ^ te_full<1>(lds, n2, l) ^ te_full<3>(lds, n0, l) ^ rk[5];
+    c.c0 = te_full<0>(lds, u0, l) ^ te_full<2>(lds, u2, l) ^ te_full<3>(lds, u3, l) ^ rk[8];
+    c.c1 = te_full<1>(lds, u2, l) ^ te_full<2>(lds, u3, l) ^ te_full<3>(lds, u0, l) ^ rk[9];
+    c.c2 = te_full<0>(lds, u2, l) ^ te_full<1>(lds, u3, l) ^ te_full<2>(lds, u0, l) ^ rk[10];
+    c.c3 = te_full<0>(lds, u3, l) ^ te_full<1>(lds, u0, l) ^ te_full<3>(lds, u2, l) ^ rk[11];
+    return c;
+}
+
+__device__ __forceinline__ void aes_ctr_block_cached(const uint32_t* lds, AesLane l,
+                                                     const AesKeys& k, const CtrCache& c,
+                                                     uint32_t ctr, uint32_t out[4])
+{
+    const uint32_t s3 = bswap32(ctr) ^ k.rk3;
+    const uint32_t t1 = c.u1 ^ rotl16(te<2>(lds, s3, l.b0));
+    const uint32_t v0 = c.c0 ^ te<1>(lds, t1, l.b1);
+    const uint32_t v1 = c.c1 ^ te<0>(lds, t1, l.b0);
+    const uint32_t v2 = c.c2 ^ rotl16(te<3>(lds, t1, l.b1));
+    const uint32_t v3 = c.c3 ^ rotl16(te<2>(lds, t1, l.b0));
+    aes_rounds(lds, l, k, 3, v0, v1, v2, v3, out);
+}
+
 // ---------------------------------------------------------------- GHASH
 
-// y <- y * H^T with the 4-bit per-position tables in LDS.
-__device__ __forceinline__ void gh_mul_table(const uint4* gh, uint32_t y[4])
+// out = in * H^k with the 4-bit per-position tables of H^k in LDS (position
+// p's 256-byte table is the instruction's immediate offset).  For word w of
+// `in`, L = (w << 4) & 0xf0f0f0f0 and H = w & 0xf0f0f0f0 hold nibble*16 of
+// every low / high nibble in their own bytes, so each lookup address is one
+// byte extract.
+__device__ __forceinline__ void gh_mul(const uint4* tbl, const uint32_t in[4], uint32_t out[4])
 {
     uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
-    const char* base = reinterpret_cast<const char*>(gh);
+    const char* base = reinterpret_cast<const char*>(tbl);
 #pragma unroll
-    for (int p = 0; p < 32; p += 2) {
-        const uint32_t w = y[p >> 3];
-        const int q = p & 7;
-        // nibble q of w sits at bits [4q, 4q+4); its table offset is nibble*16.
-        const uint32_t o0 = q == 0 ? ((w << 4) & 0xf0u) : ((w >> (4 * q - 4)) & 0xf0u);
-        const uint32_t o1 = (w >> (4 * q)) & 0xf0u;
-        const uint4 v0 = *reinterpret_cast<const uint4*>(base + p * 256 + o0);
-        const uint4 v1 = *reinterpret_cast<const uint4*>(base + (p + 1) * 256 + o1);
-        a0 = xor3(a0, v0.x, v1.x);
-        a1 = xor3(a1, v0.y, v1.y);
-        a2 = xor3(a2, v0.z, v1.z);
-        a3 = xor3(a3, v0.w, v1.w);
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = (in[w] << 4) & 0xf0f0f0f0u;
+        const uint32_t hi = in[w] & 0xf0f0f0f0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int p = 8 * w + 2 * b;
+            const uint32_t ol = (lo >> (8 * b)) & 0xffu;
+            const uint32_t oh = (hi >> (8 * b)) & 0xffu;
+            const uint4 v0 = *reinterpret_cast<const uint4*>(base + p * 256 + ol);
+            const uint4 v1 = *reinterpret_cast<const uint4*>(base + (p + 1) * 256 + oh);
+            a0 = xor3(a0, v0.x, v1.x);
+            a1 = xor3(a1, v0.y, v1.y);
+            a2 = xor3(a2, v0.z, v1.z);
+            a3 = xor3(a3, v0.w, v1.w);
+        }
     }
-    y[0] = a0; y[1] = a1; y[2] = a2; y[3] = a3;
+    out[0] = a0; out[1] = a1; out[2] = a2; out[3] = a3;
+}
+
+// y <- y * H^k
+__device__ __forceinline__ void gh_mul_table(const uint4* tbl, uint32_t y[4])
+{
+    uint32_t t[4];
+    gh_mul(tbl, y, t);
+    y[0] = t[0]; y[1] = t[1]; y[2] = t[2]; y[3] = t[3];
 }
 
 // Big-endian-word GF(2^128) helpers (bit 0 = MSB of word 0 = x^0).

@@ -12,11 +12,13 @@
 //     generic multiply by H^(c*CH + T - t) from the per-key power table, which
 //     places the thread's partial at its true exponent.
 // Partials are XOR-reduced over the workgroup and then across workgroups with
-// device-scope atomics; the last workgroup of a record (atomic ticket) adds
-// nothing more, compares the tag in constant time, writes the status and, on
-// failure, zeroes the record's output before the kernel ends.  Every
-// workgroup publishes its stores with an agent-scope release before taking
-// the ticket, so the zeroing is ordered after all plaintext stores.
+// device-scope atomics; the last workgroup of a record (atomic ticket)
+// compares the tag in constant time, writes the status and, on failure,
+// zeroes the record's output before the kernel ends.  The zeroing must land
+// after every plaintext store of the record: full-block stores are issued
+// write-through (sc1, agent-coherent) and drained (s_waitcnt) before a
+// workgroup takes its ticket; byte-granular stores (partial or unaligned
+// blocks) fall back to an agent-scope release (L2 write-back) instead.
 #include "si_device.h"
 #include "si_kernels.h"
 
@@ -121,19 +123,228 @@ __device__ __forceinline__ RecView view_of(const RecBatch& b, uint32_t r)
     return v;
 }
 
-template <int kMode, bool kAligned>
-__global__ __launch_bounds__(SI_T) void gcm_records_kernel(const GcmCtx* __restrict__ ctx,
-                                                           RecBatch batch, Sched sch,
-                                                           RecAcc* __restrict__ acc)
-{
-    __shared__ uint32_t s_aes[256 * 64];  // AES tables; reused for the generic multiply
-    __shared__ uint4 s_gh[32 * 16];
-    __shared__ uint32_t s_red[SI_T / 64][4];
-    __shared__ uint32_t s_last;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Write-through (sc1) 16-byte store: agent-coherent once s_waitcnt drains it,
+// and measured faster than plain or non-temporal stores for this stream.
+__device__ __forceinline__ void st_wt(__amdgpu_buffer_rsrc_t rsrc, uint64_t k, uint4 v)
+{
+    u32x4 w;
+    w.x = v.x; w.y = v.y; w.z = v.z; w.w = v.w;
+    __builtin_amdgcn_raw_buffer_store_b128(w, rsrc, uint32_t(k * 16u), 0, 16 /* sc1 */);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// One general row: any mix of AAD / ciphertext / length blocks, partial
+// blocks and unaligned buffers.  Used for the few rows at a record's ends.
+template <int kMode, bool kAligned, bool kWT>
+__device__ __forceinline__ void row_general(const RecBatch& batch, const Sched& sch, const RecView& v,
+                                            const uint32_t* aes, AesLane lane, const AesKeys& keys,
+                                            uint32_t n0, uint32_t n1, uint32_t n2, int64_t i,
+                                            uint32_t tail, uint32_t aad_tail, uint32_t y[4])
+{
+    if (i < 0) return;
+    uint32_t x[4];
+    if (i >= int64_t(sch.a) && i < int64_t(sch.a) + int64_t(sch.n)) {
+        if (v.bad && !batch.staging) return;
+        const uint64_t k = uint64_t(i - sch.a);
+        const uint32_t valid = k == uint64_t(sch.n) - 1 ? tail : 16u;
+        uint32_t in[4];
+        load_block<kAligned>(v.src + 16 * k, valid, in);
+        if (kMode == MODE_VERIFY) {
+            x[0] = in[0]; x[1] = in[1]; x[2] = in[2]; x[3] = in[3];
+        } else {
+            uint32_t ks[4];
+            if (kMode == MODE_VERIFY_XOR) {
+                load_block<kAligned>(v.ks + 16 * k, valid, ks);
+            } else {
+                aes_ctr_block(aes, lane, keys, n0, n1, n2, v.iv[3] + uint32_t(k), ks);
+            }
+            uint32_t out[4] = {in[0] ^ ks[0], in[1] ^ ks[1], in[2] ^ ks[2], in[3] ^ ks[3]};
+            if (kWT)  // every payload block is a full aligned block
+                st_wt(rsrc_of(v.dst), k, make_uint4(out[0], out[1], out[2], out[3]));
+            else
+                store_block<kAligned>(v.dst + 16 * k, valid, out);
+            if (kMode == MODE_ENCRYPT) {
+                if (valid != 16u) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        const int lo = 4 * w;
+                        const uint32_t keep = valid >= uint32_t(lo + 4) ? 0xffffffffu
+                                              : valid <= uint32_t(lo) ? 0u
+                                              : (1u << (8 * (valid - lo))) - 1u;
+                        out[w] &= keep;
+                    }
+                }
+                x[0] = out[0]; x[1] = out[1]; x[2] = out[2]; x[3] = out[3];
+            } else {
+                x[0] = in[0]; x[1] = in[1]; x[2] = in[2]; x[3] = in[3];
+            }
+        }
+    } else if (i < int64_t(sch.a)) {
+        const uint32_t valid = uint32_t(i) == sch.a - 1 ? aad_tail : 16u;
+        load_block<false>(v.aad + 16 * i, valid, x);
+    } else {
+        // length block [len(A)]_64 || [len(C)]_64 in bits, big-endian
+        const uint64_t abits = uint64_t(sch.aad_bytes) * 8u;
+        const uint64_t cbits = sch.bytes * 8u;
+        x[0] = bswap32(uint32_t(abits >> 32));
+        x[1] = bswap32(uint32_t(abits));
+        x[2] = bswap32(uint32_t(cbits >> 32));
+        x[3] = bswap32(uint32_t(cbits));
+    }
+    y[0] ^= x[0]; y[1] ^= x[1]; y[2] ^= x[2]; y[3] ^= x[3];
+}
+
+// Keystream of ciphertext block k (cached rounds 1-2 when allowed).
+template <bool kCached>
+__device__ __forceinline__ void keystream_block(const uint32_t* aes, AesLane lane, const AesKeys& keys,
+                                                const CtrCache& cc, uint32_t n0, uint32_t n1,
+                                                uint32_t n2, uint32_t ctr, uint32_t ks[4])
+{
+    if (kCached) aes_ctr_block_cached(aes, lane, keys, cc, ctr, ks);
+    else aes_ctr_block(aes, lane, keys, n0, n1, n2, ctr, ks);
+}
+
+// Full-ciphertext rows [j0, j1) of this thread, two rows per step.  The
+// loads of the next pair are issued before the current pair's keystreams are
+// computed (software pipelining), so HBM latency hides behind the AES work.
+// Rows of the fast region whose data is already loaded: straight-line code
+// (no branches), so the compiler interleaves the GHASH work with the
+// independent AES work of every block.  Two rows fold into the accumulator as
+// y <- y*H^2T ^ x_a*H^T ^ x_b: two independent table products instead of a
+// dependent chain of two.
+template <int kMode, bool kCached, int kRows>
+__device__ __forceinline__ void rows_body(const RecView& v, __amdgpu_buffer_rsrc_t dst, const uint4* gh,
+                                          const uint4* gh2, const uint32_t* aes, AesLane lane,
+                                          const AesKeys& keys, const CtrCache& cc, uint32_t n0,
+                                          uint32_t n1, uint32_t n2, const uint64_t (&k)[kRows],
+                                          const uint4 (&in)[kRows], const uint4 (&ksin)[kRows],
+                                          uint32_t y[4])
+{
+    static_assert(kRows == 1 || kRows == 2, "rows per step");
+    uint32_t s[kRows][4];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        if (kMode == MODE_VERIFY_XOR) {
+            s[r][0] = ksin[r].x; s[r][1] = ksin[r].y; s[r][2] = ksin[r].z; s[r][3] = ksin[r].w;
+        } else if (kMode != MODE_VERIFY) {
+            keystream_block<kCached>(aes, lane, keys, cc, n0, n1, n2, v.iv[3] + uint32_t(k[r]), s[r]);
+        }
+    }
+    uint4 o[kRows];
+    uint32_t x[kRows][4];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        o[r] = in[r];
+        if (kMode != MODE_VERIFY)
+            o[r] = make_uint4(in[r].x ^ s[r][0], in[r].y ^ s[r][1], in[r].z ^ s[r][2], in[r].w ^ s[r][3]);
+        const uint4 xv = kMode == MODE_ENCRYPT ? o[r] : in[r];
+        x[r][0] = xv.x; x[r][1] = xv.y; x[r][2] = xv.z; x[r][3] = xv.w;
+    }
+    if (kRows == 2) {
+        uint32_t a[4], b[4];
+        gh_mul(gh2, y, a);
+        gh_mul(gh, x[0], b);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) y[w] = xor3(a[w], b[w], x[kRows - 1][w]);
+    } else {
+        gh_mul_table(gh, y);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) y[w] ^= x[0][w];
+    }
+    if (kMode != MODE_VERIFY) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) st_wt(dst, k[r], o[r]);
+    }
+}
+
+template <int kMode, int kRows>
+__device__ __forceinline__ void load_rows(const uint4* __restrict__ src, const uint4* __restrict__ ksrc,
+                                          const uint64_t (&k)[kRows], uint4 (&in)[kRows],
+                                          uint4 (&ksin)[kRows])
+{
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        in[r] = src[k[r]];
+        if (kMode == MODE_VERIFY_XOR) ksin[r] = ksrc[k[r]];
+    }
+}
+
+// Full-ciphertext rows [j0, j1) of this thread, two rows per step.  Ping-pong
+// buffers: the loads of the next step are issued before the current step's
+// keystreams, so HBM latency hides behind the AES work.
+template <int kMode, bool kCached>
+__device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, const uint4* gh2,
+                                          const uint32_t* aes, AesLane lane, const AesKeys& keys,
+                                          const CtrCache& cc, uint32_t n0, uint32_t n1, uint32_t n2,
+                                          uint64_t k0, uint32_t j0, uint32_t j1, uint32_t y[4])
+{
+    constexpr int kP = 2;
+    const uint4* __restrict__ src = reinterpret_cast<const uint4*>(v.src);
+    const uint4* __restrict__ ksrc = reinterpret_cast<const uint4*>(v.ks);
+    const __amdgpu_buffer_rsrc_t dst = rsrc_of(v.dst);
+    const uint32_t nsteps = (j1 - j0) / kP;
+    const uint32_t jend = j0 + nsteps * kP;
+    if (nsteps) {
+        auto rows_of = [&](uint32_t step, uint64_t (&k)[kP]) {
+            const uint32_t s = step < nsteps ? step : nsteps - 1;  // clamped prefetch
+#pragma unroll
+            for (int r = 0; r < kP; ++r) k[r] = k0 + uint64_t(j0 + s * kP + r) * SI_T;
+        };
+        uint64_t ka[kP], kb[kP];
+        uint4 a[kP], qa[kP], b[kP], qb[kP];
+        rows_of(0, ka);
+        load_rows<kMode, kP>(src, ksrc, ka, a, qa);
+        for (uint32_t st = 0; st < nsteps; st += 2) {
+            rows_of(st + 1, kb);
+            load_rows<kMode, kP>(src, ksrc, kb, b, qb);
+            __builtin_amdgcn_sched_barrier(0);
+            rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, ka, a, qa, y);
+            if (st + 1 >= nsteps) break;
+            rows_of(st + 2, ka);
+            load_rows<kMode, kP>(src, ksrc, ka, a, qa);
+            __builtin_amdgcn_sched_barrier(0);
+            rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, kb, b, qb, y);
+        }
+    }
+    for (uint32_t j = jend; j < j1; ++j) {
+        uint64_t k1[1] = {k0 + uint64_t(j) * SI_T};
+        uint4 a1[1], q1[1];
+        load_rows<kMode, 1>(src, ksrc, k1, a1, q1);
+        rows_body<kMode, kCached, 1>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, k1, a1, q1, y);
+    }
+}
+
+template <int kMode, bool kAligned, bool kWT>
+__global__ __launch_bounds__(SI_T) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sch,
+                        RecAcc* __restrict__ acc)
+{
+    // Exactly 80 KiB so two workgroups share a CU:
+    // [0, 8 KiB) GHASH tables of H^T, [8, 16 KiB) of H^2T, [16, 80 KiB) AES
+    // Te0/Te1 copies.  After the main loop the AES region holds the per-lane
+    // tables of the final generic multiply and the H^T region the reduction.
+    __shared__ uint4 s_lds[1024 + 4096];
+    uint4* const gh = s_lds;
+    uint4* const gh2 = s_lds + 512;
+    uint32_t* const aes = reinterpret_cast<uint32_t*>(s_lds + 1024);
+    uint32_t(*const s_red)[4] = reinterpret_cast<uint32_t(*)[4]>(s_lds);
+    uint32_t* const s_last = reinterpret_cast<uint32_t*>(s_lds + SI_T / 64);
+
+    constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
     const uint32_t tid = threadIdx.x;
-    aes_fill_lds(s_aes, ctx->te0, tid, SI_T);
-    for (uint32_t i = tid; i < 32u * 16u; i += SI_T) s_gh[i] = ctx->gh4[i];
+    aes_fill_lds(aes, ctx->te0, tid, SI_T);
+    for (uint32_t i = tid; i < 32u * 16u; i += SI_T) {
+        gh[i] = ctx->gh4[i];
+        gh2[i] = ctx->gh4b[i];
+    }
+    AesKeys keys;
+    load_keys(ctx, keys);
     __syncthreads();
 
     const uint32_t r = blockIdx.x / sch.nc;
@@ -150,64 +361,55 @@ __global__ __launch_bounds__(SI_T) void gcm_records_kernel(const GcmCtx* __restr
     const uint32_t tail = uint32_t(sch.bytes - (uint64_t(sch.n) - 1) * 16u);  // bytes in last block
     const uint32_t aad_tail = sch.aad_bytes ? uint32_t(sch.aad_bytes - (uint64_t(sch.a) - 1) * 16u) : 0u;
 
+    // Rows whose blocks are all full ciphertext blocks for every thread of
+    // the workgroup take the fast path: i in [a, a + nfull) for all t.
+    const int64_t nfull = int64_t(sch.bytes / 16);
+    int64_t jf0 = int64_t(sch.a) - base;                      // first fast row: base + j*T >= a
+    jf0 = jf0 <= 0 ? 0 : (jf0 + SI_T - 1) / SI_T;
+    int64_t jf1 = int64_t(sch.a) + nfull - base - SI_T;      // last fast row: base + j*T + T-1 < a + nfull
+    jf1 = jf1 < 0 ? 0 : jf1 / SI_T + 1;
+    if (jf1 > int64_t(sch.j)) jf1 = sch.j;
+    if (jf0 > jf1) jf0 = jf1;
+    const bool fast_ok = kAligned && !(v.bad && !batch.staging);
+    if (!fast_ok) jf0 = jf1 = sch.j;
+
     uint32_t y[4] = {0, 0, 0, 0};
-    for (uint32_t j = 0; j < sch.j; ++j) {
-        if (j != 0) gh_mul_table(s_gh, y);
-        const int64_t i = base + int64_t(j) * SI_T + tid;
-        if (i < 0) continue;
-        uint32_t x[4];
-        if (i >= int64_t(sch.a) && i < int64_t(sch.a) + int64_t(sch.n)) {
-            if (v.bad && !batch.staging) continue;
-            const uint64_t k = uint64_t(i - sch.a);
-            const uint32_t valid = k == uint64_t(sch.n) - 1 ? tail : 16u;
-            uint32_t in[4];
-            load_block<kAligned>(v.src + 16 * k, valid, in);
-            if (kMode == MODE_VERIFY) {
-                x[0] = in[0]; x[1] = in[1]; x[2] = in[2]; x[3] = in[3];
-            } else {
-                uint32_t ks[4];
-                if (kMode == MODE_VERIFY_XOR) {
-                    load_block<kAligned>(v.ks + 16 * k, valid, ks);
-                } else {
-                    aes_ctr_block(s_aes, lane, ctx, n0, n1, n2, v.iv[3] + uint32_t(k), ks);
-                }
-                uint32_t out[4] = {in[0] ^ ks[0], in[1] ^ ks[1], in[2] ^ ks[2], in[3] ^ ks[3]};
-                store_block<kAligned>(v.dst + 16 * k, valid, out);
-                if (kMode == MODE_ENCRYPT) {
-                    if (valid != 16u) {
-#pragma unroll
-                        for (int w = 0; w < 4; ++w) {
-                            const int lo = 4 * w;
-                            const uint32_t keep = valid >= uint32_t(lo + 4) ? 0xffffffffu
-                                                  : valid <= uint32_t(lo) ? 0u
-                                                  : (1u << (8 * (valid - lo))) - 1u;
-                            out[w] &= keep;
-                        }
-                    }
-                    x[0] = out[0]; x[1] = out[1]; x[2] = out[2]; x[3] = out[3];
-                } else {
-                    x[0] = in[0]; x[1] = in[1]; x[2] = in[2]; x[3] = in[3];
-                }
-            }
-        } else if (i < int64_t(sch.a)) {
-            const uint32_t valid = uint32_t(i) == sch.a - 1 ? aad_tail : 16u;
-            load_block<false>(v.aad + 16 * i, valid, x);
+    for (uint32_t j = 0; j < uint32_t(jf0); ++j) {
+        if (j != 0) gh_mul_table(gh, y);
+        row_general<kMode, kAligned, kWT>(batch, sch, v, aes, lane, keys, n0, n1, n2,
+                                     base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
+    }
+    if (jf1 > jf0) {
+        // Drain the key / descriptor loads so the loop's memory waits only
+        // track the ciphertext stream.
+        __builtin_amdgcn_s_waitcnt(0);
+        const uint64_t k0 = uint64_t(base + tid - int64_t(sch.a));  // block of row 0 (may wrap; rows >= jf0 are valid)
+        // Counter bytes 12..13 constant over the fast rows of the whole workgroup?
+        const uint32_t clo = v.iv[3] + uint32_t(base + jf0 * SI_T - int64_t(sch.a));
+        const uint32_t chi = v.iv[3] + uint32_t(base + jf1 * SI_T - 1 - int64_t(sch.a));
+        const bool cached = (kMode == MODE_DECRYPT || kMode == MODE_ENCRYPT) && chi >= clo &&
+                            (clo >> 16) == (chi >> 16);
+        if (cached) {
+            const uint32_t s3 = bswap32(v.iv[3] + uint32_t(k0 + uint64_t(jf0) * SI_T)) ^ keys.rk3;
+            const CtrCache cc = ctr_cache(aes, lane, ctx, n0, n1, n2, s3);
+            rows_fast<kMode, true>(v, gh, gh2, aes, lane, keys, cc, n0, n1, n2, k0, uint32_t(jf0),
+                                   uint32_t(jf1), y);
         } else {
-            // length block [len(A)]_64 || [len(C)]_64 in bits, big-endian
-            const uint64_t abits = uint64_t(sch.aad_bytes) * 8u;
-            const uint64_t cbits = sch.bytes * 8u;
-            x[0] = bswap32(uint32_t(abits >> 32));
-            x[1] = bswap32(uint32_t(abits));
-            x[2] = bswap32(uint32_t(cbits >> 32));
-            x[3] = bswap32(uint32_t(cbits));
+            const CtrCache cc{};
+            rows_fast<kMode, false>(v, gh, gh2, aes, lane, keys, cc, n0, n1, n2, k0, uint32_t(jf0),
+                                    uint32_t(jf1), y);
         }
-        y[0] ^= x[0]; y[1] ^= x[1]; y[2] ^= x[2]; y[3] ^= x[3];
+    }
+    for (uint32_t j = uint32_t(jf1); j < sch.j; ++j) {
+        if (j != 0) gh_mul_table(gh, y);
+        row_general<kMode, kAligned, kWT>(batch, sch, v, aes, lane, keys, n0, n1, n2,
+                                     base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
     }
 
     // Tag mask E_K(J0), J0 = nonce || 1, folded in by the owner of block m-1.
     uint32_t ek[4] = {0, 0, 0, 0};
     const bool owns_len = c == 0 && tid == SI_T - 1;
-    if (owns_len) aes_ctr_block(s_aes, lane, ctx, n0, n1, n2, 1u, ek);
+    if (owns_len) aes_ctr_block(aes, lane, keys, n0, n1, n2, 1u, ek);
     __syncthreads();  // AES tables are dead from here on
 
     const int64_t i_last = base + int64_t(sch.j - 1) * SI_T + tid;
@@ -216,7 +418,7 @@ __global__ __launch_bounds__(SI_T) void gcm_records_kernel(const GcmCtx* __restr
         const uint64_t e = i_last >= 0 ? uint64_t(c) * uint64_t(ch) + SI_T - tid : 0u;
         const uint4 zp = reinterpret_cast<const uint4*>(ctx + 1)[e];
         const uint32_t z[4] = {zp.x, zp.y, zp.z, zp.w};
-        gh_mul_generic(y, z, reinterpret_cast<uint4*>(s_aes), tid, SI_T, q);
+        gh_mul_generic(y, z, reinterpret_cast<uint4*>(aes), tid, SI_T, q);
     }
     q[0] ^= ek[0]; q[1] ^= ek[1]; q[2] ^= ek[2]; q[3] ^= ek[3];
     wave_xor4(q);
@@ -237,16 +439,23 @@ __global__ __launch_bounds__(SI_T) void gcm_records_kernel(const GcmCtx* __restr
             for (int k = 0; k < 4; ++k) t[k] ^= s_red[w][k];
         if (sch.nc == 1) {
             s_red[0][0] = t[0]; s_red[0][1] = t[1]; s_red[0][2] = t[2]; s_red[0][3] = t[3];
-            s_last = 1;
+            *s_last = 1;
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 __hip_atomic_fetch_xor(&ra->w[k], t[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            // Release this workgroup's data stores and XORs, take a ticket.
-            const uint32_t prev = __hip_atomic_fetch_add(&ra->count, 1u, __ATOMIC_ACQ_REL,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            s_last = prev == sch.nc - 1 ? 1u : 0u;
-            if (s_last) {
+            // Take a ticket once this workgroup's data stores and XORs are
+            // performed.  Write-through stores are complete after s_waitcnt;
+            // byte-granular stores need the agent-scope release (L2 write-back).
+            uint32_t prev;
+            if (kNeedRelease) {
+                prev = __hip_atomic_fetch_add(&ra->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0);
+                prev = __hip_atomic_fetch_add(&ra->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            *s_last = prev == sch.nc - 1 ? 1u : 0u;
+            if (*s_last) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     s_red[0][k] = __hip_atomic_exchange(&ra->w[k], 0u, __ATOMIC_RELAXED,
@@ -256,7 +465,7 @@ __global__ __launch_bounds__(SI_T) void gcm_records_kernel(const GcmCtx* __restr
         }
     }
     __syncthreads();
-    if (!s_last) return;
+    if (!*s_last) return;
 
     // Finalise the record.
     if (kMode == MODE_ENCRYPT) {
@@ -288,6 +497,8 @@ __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ct
     __shared__ uint32_t s_aes[256 * 64];
     const uint32_t tid = threadIdx.x;
     aes_fill_lds(s_aes, ctx->te0, tid, SI_T);
+    AesKeys keys;
+    load_keys(ctx, keys);
     __syncthreads();
     const AesLane lane = aes_lane(tid & 63u);
     const uint32_t n0 = bswap32(iv.x) ^ ctx->rk[0];
@@ -297,7 +508,7 @@ __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ct
     for (uint64_t k = uint64_t(blockIdx.x) * SI_T + tid; k < nb; k += uint64_t(gridDim.x) * SI_T) {
         const uint32_t valid = k == nb - 1 ? uint32_t(bytes - 16 * k) : 16u;
         uint32_t ks[4], d[4] = {0, 0, 0, 0};
-        aes_ctr_block(s_aes, lane, ctx, n0, n1, n2, iv.w + uint32_t(k), ks);
+        aes_ctr_block(s_aes, lane, keys, n0, n1, n2, iv.w + uint32_t(k), ks);
         if (in) {
             if (aligned) load_block<true>(in + 16 * k, valid, d);
             else load_block<false>(in + 16 * k, valid, d);
@@ -323,10 +534,12 @@ static hipError_t launch_mode(hipStream_t stream, const GcmCtx* ctx, const RecBa
                               const Sched& s, RecAcc* acc, bool aligned)
 {
     const dim3 grid(s.nc * s.nrec), block(SI_T);
-    if (aligned)
-        hipLaunchKernelGGL((gcm_records_kernel<kMode, true>), grid, block, 0, stream, ctx, b, s, acc);
+    if (aligned && s.bytes % 16 == 0)
+        hipLaunchKernelGGL((gcm_records_kernel<kMode, true, true>), grid, block, 0, stream, ctx, b, s, acc);
+    else if (aligned)
+        hipLaunchKernelGGL((gcm_records_kernel<kMode, true, false>), grid, block, 0, stream, ctx, b, s, acc);
     else
-        hipLaunchKernelGGL((gcm_records_kernel<kMode, false>), grid, block, 0, stream, ctx, b, s, acc);
+        hipLaunchKernelGGL((gcm_records_kernel<kMode, false, false>), grid, block, 0, stream, ctx, b, s, acc);
     return hipGetLastError();
 }
 
