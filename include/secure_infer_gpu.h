@@ -211,8 +211,10 @@ int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event,
 
 /* Library build / device information. */
 const char* secure_infer_gpu_version(void);
-/* Tuning: maximum rows (blocks per thread) of one workgroup chunk, 1..256
- * (default 16).  No reference counterpart; used by the benchmark sweep. */
+/* Tuning: minimum rows (blocks per thread) of one workgroup's chunk of a
+ * record, 1..256 (default 8); a launch splits each record into as many chunks
+ * as fill two workgroups per CU.  No reference counterpart; used by the
+ * benchmark sweep and the tests (small values force many chunks). */
 int secure_infer_gpu_set_chunk_rows(int jmax);
 
 #ifdef __cplusplus

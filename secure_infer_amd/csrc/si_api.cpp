@@ -236,7 +236,23 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
     return out;
 }
 
-int g_jmax = 16;
+int g_min_rows = 8;
+
+// Workgroup slots of the GCM kernel on the current device: two per CU (its
+// LDS use).
+uint32_t gcm_slots()
+{
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return uint32_t(2 * cus[dev]);
+}
 
 si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
 {
@@ -247,9 +263,14 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
     s.a = uint32_t((aad_bytes + 15) / 16);
     s.n = uint32_t((bytes + 15) / 16);
     const uint64_t m = uint64_t(s.a) + s.n + 1;
-    const uint64_t chmax = uint64_t(SI_T) * uint64_t(g_jmax);
-    s.nc = uint32_t((m + chmax - 1) / chmax);
-    s.j = uint32_t((m + uint64_t(s.nc) * SI_T - 1) / (uint64_t(s.nc) * SI_T));
+    s.rows = uint32_t((m + SI_T - 1) / SI_T);
+    // K chunks per record: as many as fill the slots once, none shorter than
+    // g_min_rows rows (K = 1 when the records alone fill the device).
+    uint64_t k = gcm_slots() / (nrec ? nrec : 1);
+    const uint64_t kmax = (uint64_t(s.rows) + uint64_t(g_min_rows) - 1) / uint64_t(g_min_rows);
+    if (k > kmax) k = kmax;
+    if (k < 1) k = 1;
+    s.k = uint32_t(k);
     return s;
 }
 
@@ -791,7 +812,7 @@ int secure_infer_recovery_wait_layer_authentication(uint32_t layer)
 int secure_infer_gpu_set_chunk_rows(int jmax)
 {
     if (jmax < 1 || jmax > 256) return -1;
-    g_jmax = jmax;
+    g_min_rows = jmax;
     return 0;
 }
 

@@ -96,19 +96,21 @@ __device__ __forceinline__ uint32_t te_full(const uint32_t* lds, uint32_t w, Aes
     return K >= 2 ? rotl16(v) : v;
 }
 
-// Fills the AES region (64 KiB) from Te0; all threads of the block take part.
+// Fills the AES region (64 KiB) from Te0 with 256 threads: thread e writes
+// the 16 columns of entry e (columns 0..7 hold Te0 copies, 8..15 Te1 copies),
+// starting at column e & 15 so a wave's stores spread over all banks.
 __device__ __forceinline__ void aes_fill_lds(uint32_t* lds, const uint32_t* __restrict__ te0,
-                                             uint32_t tid, uint32_t nthreads)
+                                             uint32_t tid)
 {
-    // 4096 uint4 slots: slot s -> entry s/16, 16-byte column s%16 (columns 0..7
-    // hold Te0 copies, 8..15 hold Te1 copies).  Consecutive threads write
-    // consecutive columns, so the stores are bank-conflict free.
-    uint4* dst = reinterpret_cast<uint4*>(lds);
-    for (uint32_t s = tid; s < 4096u; s += nthreads) {
-        const uint32_t e = s >> 4;
-        uint32_t v = te0[e];
-        if (s & 8u) v = __builtin_amdgcn_alignbit(v, v, 24);  // rotl8
-        dst[s] = make_uint4(v, v, v, v);
+    static_assert(SI_T == 256, "one Te0 entry per thread");
+    const uint32_t v0 = te0[tid];
+    const uint32_t v1 = __builtin_amdgcn_alignbit(v0, v0, 24);  // rotl8
+    uint4* dst = reinterpret_cast<uint4*>(lds) + tid * 16u;
+#pragma unroll
+    for (uint32_t c = 0; c < 16; ++c) {
+        const uint32_t col = (c + tid) & 15u;
+        const uint32_t v = (col & 8u) ? v1 : v0;
+        dst[col] = make_uint4(v, v, v, v);
     }
 }
 
@@ -221,6 +223,130 @@ __device__ __forceinline__ void aes_ctr_block_cached(const uint32_t* lds, AesLan
 }
 
 // ---------------------------------------------------------------- GHASH
+
+// Table reads of one AES round of state s: q[4j + K] = Te_K-source for
+// column j (byte K of word j+K), not yet rotated.
+__device__ __forceinline__ void aes_issue(const uint32_t* lds, AesLane l, const uint32_t s[4],
+                                          uint32_t q[16])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        q[4 * j + 0] = te<0>(lds, s[j], l.b0);
+        q[4 * j + 1] = te<1>(lds, s[(j + 1) & 3], l.b1);
+        q[4 * j + 2] = te<2>(lds, s[(j + 2) & 3], l.b0);
+        q[4 * j + 3] = te<3>(lds, s[(j + 3) & 3], l.b1);
+    }
+}
+
+// Round output from the reads of aes_issue and the pre-rotated round key.
+__device__ __forceinline__ void aes_combine(const uint32_t q[16], const uint32_t* rk16, uint32_t s[4])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        s[j] = xor3(q[4 * j], q[4 * j + 1], rotl16(xor3(q[4 * j + 2], q[4 * j + 3], rk16[j])));
+}
+
+// Last round from the reads of aes_issue: S-box bytes sit in byte 1 of Te0 and
+// byte 2 of Te1; (lo | hi) ^ rk is bitop3 truth table 0x56.
+__device__ __forceinline__ void aes_combine_last(const uint32_t q[16], const uint32_t* rk,
+                                                 uint32_t out[4])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        out[j] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(q[4 * j], q[4 * j + 1], 0x0c0c0205u),
+                                             __builtin_amdgcn_perm(q[4 * j + 2], q[4 * j + 3], 0x02050c0cu),
+                                             rk[j], 0x56);
+}
+
+// Reads [P0, P1) of in * H^k (4-bit per-position tables) into g.
+template <int P0, int P1>
+__device__ __forceinline__ void gh_issue(const uint4* tbl, const uint32_t in[4], uint4 g[])
+{
+    const char* base = reinterpret_cast<const char*>(tbl);
+#pragma unroll
+    for (int p = P0; p < P1; ++p) {
+        const int w = p >> 3, b = (p & 7) >> 1;
+        const uint32_t sh = (p & 1) ? (in[w] & 0xf0f0f0f0u) : ((in[w] << 4) & 0xf0f0f0f0u);
+        g[p - P0] = *reinterpret_cast<const uint4*>(base + p * 256 + ((sh >> (8 * b)) & 0xffu));
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void gh_fold(const uint4 g[], uint32_t acc[4])
+{
+    static_assert(N % 2 == 0, "pairs");
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+        acc[0] = xor3(acc[0], g[i].x, g[i + 1].x);
+        acc[1] = xor3(acc[1], g[i].y, g[i + 1].y);
+        acc[2] = xor3(acc[2], g[i].z, g[i + 1].z);
+        acc[3] = xor3(acc[3], g[i].w, g[i + 1].w);
+    }
+}
+
+#define SI_STAGE() __builtin_amdgcn_sched_barrier(0)
+
+// Keystreams of two counter blocks (counter-mode cache of rounds 1-2) and the
+// GHASH fold of a ciphertext row pair, acc = y*H^2T ^ xa*H^T, software
+// pipelined by hand: each stage consumes reads issued two stages earlier and
+// issues the next ones, and scheduling barriers keep the stages apart, so a
+// wave keeps its LDS queue (15 reads) full instead of draining it every few
+// reads.  Stage order per AES round r: GHASH slice, combine A(r-1) + issue
+// A(r), combine B(r-1) + issue B(r).
+__device__ __forceinline__ void ctr2_ghash2(const uint32_t* lds, AesLane l, const AesKeys& k,
+                                            const CtrCache& c, uint32_t ctr_a, uint32_t ctr_b,
+                                            const uint4* gh, const uint4* gh2, const uint32_t y[4],
+                                            const uint32_t xa[4], uint32_t ks_a[4],
+                                            uint32_t ks_b[4], uint32_t acc[4])
+{
+    acc[0] = acc[1] = acc[2] = acc[3] = 0;
+    uint32_t a[4], b[4], qa[16], qb[16];
+    uint4 g0[8], g1[8];
+    uint32_t ra, rb, ta, tb;
+    // Round 1: one varying read per block.
+    ra = te<2>(lds, bswap32(ctr_a) ^ k.rk3, l.b0);
+    rb = te<2>(lds, bswap32(ctr_b) ^ k.rk3, l.b0);
+    gh_issue<0, 8>(gh2, y, g0);
+    SI_STAGE();
+    // Round 2: four varying reads per block.
+    ta = c.u1 ^ rotl16(ra);
+    qa[0] = te<1>(lds, ta, l.b1); qa[1] = te<0>(lds, ta, l.b0);
+    qa[2] = te<3>(lds, ta, l.b1); qa[3] = te<2>(lds, ta, l.b0);
+    tb = c.u1 ^ rotl16(rb);
+    qb[0] = te<1>(lds, tb, l.b1); qb[1] = te<0>(lds, tb, l.b0);
+    qb[2] = te<3>(lds, tb, l.b1); qb[3] = te<2>(lds, tb, l.b0);
+    SI_STAGE();
+    gh_fold<8>(g0, acc);
+    gh_issue<8, 16>(gh2, y, g1);
+    SI_STAGE();
+    a[0] = c.c0 ^ qa[0]; a[1] = c.c1 ^ qa[1]; a[2] = c.c2 ^ rotl16(qa[2]); a[3] = c.c3 ^ rotl16(qa[3]);
+    aes_issue(lds, l, a, qa);
+    SI_STAGE();
+    b[0] = c.c0 ^ qb[0]; b[1] = c.c1 ^ qb[1]; b[2] = c.c2 ^ rotl16(qb[2]); b[3] = c.c3 ^ rotl16(qb[3]);
+    aes_issue(lds, l, b, qb);
+    SI_STAGE();
+#define SI_ROUND(R, FOLD_N, FOLD_G, ISSUE)                                \
+    gh_fold<FOLD_N>(FOLD_G, acc);                                         \
+    ISSUE;                                                                \
+    SI_STAGE();                                                           \
+    aes_combine(qa, k.r16 + 4 * ((R) - 1), a);                            \
+    aes_issue(lds, l, a, qa);                                             \
+    SI_STAGE();                                                           \
+    aes_combine(qb, k.r16 + 4 * ((R) - 1), b);                            \
+    aes_issue(lds, l, b, qb);                                             \
+    SI_STAGE();
+    SI_ROUND(3, 8, g1, (gh_issue<16, 22>(gh2, y, g0)))
+    SI_ROUND(4, 6, g0, (gh_issue<22, 30>(gh2, y, g1)))
+    SI_ROUND(5, 8, g1, (gh_issue<30, 32>(gh2, y, g0), gh_issue<0, 6>(gh, xa, g0 + 2)))
+    SI_ROUND(6, 8, g0, (gh_issue<6, 12>(gh, xa, g1)))
+    SI_ROUND(7, 6, g1, (gh_issue<12, 20>(gh, xa, g0)))
+    SI_ROUND(8, 8, g0, (gh_issue<20, 26>(gh, xa, g1)))
+    SI_ROUND(9, 6, g1, (gh_issue<26, 32>(gh, xa, g0)))
+#undef SI_ROUND
+    aes_combine_last(qa, k.last, ks_a);
+    aes_combine_last(qb, k.last, ks_b);
+    gh_fold<6>(g0, acc);
+}
 
 // out = in * H^k with the 4-bit per-position tables of H^k in LDS (position
 // p's 256-byte table is the instruction's immediate offset).  For word w of

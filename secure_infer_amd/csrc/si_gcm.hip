@@ -2,23 +2,26 @@
 //
 // One launch processes a batch of records.  Each record's GHASH input is the
 // block sequence X = AAD || C || L (SP 800-38D), m = a + n + 1 blocks, and
-// GHASH = XOR_k X_k * H^(m-k).  The record is cut into NC chunks of CH = J*T
-// blocks, counted from the end of X; workgroup (r, c) owns chunk c and thread
-// t of it owns blocks base_c + j*T + t (j = 0..J-1), so every row of a chunk
-// is one coalesced 4 KiB sweep.  Per thread:
+// GHASH = XOR_k X_k * H^(m-k).  X is cut into R rows of T blocks counted from
+// its end (row R-1 ends with L; row 0 may start before X), and thread t of a
+// workgroup owns block t of each of its rows, so every row is one coalesced
+// 4 KiB sweep.  Each record's rows are split into K contiguous chunks, one
+// per workgroup.  Per thread:
 //   * CTR: keystream of counter iv3 + k for ciphertext block k (32-bit wrap,
 //     ghash.aicpu:174-221), XORed into the data and stored;
 //   * GHASH: Horner with H^T over the thread's blocks (LDS tables), then one
-//     generic multiply by H^(c*CH + T - t) from the per-key power table, which
-//     places the thread's partial at its true exponent.
+//     generic multiply by H^((R - q1)*T + T - t) from the per-key power table
+//     (q1 = end row of the chunk), which places the
+//     thread's partial at its true exponent.
 // Partials are XOR-reduced over the workgroup and then across workgroups with
-// device-scope atomics; the last workgroup of a record (atomic ticket)
-// compares the tag in constant time, writes the status and, on failure,
-// zeroes the record's output before the kernel ends.  The zeroing must land
-// after every plaintext store of the record: full-block stores are issued
-// write-through (sc1, agent-coherent) and drained (s_waitcnt) before a
-// workgroup takes its ticket; byte-granular stores (partial or unaligned
-// blocks) fall back to an agent-scope release (L2 write-back) instead.
+// device-scope atomics; a ticket names the workgroup that completes a
+// record, which compares the tag in constant time, writes the
+// status and, on failure, zeroes the record's output before the kernel ends.
+// The zeroing must land after every plaintext store of the record:
+// full-block stores are issued write-through (sc1, agent-coherent) and
+// drained (s_waitcnt) before a workgroup takes its ticket; byte-granular
+// stores (partial or unaligned blocks) fall back to an agent-scope release
+// (L2 write-back) instead.
 #include "si_device.h"
 #include "si_kernels.h"
 
@@ -227,6 +230,17 @@ __device__ __forceinline__ void rows_body(const RecView& v, __amdgpu_buffer_rsrc
                                           uint32_t y[4])
 {
     static_assert(kRows == 1 || kRows == 2, "rows per step");
+    if constexpr (kRows == 2 && kCached && kMode == MODE_DECRYPT) {
+        // GHASH reads ciphertext only, so it interleaves with the keystreams.
+        const uint32_t xa[4] = {in[0].x, in[0].y, in[0].z, in[0].w};
+        uint32_t ka[4], kb[4], acc[4];
+        ctr2_ghash2(aes, lane, keys, cc, v.iv[3] + uint32_t(k[0]), v.iv[3] + uint32_t(k[1]), gh, gh2,
+                    y, xa, ka, kb, acc);
+        y[0] = acc[0] ^ in[1].x; y[1] = acc[1] ^ in[1].y; y[2] = acc[2] ^ in[1].z; y[3] = acc[3] ^ in[1].w;
+        st_wt(dst, k[0], make_uint4(in[0].x ^ ka[0], in[0].y ^ ka[1], in[0].z ^ ka[2], in[0].w ^ ka[3]));
+        st_wt(dst, k[1], make_uint4(in[1].x ^ kb[0], in[1].y ^ kb[1], in[1].z ^ kb[2], in[1].w ^ kb[3]));
+        return;
+    }
     uint32_t s[kRows][4];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
@@ -320,44 +334,22 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
     }
 }
 
+// Rows [q0, q1) of one record: Horner with H^T over the thread's blocks into
+// y.  Row q holds blocks m - (R - q)*T + t (row R-1 ends with the length
+// block).  The owner of the length block also returns the tag mask E_K(J0).
 template <int kMode, bool kAligned, bool kWT>
-__global__ __launch_bounds__(SI_T) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sch,
-                        RecAcc* __restrict__ acc)
+__device__ __forceinline__ void segment_rows(const GcmCtx* __restrict__ ctx, const RecBatch& batch,
+                                             const Sched& sch, const RecView& v, const uint4* gh,
+                                             const uint4* gh2, const uint32_t* aes, AesLane lane,
+                                             const AesKeys& keys, uint32_t tid, uint32_t q0,
+                                             uint32_t q1, uint32_t y[4], uint32_t ek[4])
 {
-    // Exactly 80 KiB so two workgroups share a CU:
-    // [0, 8 KiB) GHASH tables of H^T, [8, 16 KiB) of H^2T, [16, 80 KiB) AES
-    // Te0/Te1 copies.  After the main loop the AES region holds the per-lane
-    // tables of the final generic multiply and the H^T region the reduction.
-    __shared__ uint4 s_lds[1024 + 4096];
-    uint4* const gh = s_lds;
-    uint4* const gh2 = s_lds + 512;
-    uint32_t* const aes = reinterpret_cast<uint32_t*>(s_lds + 1024);
-    uint32_t(*const s_red)[4] = reinterpret_cast<uint32_t(*)[4]>(s_lds);
-    uint32_t* const s_last = reinterpret_cast<uint32_t*>(s_lds + SI_T / 64);
-
-    constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
-    const uint32_t tid = threadIdx.x;
-    aes_fill_lds(aes, ctx->te0, tid, SI_T);
-    for (uint32_t i = tid; i < 32u * 16u; i += SI_T) {
-        gh[i] = ctx->gh4[i];
-        gh2[i] = ctx->gh4b[i];
-    }
-    AesKeys keys;
-    load_keys(ctx, keys);
-    __syncthreads();
-
-    const uint32_t r = blockIdx.x / sch.nc;
-    const uint32_t c = blockIdx.x % sch.nc;
-    const RecView v = view_of(batch, r);
-    const AesLane lane = aes_lane(tid & 63u);
     const uint32_t n0 = bswap32(v.iv[0]) ^ ctx->rk[0];
     const uint32_t n1 = bswap32(v.iv[1]) ^ ctx->rk[1];
     const uint32_t n2 = bswap32(v.iv[2]) ^ ctx->rk[2];
-
     const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
-    const int64_t ch = int64_t(sch.j) * SI_T;
-    const int64_t base = m - int64_t(c + 1) * ch;
+    const int64_t base = m - int64_t(sch.rows - q0) * SI_T;
+    const uint32_t J = q1 - q0;
     const uint32_t tail = uint32_t(sch.bytes - (uint64_t(sch.n) - 1) * 16u);  // bytes in last block
     const uint32_t aad_tail = sch.aad_bytes ? uint32_t(sch.aad_bytes - (uint64_t(sch.a) - 1) * 16u) : 0u;
 
@@ -368,16 +360,16 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     jf0 = jf0 <= 0 ? 0 : (jf0 + SI_T - 1) / SI_T;
     int64_t jf1 = int64_t(sch.a) + nfull - base - SI_T;      // last fast row: base + j*T + T-1 < a + nfull
     jf1 = jf1 < 0 ? 0 : jf1 / SI_T + 1;
-    if (jf1 > int64_t(sch.j)) jf1 = sch.j;
+    if (jf1 > int64_t(J)) jf1 = J;
     if (jf0 > jf1) jf0 = jf1;
     const bool fast_ok = kAligned && !(v.bad && !batch.staging);
-    if (!fast_ok) jf0 = jf1 = sch.j;
+    if (!fast_ok) jf0 = jf1 = J;
 
-    uint32_t y[4] = {0, 0, 0, 0};
+    y[0] = y[1] = y[2] = y[3] = 0;
     for (uint32_t j = 0; j < uint32_t(jf0); ++j) {
         if (j != 0) gh_mul_table(gh, y);
         row_general<kMode, kAligned, kWT>(batch, sch, v, aes, lane, keys, n0, n1, n2,
-                                     base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
+                                          base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
     }
     if (jf1 > jf0) {
         // Drain the key / descriptor loads so the loop's memory waits only
@@ -400,30 +392,75 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
                                     uint32_t(jf1), y);
         }
     }
-    for (uint32_t j = uint32_t(jf1); j < sch.j; ++j) {
+    for (uint32_t j = uint32_t(jf1); j < J; ++j) {
         if (j != 0) gh_mul_table(gh, y);
         row_general<kMode, kAligned, kWT>(batch, sch, v, aes, lane, keys, n0, n1, n2,
-                                     base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
+                                          base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
     }
+    ek[0] = ek[1] = ek[2] = ek[3] = 0;
+    if (q1 == sch.rows && tid == SI_T - 1) aes_ctr_block(aes, lane, keys, n0, n1, n2, 1u, ek);
+}
 
-    // Tag mask E_K(J0), J0 = nonce || 1, folded in by the owner of block m-1.
-    uint32_t ek[4] = {0, 0, 0, 0};
-    const bool owns_len = c == 0 && tid == SI_T - 1;
-    if (owns_len) aes_ctr_block(aes, lane, keys, n0, n1, n2, 1u, ek);
-    __syncthreads();  // AES tables are dead from here on
+// Workgroup w = r*K + c owns rows [c*R/K, (c+1)*R/K) of record r (K chunks
+// per record, chosen by the host so that the grid fills two workgroups per
+// CU without a chunk ever spanning two records).
+template <int kMode, bool kAligned, bool kWT>
+__global__ __launch_bounds__(SI_T) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sch,
+                        RecAcc* __restrict__ acc)
+{
+    // Exactly 80 KiB so two workgroups share a CU:
+    // [0, 8 KiB) GHASH tables of H^T, [8, 16 KiB) of H^2T, [16, 80 KiB) AES
+    // Te0/Te1 copies.  After the row work the AES region holds the per-lane
+    // tables of the placement multiply and the H^T region the reduction.
+    __shared__ uint4 s_lds[1024 + 4096];
+    uint4* const gh = s_lds;
+    uint4* const gh2 = s_lds + 512;
+    uint32_t* const aes = reinterpret_cast<uint32_t*>(s_lds + 1024);
+    uint32_t(*const s_red)[4] = reinterpret_cast<uint32_t(*)[4]>(s_lds);
+    uint32_t* const s_last = reinterpret_cast<uint32_t*>(s_lds + SI_T / 64);
 
-    const int64_t i_last = base + int64_t(sch.j - 1) * SI_T + tid;
+    constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
+    const uint32_t tid = threadIdx.x;
+    {
+        // Every global load of the set-up is issued before the first LDS
+        // write, so the whole fill costs about one L2 round trip.
+        const uint4 g0 = ctx->gh4[tid], g1 = ctx->gh4[tid + SI_T];
+        const uint4 g2 = ctx->gh4b[tid], g3 = ctx->gh4b[tid + SI_T];
+        aes_fill_lds(aes, ctx->te0, tid);
+        gh[tid] = g0; gh[tid + SI_T] = g1;
+        gh2[tid] = g2; gh2[tid + SI_T] = g3;
+    }
+    AesKeys keys;
+    load_keys(ctx, keys);
+    __syncthreads();
+
+    const uint32_t r = blockIdx.x / sch.k;
+    const uint32_t c = blockIdx.x % sch.k;
+    const uint32_t q0 = uint32_t(uint64_t(c) * sch.rows / sch.k);
+    const uint32_t q1 = uint32_t(uint64_t(c + 1) * sch.rows / sch.k);
+    const RecView v = view_of(batch, r);
+    uint32_t y[4], ek[4];
+    segment_rows<kMode, kAligned, kWT>(ctx, batch, sch, v, gh, gh2, aes, aes_lane(tid & 63u), keys, tid,
+                                       q0, q1, y, ek);
+    __syncthreads();  // AES and GHASH tables are dead from here on
+
+    // Thread t's partial covers blocks whose last one has exponent
+    // (R - q1)*T + T - t; threads whose blocks all precede X carry zero.
     uint32_t q[4] = {0, 0, 0, 0};
     {
-        const uint64_t e = i_last >= 0 ? uint64_t(c) * uint64_t(ch) + SI_T - tid : 0u;
+        const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
+        const int64_t i_last = m - int64_t(sch.rows - q1 + 1) * SI_T + tid;
+        const uint64_t e = i_last >= 0 ? uint64_t(sch.rows - q1) * SI_T + SI_T - tid : 0u;
         const uint4 zp = reinterpret_cast<const uint4*>(ctx + 1)[e];
         const uint32_t z[4] = {zp.x, zp.y, zp.z, zp.w};
         gh_mul_generic(y, z, reinterpret_cast<uint4*>(aes), tid, SI_T, q);
     }
     q[0] ^= ek[0]; q[1] ^= ek[1]; q[2] ^= ek[2]; q[3] ^= ek[3];
     wave_xor4(q);
-    // Every wave's data stores must have reached L2 before thread 0's
-    // agent-scope release below writes L2 back (s_barrier does not wait).
+    // Every wave's data stores must be complete (write-through) or at least
+    // in L2 (before thread 0's release) when the ticket is taken; s_barrier
+    // does not wait for them.
     __builtin_amdgcn_s_waitcnt(0);
     if ((tid & 63u) == 0) {
         s_red[tid >> 6][0] = q[0]; s_red[tid >> 6][1] = q[1];
@@ -437,7 +474,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         for (int w = 0; w < SI_T / 64; ++w)
 #pragma unroll
             for (int k = 0; k < 4; ++k) t[k] ^= s_red[w][k];
-        if (sch.nc == 1) {
+        if (sch.k == 1) {
             s_red[0][0] = t[0]; s_red[0][1] = t[1]; s_red[0][2] = t[2]; s_red[0][3] = t[3];
             *s_last = 1;
         } else {
@@ -454,7 +491,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
                 __builtin_amdgcn_s_waitcnt(0);
                 prev = __hip_atomic_fetch_add(&ra->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            *s_last = prev == sch.nc - 1 ? 1u : 0u;
+            *s_last = prev == sch.k - 1 ? 1u : 0u;
             if (*s_last) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
@@ -466,7 +503,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     }
     __syncthreads();
     if (!*s_last) return;
-
+    
     // Finalise the record.
     if (kMode == MODE_ENCRYPT) {
         if (tid == 0 && v.bad && batch.fail_count) atomicAdd(batch.fail_count, 1u);
@@ -487,8 +524,6 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     if (!ok && kMode != MODE_VERIFY && !(v.bad && !batch.staging)) zero_bytes(v.dst, sch.bytes, tid, SI_T);
 }
 
-// ---------------------------------------------------------------- CTR only
-
 __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ctx,
                                                    const uint8_t* __restrict__ in,
                                                    uint8_t* __restrict__ out, uint64_t bytes,
@@ -496,7 +531,7 @@ __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ct
 {
     __shared__ uint32_t s_aes[256 * 64];
     const uint32_t tid = threadIdx.x;
-    aes_fill_lds(s_aes, ctx->te0, tid, SI_T);
+    aes_fill_lds(s_aes, ctx->te0, tid);
     AesKeys keys;
     load_keys(ctx, keys);
     __syncthreads();
@@ -533,7 +568,7 @@ template <int kMode>
 static hipError_t launch_mode(hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                               const Sched& s, RecAcc* acc, bool aligned)
 {
-    const dim3 grid(s.nc * s.nrec), block(SI_T);
+    const dim3 grid(s.nrec * s.k), block(SI_T);
     if (aligned && s.bytes % 16 == 0)
         hipLaunchKernelGGL((gcm_records_kernel<kMode, true, true>), grid, block, 0, stream, ctx, b, s, acc);
     else if (aligned)

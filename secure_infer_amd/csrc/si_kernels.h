@@ -42,14 +42,13 @@ struct RecBatch {
 // Work decomposition shared by all records of a batch (uniform sizes).
 struct Sched {
     uint32_t nrec;       // records
-    uint32_t nc;         // chunks per record
-    uint32_t j;          // rows per chunk (blocks per thread)
+    uint32_t rows;       // R: rows of T blocks per record, ceil((a + n + 1) / T)
+    uint32_t k;          // workgroups (row chunks) per record, 1..R
     uint32_t a;          // AAD blocks
     uint32_t n;          // payload blocks
     uint32_t aad_bytes;
     uint64_t bytes;      // payload bytes
 };
-
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                       const Sched& s, RecAcc* acc, bool aligned);
 hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, uint8_t* out,
