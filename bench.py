@@ -1,14 +1,17 @@
-"""Authenticated KV reload benchmark on one MI355X.
+"""Authenticated KV reload / writeback benchmark on one MI355X.
 
 Workload (default): Llama-3-8B KV shape, 32 layers x 8 kv heads x head_dim 128,
 bf16 ~N(0,1), a 6144-token prefix = 48 blocks of 128 tokens, reloaded into a
 paged cache of 512 slots per (layer, kind) at a seeded permutation of slots.
 One record = one (block, kind) slice of 262,144 B; 96 records per layer.  A
 step reloads all 32 layers, one fused verify + decrypt + scatter launch per
-layer, with the ciphertext wire records already resident in HBM.
+layer, with the ciphertext wire records already resident in HBM.  Other
+workloads (--config): int8 / int4 codec reloads (the int4 one with 1 % of the
+records tampered, which must fail closed) and a Llama-3-70B int4 writeback.
 
-Prints ONE JSON line.  `value` is GB/s of algorithmic bytes
-(per record: ciphertext read + plaintext write + tag + AAD + status).
+Prints ONE JSON line.  `value` is GB/s of algorithmic bytes over the timed
+region (reload, per record: ciphertext read + bf16 write + tag + AAD + status;
+writeback: bf16 read + ciphertext write + tag + AAD).
 """
 from __future__ import annotations
 
@@ -28,10 +31,15 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "authenticated KV reload GB/s and μs/layer (1 GPU); % of HBM peak"
 
 CONFIGS = {
-    # name: layers, kv_heads, head_dim, blocks, slots, codec bits
-    "reload_bf16_llama3_8b_6144tok": dict(layers=32, heads=8, dim=128, blocks=48, slots=512, bits=0),
-    "reload_int8_llama3_8b_8192tok": dict(layers=32, heads=8, dim=128, blocks=64, slots=512, bits=8),
-    "reload_int4_qwen2_5_7b_8192tok": dict(layers=28, heads=4, dim=128, blocks=64, slots=512, bits=4),
+    # name: direction, layers, kv_heads, head_dim, blocks, slots, codec bits, tampered fraction
+    "reload_bf16_llama3_8b_6144tok": dict(op="reload", layers=32, heads=8, dim=128, blocks=48, slots=512,
+                                          bits=0, tamper=0.0),
+    "reload_int8_llama3_8b_8192tok": dict(op="reload", layers=32, heads=8, dim=128, blocks=64, slots=512,
+                                          bits=8, tamper=0.0),
+    "reload_int4_qwen2_5_7b_8192tok": dict(op="reload", layers=28, heads=4, dim=128, blocks=64, slots=512,
+                                           bits=4, tamper=0.01),
+    "writeback_int4_llama3_70b_32768tok": dict(op="writeback", layers=80, heads=8, dim=128, blocks=256,
+                                               slots=512, bits=4, tamper=0.0),
 }
 DEFAULT = "reload_bf16_llama3_8b_6144tok"
 
@@ -47,9 +55,10 @@ def aad_bytes(direction: int, kind: int, layer: int, block_id: int, nbytes: int,
     return bytes(out)
 
 
-def algorithmic_bytes_per_record(record_bytes: int, out_bytes: int) -> int:
-    # ciphertext read + plaintext (or dequantised bf16) write + tag 16 + AAD 64 + status 4
-    return record_bytes + out_bytes + 16 + 64 + 4
+def algorithmic_bytes_per_record(op: str, record_bytes: int, block_bytes: int) -> int:
+    if op == "reload":  # ciphertext read + bf16 write + tag 16 + AAD 64 + status 4
+        return record_bytes + block_bytes + 16 + 64 + 4
+    return block_bytes + record_bytes + 16 + 64  # bf16 read + ciphertext write + tag + AAD
 
 
 def load_traffic(workload: str):
@@ -63,34 +72,48 @@ def load_traffic(workload: str):
     return None
 
 
-def cpu_baseline(wire_host: np.ndarray, stride: int, nbytes: int, nrec: int, n_k: int, key: bytes,
-                 ivs: np.ndarray, heads: int, dim: int, bits: int, layer: int, sample_layers: int,
-                 budget_s: float, algo_per_layer: int, expect_planes):
-    """OpenSSL EVP AES-128-GCM decrypt + verify + (decode) + scatter into a host
-    paged cache, on the host cores, over the same records the GPU reloaded."""
+def cpu_baseline(op: str, wire_host: np.ndarray, stride: int, nbytes: int, nrec: int, n_k: int,
+                 key: bytes, ivs: np.ndarray, heads: int, dim: int, bits: int, layer: int,
+                 budget_s: float, algo_per_layer: int, planes, gpu_wire: np.ndarray | None):
+    """OpenSSL EVP AES-128-GCM on the host cores over the same records as the
+    GPU: reload = decrypt + verify + (decode) + scatter into a host paged cache;
+    writeback = gather + (encode) + encrypt + tag from one."""
     from oracle import oracle as O
     lib = O.ossl()
     threads = min(len(os.sched_getaffinity(0)), 16)
     slot_bytes = 128 * heads * dim * 2
-    slots = np.arange(nrec, dtype=np.int64) % max(n_k, 1)
+    nb = max(n_k, 1)
+    slots = np.arange(nrec, dtype=np.int64) % nb
     kinds = np.array([0] * n_k + [1] * (nrec - n_k), np.uint32)
-    cache = [np.zeros(max(n_k, 1) * slot_bytes, np.uint8) for _ in range(2)]
+    if op == "reload":
+        cache = [np.zeros(nb * slot_bytes, np.uint8) for _ in range(2)]
+    else:
+        cache = [np.ascontiguousarray(planes[k]).reshape(-1).copy() for k in range(2)]
     status = np.zeros(nrec, np.uint32)
     iv12 = np.ascontiguousarray(
         np.stack([ivs[:, w].astype(">u4").view(np.uint8).reshape(-1, 4) for w in range(3)], 1)
         .reshape(nrec, 12))
     tag_off = (nbytes + 31) & ~31
+    direction = 1 if op == "reload" else 2
 
     def run(nthr):
-        return lib.si_ossl_layer(1, O._ptr(np.frombuffer(key, np.uint8).copy()), O._ptr(iv12),
+        return lib.si_ossl_layer(direction, O._ptr(np.frombuffer(key, np.uint8).copy()), O._ptr(iv12),
                                  O._ptr(wire_host), stride, nbytes, tag_off, tag_off + 32, nrec,
                                  O._ptr(cache[0]), O._ptr(cache[1]), slot_bytes, O._ptr(slots),
                                  O._ptr(kinds), bits, heads, dim, layer, O._ptr(status), nthr)
 
-    run(threads)  # warm-up
-    ok = bool(status.all())
-    same = all(np.array_equal(cache[k].reshape(-1, slot_bytes)[i], expect_planes[k][i])
-               for k in range(2) for i in range(min(2, n_k)))
+    run(threads)  # warm-up (and the result that is compared with the GPU's)
+    if op == "reload":
+        gst = gpu_wire.reshape(nrec, stride)[:, tag_off + 16:tag_off + 20].copy().view("<u4").ravel()
+        ok = bool(np.array_equal(status, gst))  # same accept / reject decision per record
+        same = all(np.array_equal(cache[k].reshape(-1, slot_bytes)[i], planes[k][i])
+                   for k in range(2) for i in range(n_k))
+    else:
+        ok = True
+        w = wire_host.reshape(nrec, stride)
+        g = gpu_wire.reshape(nrec, stride)
+        same = bool(np.array_equal(w[:, :nbytes], g[:, :nbytes]) and
+                    np.array_equal(w[:, tag_off:tag_off + 16], g[:, tag_off:tag_off + 16]))
     times = []
     t_end = time.time() + budget_s
     while time.time() < t_end or len(times) < 5:
@@ -99,13 +122,14 @@ def cpu_baseline(wire_host: np.ndarray, stride: int, nbytes: int, nrec: int, n_k
             break
     t1 = [run(1) / 1e9 for _ in range(3)]
     med = float(np.median(times))
+    what = ("decrypt+verify" + ("+decode" if bits else "") + "+scatter") if op == "reload" else \
+           ("gather" + ("+encode" if bits else "") + "+encrypt+tag")
     return dict(value=round(algo_per_layer / med / 1e9, 3), unit="GB/s", cores=threads,
                 kind="port",
-                sample=(f"OpenSSL {lib.si_ossl_version().decode()} EVP_aes_128_gcm decrypt+verify"
-                        f"{'+decode' if bits else ''}+scatter of one layer ({nrec} records x {nbytes} B)"
-                        f" x {len(times)} reps, median; 1 thread: "
+                sample=(f"OpenSSL {lib.si_ossl_version().decode()} EVP_aes_128_gcm {what} of one layer "
+                        f"({nrec} records x {nbytes} B) x {len(times)} reps, median; 1 thread: "
                         f"{round(algo_per_layer / float(np.median(t1)) / 1e9, 3)} GB/s"),
-                us_per_layer=round(med * 1e6, 1), statuses_ok=ok, matches_gpu=bool(same))
+                us_per_layer=round(med * 1e6, 1), statuses_match_gpu=ok, matches_gpu=bool(same))
 
 
 def main():
@@ -139,6 +163,7 @@ def main():
         return
 
     cfg = CONFIGS[args.config]
+    op = cfg["op"]
     L, H, D, NB, NS, bits = cfg["layers"], cfg["heads"], cfg["dim"], cfg["blocks"], cfg["slots"], cfg["bits"]
     if args.chunk_rows:
         si.set_chunk_rows(args.chunk_rows)
@@ -154,77 +179,102 @@ def main():
     stride = si.wire_stride(nbytes)
     tag_off = si.wire_tag_offset(nbytes)
     sess = si.GcmSession(key, salt, 0, max_record_bytes=nbytes)
+    direction = 1 if op == "reload" else 2
 
-    # paged caches [L, 2, NS, 128, H, D] bf16 and per-layer slot tables
+    # paged caches [L, 2, NS, 128, H, D] bf16 and per-layer slot tables (seeded
+    # permutations of the slots; K records then V records)
     cache = torch.zeros((L, 2, NS, 128, H, D), dtype=torch.bfloat16, device=dev)
     slots = torch.stack([torch.randperm(NS, generator=gen, device=dev)[:NB] for _ in range(L)])
-    slots2 = torch.cat([slots, slots], 1).contiguous()  # K records then V records
-    truth = torch.randn((L, 2, NB, 128, H, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    slots2 = torch.cat([slots, slots], 1).contiguous()
+    for layer in range(L):
+        cache[layer, :, slots[layer]] = torch.randn((2, NB, 128, H, D), generator=gen, device=dev,
+                                                    dtype=torch.float32).to(torch.bfloat16)
 
-    # Wire records: host-built AADs, ciphertext made by the GPU writeback path
-    # (bit-exact with OpenSSL, checked by the parity tests).
+    # Wire records with host-built AADs.  Reload: the ciphertext is made by
+    # the GPU writeback path (bit-exact with OpenSSL, checked by the tests).
     wire = torch.zeros((L, nrec * stride), dtype=torch.uint8, device=dev)
     ticket0 = 1
     aads = np.zeros((L, nrec, 64), np.uint8)
     for layer in range(L):
         for r in range(nrec):
             t = ticket0 + layer * nrec + r
-            aads[layer, r] = np.frombuffer(aad_bytes(1, 0 if r < n_k else 1, layer, r % NB, nbytes, t), np.uint8)
+            aads[layer, r] = np.frombuffer(aad_bytes(direction, 0 if r < n_k else 1, layer, r % NB, nbytes, t),
+                                           np.uint8)
     wv = wire.view(L, nrec, stride)
     wv[:, :, tag_off + 32:tag_off + 96] = torch.from_numpy(aads).to(dev)
     staging = torch.zeros(nrec * tag_off, dtype=torch.uint8, device=dev) if bits else None
-    for layer in range(L):
-        cache[layer, :, slots[layer]] = truth[layer]
-        ck, cv = cache[layer, 0], cache[layer, 1]
-        sess.writeback_layer(wire[layer], nbytes, nrec, n_k, ck, cv, slots2[layer],
+    fails = torch.zeros(L, dtype=torch.int32, device=dev)
+
+    def writeback_layer(layer):
+        sess.writeback_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1], slots2[layer],
                              ticket_base=ticket0 + layer * nrec, codec_bits=bits, heads=H, head_dim=D,
                              layer=layer, staging=staging)
-    torch.cuda.synchronize()
-    cache.zero_()
-    fails = torch.zeros(L, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream()
 
     def reload_layer(layer):
         sess.reload_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1], slots2[layer],
                           ticket_base=ticket0 + layer * nrec, codec_bits=bits, heads=H, head_dim=D,
                           layer=layer, staging=staging, fail_count=fails[layer:layer + 1])
 
+    tampered = []
+    if op == "reload":
+        for layer in range(L):
+            writeback_layer(layer)
+        torch.cuda.synchronize()
+        if cfg["tamper"]:
+            # seeded records with one seeded ciphertext byte flipped: they must fail closed
+            ntam = max(1, round(cfg["tamper"] * L * nrec))
+            picks = rng.choice(L * nrec, ntam, replace=False)
+            for p in picks:
+                layer, r = divmod(int(p), nrec)
+                off = int(rng.integers(0, nbytes))
+                wv[layer, r, off] ^= 0x5A
+                tampered.append((layer, r))
+        if bits == 0:
+            truth = torch.stack([cache[l][:, slots[l]] for l in range(L)]).clone()
+        cache.zero_()
+        step = reload_layer
+    else:
+        step = writeback_layer
+    torch.cuda.synchronize()
+
     for _ in range(args.warmup):
         for layer in range(L):
-            reload_layer(layer)
+            step(layer)
     torch.cuda.synchronize()
     fails.zero_()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps * L)]
+    # Timed region: K steps of one launch per layer on one stream, nothing
+    # else queued; the average launch duration is the region over K*L.
+    stream = torch.cuda.current_stream()
     t_start, t_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    k = 0
     for _ in range(args.steps):
         for layer in range(L):
-            evs[k][0].record(stream)
-            reload_layer(layer)
-            evs[k][1].record(stream)
-            k += 1
+            step(layer)
     t_stop.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_stop)
-    kern_ms = [a.elapsed_time(b) for a, b in evs]
     ms_per_step = total_ms / args.steps
-    kern_avg_us = float(np.mean(kern_ms)) * 1e3
+    us_launch = total_ms * 1e3 / (args.steps * L)
 
     # correctness of what was timed
-    nfail = int(fails.sum().item())
-    if bits == 0:
+    nfail = int(fails.sum().item()) if op == "reload" else 0
+    exact = None
+    if op == "reload" and bits == 0:
         got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
+        if tampered:
+            for layer, r in tampered:
+                k, b = divmod(r, NB)
+                truth[layer, k, b] = 0
         exact = bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
-    else:
-        exact = None
+    tamper_ok = None
+    if op == "reload" and tampered:
+        zeroed = all(bool((cache[l, r // NB, slots[l, r % NB]] == 0).all()) for l, r in tampered)
+        tamper_ok = nfail == len(tampered) * args.steps and zeroed
 
-    out_bytes = block_bytes
-    algo_layer = nrec * algorithmic_bytes_per_record(nbytes, out_bytes)
+    algo_layer = nrec * algorithmic_bytes_per_record(op, nbytes, block_bytes)
     gbs = algo_layer * L / (ms_per_step * 1e-3) / 1e9
-    achieved = algo_layer / (kern_avg_us * 1e-6) / 1e9
+    achieved = algo_layer / (us_launch * 1e-6) / 1e9
     res = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -238,27 +288,30 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic (seeded torch.randn bf16 KV, seeded key/salt; ciphertext produced on device)",
-        "config": {"workload": args.config, "layers": L, "kv_heads": H, "head_dim": D,
+        "config": {"workload": args.config, "direction": op, "layers": L, "kv_heads": H, "head_dim": D,
                    "tokens": NB * 128, "blocks": NB, "records_per_layer": nrec,
                    "record_bytes": nbytes, "cache_slots": NS, "codec_bits": bits,
-                   "algorithmic_bytes_per_layer": algo_layer},
-        "us_per_layer": round(ms_per_step * 1e3 / L, 3),
-        "kernel_us_per_layer": round(kern_avg_us, 3),
+                   "tampered_records": len(tampered), "algorithmic_bytes_per_layer": algo_layer},
+        "us_per_layer": round(us_launch, 3),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "failed_records": nfail,
+        "failed_records_per_step": nfail // max(args.steps, 1),
         "bit_exact": exact,
+        "tamper_fail_closed": tamper_ok,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(args.config)},
     }
     if not args.no_cpu:
         layer = 0
-        wh = wire[layer].cpu().numpy()
         ivs = np.array([sess.record_iv(ticket0 + r) for r in range(nrec)], np.uint32)
         planes = [cache[layer, k][slots[layer]].view(torch.uint8).reshape(NB, -1).cpu().numpy()
                   for k in range(2)]
-        res["cpu_baseline"] = cpu_baseline(wh, stride, nbytes, nrec, n_k, key, ivs, H, D, bits, layer,
-                                           1, args.cpu_budget, algo_layer, planes)
+        gw = wire[layer].cpu().numpy()
+        wh = gw.copy()
+        if op == "writeback":
+            wh.reshape(nrec, stride)[:, :tag_off + 16] = 0  # the host recomputes ciphertext and tags
+        res["cpu_baseline"] = cpu_baseline(op, wh, stride, nbytes, nrec, n_k, key, ivs, H, D, bits, layer,
+                                           args.cpu_budget, algo_layer, planes, gw)
     print(json.dumps(res), flush=True)
 
 
