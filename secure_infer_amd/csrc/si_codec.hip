@@ -9,7 +9,9 @@
 //
 // Float semantics follow the reference's torch ops one rounding at a time:
 // decode v = fl(fl(q*scale) + low) then bf16 round-to-nearest-even; encode
-// scale = max(fl((hi-lo)/(2^bits-1)), 1e-12f), q = clamp(rne(fl(fl(x-lo)/scale))).
+// scale = max(fl((hi-lo)/(2^bits-1)), 1e-12f), q = clamp(rne(fl(fl(x-lo)/scale))),
+// with fl(a/scale) formed from the correctly rounded reciprocal of the
+// group's scale and one FMA correction (bit-identical to IEEE division).
 #include "si_kernels.h"
 
 namespace si {
@@ -27,59 +29,72 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h)
     return __uint_as_float(h << 16);
 }
 
-// One thread -> 8 consecutive elements (16 B of bf16 output).
-__global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint32_t groups_per_rec)
+// n / d for n < 2^24, d < 2^16 (exact): float estimate, then one correction.
+__device__ __forceinline__ uint32_t udiv_small(uint32_t n, uint32_t d)
 {
-    const uint32_t r = blockIdx.x / groups_per_rec;
-    const uint32_t g = (blockIdx.x % groups_per_rec) * 256u + threadIdx.x;
+    uint32_t q = uint32_t(__fmul_rn(float(n), __frcp_rn(float(d))));
+    if (q * d > n) --q;
+    else if ((q + 1u) * d <= n) ++q;
+    return q;
+}
+
+__device__ __forceinline__ uint32_t dq2(float q0, float s0, float o0, float q1, float s1, float o1)
+{
+    const float v0 = __fadd_rn(__fmul_rn(q0, s0), o0);
+    const float v1 = __fadd_rn(__fmul_rn(q1, s1), o1);
+    return f32_to_bf16(v0) | (f32_to_bf16(v1) << 16);
+}
+
+// One thread -> 16 consecutive elements (32 B of bf16 output); grid (x, record).
+// K parameters of the 16 elements are 16 consecutive floats (four 16-byte
+// loads each); V elements share one (t, h, dim-group) parameter pair.
+__global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b)
+{
+    const uint32_t r = blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
-    const uint32_t total = 128u * hd;
-    const uint32_t e0 = g * 8u;
-    if (e0 >= total) return;
+    const uint32_t e0 = (blockIdx.x * 256u + threadIdx.x) * 16u;
+    if (e0 >= 128u * hd) return;
+    const int64_t sid = b.slots[r];
+    if (sid < 0 || sid >= b.nslots) return;
     const uint32_t kind = r < b.n_k ? 0u : 1u;
     const uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
     const float* scale = reinterpret_cast<const float*>(pkt + b.qbytes);
     const float* low = reinterpret_cast<const float*>(pkt + b.qbytes + b.sbytes);
-    const uint32_t t = e0 / hd;
-    const uint32_t rem = e0 % hd;
-    const uint32_t hh = rem / b.dim;
-    const uint32_t dd = rem % b.dim;
+    const uint32_t t = udiv_small(e0, hd);
+    const uint32_t rem = e0 - t * hd;
 
-    float q[8];
+    float q[16];
     if (b.bits == 8) {
-        const uint2 w = *reinterpret_cast<const uint2*>(pkt + e0);
+        const uint4 w = *reinterpret_cast<const uint4*>(pkt + e0);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) q[k] = float((ww[k >> 2] >> (8 * (k & 3))) & 0xffu);
+    } else {
+        const uint2 w = *reinterpret_cast<const uint2*>(pkt + e0 / 2u);
+        const uint32_t ww[2] = {w.x, w.y};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) q[k] = float((ww[k >> 3] >> (4 * (k & 7))) & 0xfu);
+    }
+    uint32_t out[8];
+    if (kind == 0) {
+        const uint32_t p = (t >> 6) * hd + rem;
+        const float4* s4 = reinterpret_cast<const float4*>(scale + p);
+        const float4* o4 = reinterpret_cast<const float4*>(low + p);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            q[k] = float((w.x >> (8 * k)) & 0xffu);
-            q[4 + k] = float((w.y >> (8 * k)) & 0xffu);
+            const float4 sv = s4[k], ov = o4[k];
+            out[2 * k] = dq2(q[4 * k], sv.x, ov.x, q[4 * k + 1], sv.y, ov.y);
+            out[2 * k + 1] = dq2(q[4 * k + 2], sv.z, ov.z, q[4 * k + 3], sv.w, ov.w);
         }
     } else {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(pkt + e0 / 2);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = float((w >> (4 * k)) & 0xfu);
-    }
-    float s[8], o[8];
-    if (kind == 0) {
-        const uint32_t p = (t / 64u) * hd + rem;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) { s[k] = scale[p + k]; o[k] = low[p + k]; }
-    } else {
-        const uint32_t p = (t * b.heads + hh) * (b.dim / 64u) + dd / 64u;
+        const uint32_t p = e0 >> 6;  // (t, h, dim-group) row-major: 64 elements per group
         const float sv = scale[p], ov = low[p];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) { s[k] = sv; o[k] = ov; }
+        for (int k = 0; k < 8; ++k) out[k] = dq2(q[2 * k], sv, ov, q[2 * k + 1], sv, ov);
     }
-    uint32_t out[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float v0 = __fadd_rn(__fmul_rn(q[2 * k], s[2 * k]), o[2 * k]);
-        const float v1 = __fadd_rn(__fmul_rn(q[2 * k + 1], s[2 * k + 1]), o[2 * k + 1]);
-        out[k] = f32_to_bf16(v0) | (f32_to_bf16(v1) << 16);
-    }
-    const int64_t sid = b.slots[r];
-    if (sid < 0 || sid >= b.nslots) return;
-    uint8_t* slot = b.cache[kind] + uint64_t(sid) * b.slot_bytes;
-    *reinterpret_cast<uint4*>(slot + uint64_t(e0) * 2u) = make_uint4(out[0], out[1], out[2], out[3]);
+    uint4* dst = reinterpret_cast<uint4*>(b.cache[kind] + uint64_t(sid) * b.slot_bytes + uint64_t(e0) * 2u);
+    dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
 }
 
 __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
@@ -88,139 +103,196 @@ __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
     return s < 1e-12f ? 1e-12f : s;
 }
 
-__device__ __forceinline__ uint32_t quant_one(float x, float lo, float s, float qmax)
+// RN(1/s) for a normal s: hardware estimate, two Newton steps, then the
+// neighbour with the smallest exact residual |1 - s*y| (one FMA each).
+__device__ __forceinline__ float recip_rn(float s)
 {
-    float q = rintf(__fdiv_rn(__fsub_rn(x, lo), s));
-    q = q < 0.f ? 0.f : q;
-    q = q > qmax ? qmax : q;
-    return uint32_t(q);
+    float y = __builtin_amdgcn_rcpf(s);
+    y = fmaf(fmaf(-s, y, 1.0f), y, y);
+    y = fmaf(fmaf(-s, y, 1.0f), y, y);
+    const float ylo = __uint_as_float(__float_as_uint(y) - 1u);
+    const float yhi = __uint_as_float(__float_as_uint(y) + 1u);
+    const float e = fabsf(fmaf(-s, y, 1.0f));
+    const float elo = fabsf(fmaf(-s, ylo, 1.0f));
+    const float ehi = fabsf(fmaf(-s, yhi, 1.0f));
+    if (elo < e) return ylo;
+    if (ehi < e) return yhi;
+    return y;
 }
 
-// K: one thread per (token group, head, column pair).
-__global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b, uint32_t rec0, uint32_t blocks_per_rec)
+// RN(a/s) given y = RN(1/s) (Markstein: q within 1 ulp of a/s, exact FMA
+// residual r = a - q*s, q + r*y rounds correctly); a >= 0, a/s < 2^23.
+__device__ __forceinline__ float div_rn(float a, float s, float y)
 {
-    const uint32_t r = rec0 + blockIdx.x / blocks_per_rec;
-    const uint32_t idx = (blockIdx.x % blocks_per_rec) * 256u + threadIdx.x;
+    const float q = __fmul_rn(a, y);
+    return fmaf(fmaf(-q, s, a), y, q);
+}
+
+// q = clamp(rne(RN((x - lo) / s)), 0, qmax) as an integer: the clamp commutes
+// with rounding (integer bounds), and adding 2^23 rounds half-to-even into
+// the low mantissa bits.
+__device__ __forceinline__ uint32_t quant_one(float x, float lo, float s, float y, float qmax)
+{
+    const float v = __builtin_amdgcn_fmed3f(div_rn(__fsub_rn(x, lo), s, y), 0.0f, qmax);
+    return __float_as_uint(__fadd_rn(v, 8388608.0f)) & 0xffu;
+}
+
+__device__ __forceinline__ void unpack8(uint4 w, float x[8])
+{
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        x[2 * k] = bf16_to_f32(ww[k] & 0xffffu);
+        x[2 * k + 1] = bf16_to_f32(ww[k] >> 16);
+    }
+}
+
+// 8 quantised values -> int8 bytes (2 dwords) or int4 nibbles (1 dword,
+// element 2i in the low nibble).
+__device__ __forceinline__ void pack8(const uint32_t q[8], uint32_t bits, uint32_t out[2])
+{
+    if (bits == 8) {
+        out[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+        out[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+    } else {
+        out[0] = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[0] |= q[k] << (4 * k);
+        out[1] = 0;
+    }
+}
+
+__device__ __forceinline__ void store_q8(uint8_t* pkt, uint32_t e, uint32_t bits, const uint32_t w[2])
+{
+    if (bits == 8) *reinterpret_cast<uint2*>(pkt + e) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(pkt + e / 2u) = w[0];
+}
+
+// Header {1, layer, kind, bits} closing the packet (the width is a multiple
+// of 16, so there is no further padding).
+__device__ __forceinline__ void store_header(const CodecBatch& b, uint8_t* pkt, uint32_t kind)
+{
+    *reinterpret_cast<uint4*>(pkt + b.qbytes + 2 * b.sbytes) = make_uint4(1u, b.layer, kind, b.bits);
+}
+
+// K: eight lanes per (token group of 64, 8 consecutive columns), each lane 8
+// tokens held in registers; the column min / max is reduced across the eight
+// lanes, so the slot is read once.  Grid (x, K record).
+__global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
+{
+    const uint32_t r = blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
-    if (idx >= hd) return;  // 2 groups * hd/2 column pairs
-    const uint32_t grp = idx / (hd / 2u);
-    const uint32_t col = (idx % (hd / 2u)) * 2u;
-    const float qmax = float((1u << b.bits) - 1u);
+    const uint32_t nch = hd / 8u;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    // Whole 8-lane groups take the same branch (shuffle partners stay active).
+    if (idx >= 2u * nch * 8u) return;
     const int64_t sid = b.slots[r];
     if (sid < 0 || sid >= b.nslots) return;
+    const uint32_t l8 = idx & 7u, cg = idx >> 3;
+    const uint32_t g = cg >= nch ? 1u : 0u;
+    const uint32_t col = (cg - g * nch) * 8u;
+    const float qmax = float((1u << b.bits) - 1u);
     const uint8_t* slot = b.cache[0] + uint64_t(sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
-    float lo0 = INFINITY, lo1 = INFINITY, hi0 = -INFINITY, hi1 = -INFINITY;
-    for (uint32_t tt = 0; tt < 64u; ++tt) {
-        const uint32_t t = grp * 64u + tt;
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(slot + (uint64_t(t) * hd + col) * 2u);
-        const float x0 = bf16_to_f32(w & 0xffffu), x1 = bf16_to_f32(w >> 16);
-        lo0 = fminf(lo0, x0); hi0 = fmaxf(hi0, x0);
-        lo1 = fminf(lo1, x1); hi1 = fmaxf(hi1, x1);
-    }
-    const float s0 = quant_scale(lo0, hi0, qmax), s1 = quant_scale(lo1, hi1, qmax);
-    const uint32_t p = grp * hd + col;
-    float* scale = reinterpret_cast<float*>(pkt + b.qbytes);
-    float* low = reinterpret_cast<float*>(pkt + b.qbytes + b.sbytes);
-    scale[p] = s0; scale[p + 1] = s1;
-    low[p] = lo0; low[p + 1] = lo1;
-    for (uint32_t tt = 0; tt < 64u; ++tt) {
-        const uint32_t t = grp * 64u + tt;
-        const uint64_t e = uint64_t(t) * hd + col;
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(slot + e * 2u);
-        const uint32_t q0 = quant_one(bf16_to_f32(w & 0xffffu), lo0, s0, qmax);
-        const uint32_t q1 = quant_one(bf16_to_f32(w >> 16), lo1, s1, qmax);
-        if (b.bits == 8)
-            *reinterpret_cast<uint16_t*>(pkt + e) = uint16_t(q0 | (q1 << 8));
-        else
-            pkt[e / 2] = uint8_t(q0 | (q1 << 4));
-    }
-}
+    if (idx == 0) store_header(b, pkt, 0u);
 
-// V: one thread per (token, head, dim group of 64).
-__global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b, uint32_t rec0, uint32_t blocks_per_rec)
-{
-    const uint32_t r = rec0 + blockIdx.x / blocks_per_rec;
-    const uint32_t idx = (blockIdx.x % blocks_per_rec) * 256u + threadIdx.x;
-    const uint32_t ng = b.dim / 64u;
-    const uint32_t hd = b.heads * b.dim;
-    if (idx >= 128u * b.heads * ng) return;
-    const uint32_t t = idx / (b.heads * ng);
-    const uint32_t hh = (idx / ng) % b.heads;
-    const uint32_t dg = idx % ng;
-    const float qmax = float((1u << b.bits) - 1u);
-    const int64_t sid = b.slots[r];
-    if (sid < 0 || sid >= b.nslots) return;
-    const uint8_t* slot = b.cache[1] + uint64_t(sid) * b.slot_bytes;
-    uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
-    const uint64_t e0 = uint64_t(t) * hd + uint64_t(hh) * b.dim + dg * 64u;
-    const uint4* src = reinterpret_cast<const uint4*>(slot + e0 * 2u);
-    uint32_t raw[32];
+    const uint32_t t0 = g * 64u + l8 * 8u;
+    uint4 raw[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+        raw[tt] = *reinterpret_cast<const uint4*>(slot + (uint64_t(t0 + tt) * hd + col) * 2u);
+    float lo[8], hi[8];
+    {
+        float x[8];
+        unpack8(raw[0], x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { lo[k] = x[k]; hi[k] = x[k]; }
+    }
+#pragma unroll
+    for (int tt = 1; tt < 8; ++tt) {
+        float x[8];
+        unpack8(raw[tt], x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { lo[k] = fminf(lo[k], x[k]); hi[k] = fmaxf(hi[k], x[k]); }
+    }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            lo[k] = fminf(lo[k], __shfl_xor(lo[k], m));
+            hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], m));
+        }
+    float sc[8], rc[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const uint4 v = src[k];
-        raw[4 * k] = v.x; raw[4 * k + 1] = v.y; raw[4 * k + 2] = v.z; raw[4 * k + 3] = v.w;
+        sc[k] = quant_scale(lo[k], hi[k], qmax);
+        rc[k] = recip_rn(sc[k]);
     }
-    float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const float a = bf16_to_f32(raw[k] & 0xffffu), c = bf16_to_f32(raw[k] >> 16);
-        lo = fminf(lo, fminf(a, c));
-        hi = fmaxf(hi, fmaxf(a, c));
+    if (l8 == 0) {
+        const uint32_t p = g * hd + col;
+        float4* sp = reinterpret_cast<float4*>(pkt + b.qbytes) + p / 4u;
+        float4* lp = reinterpret_cast<float4*>(pkt + b.qbytes + b.sbytes) + p / 4u;
+        sp[0] = make_float4(sc[0], sc[1], sc[2], sc[3]); sp[1] = make_float4(sc[4], sc[5], sc[6], sc[7]);
+        lp[0] = make_float4(lo[0], lo[1], lo[2], lo[3]); lp[1] = make_float4(lo[4], lo[5], lo[6], lo[7]);
     }
-    const float s = quant_scale(lo, hi, qmax);
-    const uint32_t p = idx;  // (t, h, dg) row-major == idx
-    reinterpret_cast<float*>(pkt + b.qbytes)[p] = s;
-    reinterpret_cast<float*>(pkt + b.qbytes + b.sbytes)[p] = lo;
-    uint32_t qw[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) qw[k] = 0;
+    for (int tt = 0; tt < 8; ++tt) {
+        float x[8];
+        unpack8(raw[tt], x);
+        uint32_t q[8], w[2];
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const uint32_t q0 = quant_one(bf16_to_f32(raw[k] & 0xffffu), lo, s, qmax);
-        const uint32_t q1 = quant_one(bf16_to_f32(raw[k] >> 16), lo, s, qmax);
-        if (b.bits == 8) {
-            // elements 2k, 2k+1 -> bytes 2k, 2k+1
-            qw[k >> 1] |= (q0 | (q1 << 8)) << (16 * (k & 1));
-        } else {
-            // byte k = q[2k] | q[2k+1] << 4
-            qw[k >> 2] |= (q0 | (q1 << 4)) << (8 * (k & 3));
-        }
-    }
-    if (b.bits == 8) {
-        uint4* dst = reinterpret_cast<uint4*>(pkt + e0);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) dst[k] = make_uint4(qw[4 * k], qw[4 * k + 1], qw[4 * k + 2], qw[4 * k + 3]);
-    } else {
-        uint4* dst = reinterpret_cast<uint4*>(pkt + e0 / 2);
-#pragma unroll
-        for (int k = 0; k < 2; ++k) dst[k] = make_uint4(qw[4 * k], qw[4 * k + 1], qw[4 * k + 2], qw[4 * k + 3]);
+        for (int k = 0; k < 8; ++k) q[k] = quant_one(x[k], lo[k], sc[k], rc[k], qmax);
+        pack8(q, b.bits, w);
+        store_q8(pkt, (t0 + tt) * hd + col, b.bits, w);
     }
 }
 
-// Header {1, layer, kind, bits} and the zero pad of every packet.
-__global__ void packet_tail_kernel(CodecBatch b)
+// V: eight lanes per (token, head, dim group of 64), 8 elements each; the
+// group's min / max is reduced across the eight lanes.  Grid (x, V record).
+__global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b)
 {
-    const uint32_t r = blockIdx.x;
+    const uint32_t r = b.n_k + blockIdx.y;
+    const uint32_t hd = b.heads * b.dim;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t ngroups = 2u * hd;  // 128 * hd / 64
+    // Whole 8-lane groups take the same branch, so the shuffles below see
+    // only active partners.
+    if (idx >= ngroups * 8u) return;
+    const int64_t sid = b.slots[r];
+    if (sid < 0 || sid >= b.nslots) return;
+    const uint32_t gi = idx >> 3, l8 = idx & 7u;
+    const float qmax = float((1u << b.bits) - 1u);
+    const uint8_t* slot = b.cache[1] + uint64_t(sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
-    const uint64_t h0 = b.qbytes + 2 * b.sbytes;
-    const uint32_t kind = r < b.n_k ? 0u : 1u;
-    for (uint64_t i = h0 + threadIdx.x; i < b.width; i += blockDim.x) {
-        const uint64_t o = i - h0;
-        uint32_t word = 0;
-        if (o < 16) {
-            const uint32_t f = uint32_t(o / 4);
-            word = f == 0 ? 1u : f == 1 ? b.layer : f == 2 ? kind : b.bits;
-        }
-        pkt[i] = o < 16 ? uint8_t(word >> (8 * (o & 3))) : 0;
+    if (idx == 0) store_header(b, pkt, 1u);
+    const uint32_t e = gi * 64u + l8 * 8u;
+    float x[8];
+    unpack8(*reinterpret_cast<const uint4*>(slot + uint64_t(e) * 2u), x);
+    float lo = x[0], hi = x[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) { lo = fminf(lo, x[k]); hi = fmaxf(hi, x[k]); }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, m));
+        hi = fmaxf(hi, __shfl_xor(hi, m));
     }
+    const float s = quant_scale(lo, hi, qmax);
+    const float y = recip_rn(s);
+    if (l8 == 0) {
+        reinterpret_cast<float*>(pkt + b.qbytes)[gi] = s;
+        reinterpret_cast<float*>(pkt + b.qbytes + b.sbytes)[gi] = lo;
+    }
+    uint32_t q[8], w[2];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = quant_one(x[k], lo, s, y, qmax);
+    pack8(q, b.bits, w);
+    store_q8(pkt, e, b.bits, w);
 }
 
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b)
 {
-    const uint32_t total8 = 128u * b.heads * b.dim / 8u;
-    const uint32_t gpr = (total8 + 255u) / 256u;
-    hipLaunchKernelGGL(dequant_scatter_kernel, dim3(b.nrec * gpr), dim3(256), 0, stream, b, gpr);
+    const uint32_t per_rec = 128u * b.heads * b.dim / 16u;
+    hipLaunchKernelGGL(dequant_scatter_kernel, dim3((per_rec + 255u) / 256u, b.nrec), dim3(256), 0, stream, b);
     return hipGetLastError();
 }
 
@@ -228,15 +300,10 @@ hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b)
 {
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nv = b.nrec - b.n_k;
-    if (b.n_k) {
-        const uint32_t bpr = (hd + 255u) / 256u;
-        hipLaunchKernelGGL(quant_k_kernel, dim3(b.n_k * bpr), dim3(256), 0, stream, b, 0u, bpr);
-    }
-    if (nv) {
-        const uint32_t bpr = (128u * b.heads * (b.dim / 64u) + 255u) / 256u;
-        hipLaunchKernelGGL(quant_v_kernel, dim3(nv * bpr), dim3(256), 0, stream, b, b.n_k, bpr);
-    }
-    hipLaunchKernelGGL(packet_tail_kernel, dim3(b.nrec), dim3(64), 0, stream, b);
+    if (b.n_k)
+        hipLaunchKernelGGL(quant_k_kernel, dim3((2u * hd + 255u) / 256u, b.n_k), dim3(256), 0, stream, b);
+    if (nv)
+        hipLaunchKernelGGL(quant_v_kernel, dim3((16u * hd + 255u) / 256u, nv), dim3(256), 0, stream, b);
     return hipGetLastError();
 }
 
