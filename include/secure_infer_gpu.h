@@ -209,6 +209,58 @@ int secure_infer_recovery_wait_layer_authentication(uint32_t layer);
 int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event,
                                       const uint32_t* fail_count);
 
+/* ------------------------------------------------------------------ */
+/* 4. Host transfer runtime: host AES-GCM, pinned ring, copy streams.     */
+/*                                                                        */
+/* The reference turns every intercepted aclrtMemcpyAsync of a registered */
+/* host range into one record (secure_infer.cpp:7729-8571).  ROCm has     */
+/* nothing to interpose, so the maintainer replaces each swap_blocks call */
+/* site with the explicit calls below; `mapping` is the swap_blocks       */
+/* mapping, n int64 pairs (source block, destination block) in host       */
+/* memory.  Host blocks are `host_block_bytes` apart from `host_base`:    */
+/* bf16 KV blocks [128, heads, head_dim], or codec packets (rows of a     */
+/* packet array, at least secure_infer_codec_width bytes).  AADs are      */
+/* built from the registered host ranges (secure_infer_build_gcm_aad).    */
+
+/* H2D reload of n blocks of one (layer, kind): host OpenSSL AES-128-GCM on
+ * the library's worker pool into a pinned ring slot (inline_h2d_encrypt_commit,
+ * secure_infer.cpp:6486-6550; slot ring :5174-5229, :5905-6059), DMA on the
+ * library's copy stream, then the fused verify + decrypt (+ dequantise) +
+ * paged scatter on `stream` once the copy has landed.  Returns when the work
+ * is queued; a ring slot is reused only after its kernel completed.  Inside
+ * secure_infer_h2d_layer_group_begin/end, the layer is registered for
+ * secure_infer_recovery_wait_layer_authentication (needs fail_count, a device
+ * u32 the caller zeroes per layer). */
+int secure_infer_h2d_swap(hipStream_t stream, si_session* session, const void* host_base,
+                          uint64_t host_block_bytes, void* dev_cache, uint64_t slot_bytes,
+                          uint64_t nslots, const int64_t* mapping, uint32_t n, uint32_t kind,
+                          uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim,
+                          uint32_t* fail_count);
+
+/* D2H batch / group API (same names, thread-local contexts and returns as
+ * secure_infer.cpp:2707-2970): batch_begin returns 1 (-1 when nested),
+ * group_begin 1 (-1 without a batch or inside a group), group_end and
+ * batch_device_barrier 0, batch_end 0 when every record of the batch
+ * authenticated on the host and -1 otherwise (failed records are zeroed). */
+int secure_infer_d2h_batch_begin(size_t expected_tasks);
+int secure_infer_d2h_group_begin(size_t expected_tasks);
+int secure_infer_d2h_group_end(void);
+int secure_infer_d2h_batch_device_barrier(void);
+int secure_infer_d2h_batch_end(void);
+
+/* Inside an open D2H group: gather (+ quantise) and seal n device blocks of
+ * one (layer, kind) on `stream` (the hook's D2H branch, secure_infer.cpp:
+ * 8076-8562, with gcm_encrypt_tag, ghash.aicpu:656-699), copy the records to
+ * pinned memory on the library's D2H stream; at group end the worker pool
+ * authenticates and decrypts each into host_base + block*host_block_bytes
+ * (d2h_host_decrypt_one, secure_infer.cpp:2470-2547).  mapping pairs are
+ * (device slot, host block). */
+int secure_infer_d2h_swap(hipStream_t stream, si_session* session, const void* dev_cache,
+                          uint64_t slot_bytes, uint64_t nslots, void* host_base,
+                          uint64_t host_block_bytes, const int64_t* mapping, uint32_t n,
+                          uint32_t kind, uint32_t layer, uint32_t codec_bits, uint32_t heads,
+                          uint32_t head_dim);
+
 /* Library build / device information. */
 const char* secure_infer_gpu_version(void);
 /* Tuning: minimum rows (blocks per thread) of one workgroup's chunk of a

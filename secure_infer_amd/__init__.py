@@ -6,7 +6,7 @@ tensors.  See ``secure_infer_amd.gcm``.
 """
 from .gcm import (  # noqa: F401
     AAD_BYTES, SI_CODEC_INT4, SI_CODEC_INT8, SI_CODEC_NONE, GcmSession, LayerShape,
-    NativeTransfer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
+    D2HTransfer, NativeTransfer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
     derive_transfer_iv, gcm_decrypt_verify, gcm_encrypt_tag, gcm_verify_only, gcm_verify_xor,
     iv_words, keystream, new_transfer_ticket, register_host_range, replay_reserve,
     set_chunk_rows, wire_stride, wire_tag_offset)

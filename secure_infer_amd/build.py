@@ -11,7 +11,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "_lib" / "libsecure_infer.so"
 
-SOURCES = ["si_gcm.hip", "si_codec.hip", "si_api.cpp"]
+SOURCES = ["si_gcm.hip", "si_codec.hip", "si_api.cpp", "si_host.cpp"]
+LIBS = ["-lcrypto", "-lpthread"]
 
 FLAGS = [
     "--offload-arch=gfx950",
@@ -38,7 +39,7 @@ def build(verbose: bool = False) -> Path:
     OUT.parent.mkdir(parents=True, exist_ok=True)
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [hipcc(), *FLAGS, "-I", str(ROOT / "include"), "-I", str(CSRC), "-o", str(tmp),
-           *[str(CSRC / s) for s in SOURCES]]
+           *[str(CSRC / s) for s in SOURCES], *LIBS]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "si_device.h"
+#include "si_host.h"
 #include "si_kernels.h"
 
 namespace {
@@ -367,9 +368,19 @@ std::unordered_set<uint64_t> g_replay;
 
 thread_local int64_t t_group_expected = -1;
 
+// Layer reloads issued through the host pipeline inside the calling thread's
+// open layer group; the group's end publishes one completion event per entry.
+struct GroupNote {
+    hipStream_t stream;
+    uint32_t layer;
+    uint32_t* fail_count;
+};
+thread_local std::vector<GroupNote> t_group_notes;
+
 struct TrackedLayer {
     hipEvent_t event;
     const uint32_t* fail_count;
+    bool owned;  // event created by the library: destroyed once observed
 };
 std::mutex g_track_lock;
 std::multimap<uint32_t, TrackedLayer> g_tracked;
@@ -772,6 +783,7 @@ int secure_infer_h2d_layer_group_begin(size_t expected)
 {
     if (t_group_expected >= 0) return -1;
     t_group_expected = int64_t(expected);
+    t_group_notes.clear();
     return 0;
 }
 
@@ -779,14 +791,32 @@ int secure_infer_h2d_layer_group_end(void)
 {
     if (t_group_expected < 0) return -1;
     t_group_expected = -1;
-    return 0;
+    int rc = 0;
+    std::vector<GroupNote> notes;
+    notes.swap(t_group_notes);
+    for (size_t i = 0; i < notes.size(); ++i) {
+        bool seen = false;
+        for (size_t j = 0; j < i; ++j)
+            seen |= notes[j].stream == notes[i].stream && notes[j].layer == notes[i].layer &&
+                    notes[j].fail_count == notes[i].fail_count;
+        if (seen) continue;
+        hipEvent_t ev = nullptr;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess ||
+            hipEventRecord(ev, notes[i].stream) != hipSuccess) {
+            rc = -1;
+            continue;
+        }
+        std::lock_guard<std::mutex> g(g_track_lock);
+        g_tracked.emplace(notes[i].layer, TrackedLayer{ev, notes[i].fail_count, true});
+    }
+    return rc;
 }
 
 int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event, const uint32_t* fail_count)
 {
     if (!event || !fail_count) return -1;
     std::lock_guard<std::mutex> g(g_track_lock);
-    g_tracked.emplace(layer, TrackedLayer{event, fail_count});
+    g_tracked.emplace(layer, TrackedLayer{event, fail_count, false});
     return 0;
 }
 
@@ -801,10 +831,13 @@ int secure_infer_recovery_wait_layer_authentication(uint32_t layer)
     }
     int rc = 0;
     for (const TrackedLayer& t : recs) {
-        if (hipEventSynchronize(t.event) != hipSuccess) return -1;
         uint32_t fails = 1;
-        if (hipMemcpy(&fails, t.fail_count, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
-        if (fails != 0) rc = -1;
+        if (hipEventSynchronize(t.event) != hipSuccess ||
+            hipMemcpy(&fails, t.fail_count, 4, hipMemcpyDeviceToHost) != hipSuccess)
+            rc = -1;
+        else if (fails != 0)
+            rc = -1;
+        if (t.owned) (void)hipEventDestroy(t.event);
     }
     return rc;
 }
@@ -817,3 +850,34 @@ int secure_infer_gpu_set_chunk_rows(int jmax)
 }
 
 }  // extern "C"
+
+namespace si_internal {
+
+SessionKeys session_keys(const si_session* s)
+{
+    SessionKeys k{};
+    memcpy(k.key, s->ctx->key, 16);
+    put_be32(k.salt, s->salt_word);
+    k.nonce = s->session_nonce;
+    k.max_record_bytes = s->max_record_bytes;
+    return k;
+}
+
+uint64_t reserve_tickets(uint32_t n)
+{
+    const uint64_t t = g_next_ticket.fetch_add(n, std::memory_order_relaxed);
+    if (t == 0 || t + n < t) {
+        fprintf(stderr, "[secure_infer] transfer ticket space exhausted\n");
+        abort();
+    }
+    return t;
+}
+
+bool group_note(hipStream_t stream, uint32_t layer, uint32_t* fail_count)
+{
+    if (t_group_expected < 0 || !fail_count) return false;
+    t_group_notes.push_back(GroupNote{stream, layer, fail_count});
+    return true;
+}
+
+}  // namespace si_internal

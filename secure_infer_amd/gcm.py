@@ -299,12 +299,20 @@ def set_chunk_rows(jmax: int) -> None:
 class NativeTransfer:
     """Per-layer authenticated reload driver (native_layerwise.py:85-130).
 
-    ``single_layer_kv_transfer((wire, mapping), (cache_k, cache_v))`` reloads
-    one layer: ``wire`` holds 2*N device wire records (K blocks then V blocks,
-    tickets ``ticket_base .. ticket_base+2N-1``), ``mapping`` is the [N, 2]
-    int64 (cpu_block, gpu_slot) table of vLLM's swap_blocks.  The whole layer
-    is one fused launch bracketed by the layer-group calls; the layer's
-    authentication result is then available through ``wait_layer``.
+    ``single_layer_kv_transfer((host, mapping), destination)`` has the
+    reference's contract: ``host`` = (cpu_k, cpu_v) host pools of this layer
+    ([num_cpu_blocks, 128, h, d] bf16, or packet arrays [num_cpu_blocks,
+    width] uint8 with a codec), ``mapping`` = the [N, 2] int64 (cpu_block,
+    gpu_slot) table of swap_blocks, ``destination`` = (cache_k, cache_v) device
+    paged caches [num_slots, 128, h, d].  Each kind is sealed on the host
+    (OpenSSL, worker pool), copied through the library's pinned ring on its
+    copy stream and verified / decrypted / scattered on the device; the call
+    returns once the work is queued.  The layer's authentication result is
+    available through ``wait_layer`` (wait_for_layer_load, connector.py:378-410).
+
+    ``single_layer_wire_transfer((wire, mapping), destination, ticket_base)``
+    reloads records already resident on the device (K blocks then V blocks,
+    tickets ticket_base .. ticket_base+2N-1).
     """
 
     def __init__(self, session: GcmSession, shape: LayerShape, stream=None):
@@ -316,7 +324,38 @@ class NativeTransfer:
         self._events = {}
         self._staging = None
 
-    def single_layer_kv_transfer(self, payload, destination, ticket_base: int) -> None:
+    def _fail_counter(self, device) -> torch.Tensor:
+        fail = torch.zeros(1, dtype=torch.int32, device=device)
+        self._fail[self.layer] = fail
+        return fail
+
+    def single_layer_kv_transfer(self, payload, destination) -> None:
+        host, mapping = payload
+        mapping = mapping.to(device="cpu", dtype=torch.int64).contiguous()
+        n = int(mapping.shape[0])
+        if n == 0:
+            self.layer += 1
+            return
+        fail = self._fail_counter(destination[0].device)
+        stream = _stream(self.stream)
+        _check(lib().secure_infer_h2d_layer_group_begin(2 * n), "h2d_layer_group_begin")
+        try:
+            for kind, (src, dst) in enumerate(zip(host, destination)):
+                if src.is_cuda or not src.is_contiguous():
+                    raise ValueError("host pools must be contiguous CPU tensors")
+                _dev(dst, "destination cache")
+                _check(lib().secure_infer_h2d_swap(
+                    stream, self.session._h, ct.c_void_p(src.data_ptr()),
+                    src[0].numel() * src.element_size(), ct.c_void_p(dst.data_ptr()),
+                    dst[0].numel() * dst.element_size(), dst.shape[0],
+                    ct.c_void_p(mapping.data_ptr()), n, kind, self.layer, self.shape.codec_bits,
+                    self.shape.heads, self.shape.head_dim, ct.c_void_p(fail.data_ptr())),
+                    "h2d_swap")
+        finally:
+            _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
+        self.layer += 1
+
+    def single_layer_wire_transfer(self, payload, destination, ticket_base: int) -> None:
         wire, mapping = payload
         cache_k, cache_v = destination
         n = int(mapping.shape[0])
@@ -329,7 +368,7 @@ class NativeTransfer:
             if self._staging is None or self._staging.numel() < need:
                 self._staging = torch.empty(need, dtype=torch.uint8, device=cache_k.device)
             staging = self._staging
-        fail = torch.zeros(1, dtype=torch.int32, device=cache_k.device)
+        fail = self._fail_counter(cache_k.device)
         _check(lib().secure_infer_h2d_layer_group_begin(2 * n), "h2d_layer_group_begin")
         try:
             self.session.reload_layer(wire, nbytes, 2 * n, n, cache_k, cache_v, slots,
@@ -341,7 +380,6 @@ class NativeTransfer:
             _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
         ev = torch.cuda.Event()
         ev.record(self.stream if self.stream is not None else torch.cuda.current_stream())
-        self._fail[self.layer] = fail
         self._events[self.layer] = ev
         _check(lib().secure_infer_recovery_track_layer(self.layer, ct.c_void_p(ev.cuda_event),
                                                        ct.c_void_p(fail.data_ptr())),
@@ -354,3 +392,59 @@ class NativeTransfer:
         self._fail.pop(layer, None)
         self._events.pop(layer, None)
         return rc
+
+
+class D2HTransfer:
+    """Sealed writeback of device KV blocks into host pools: the D2H branch of
+    _submit_transfer (npu_predict.py:874-916) with the same batch / group
+    brackets (secure_infer_d2h_batch_begin ... batch_end).
+
+    ``store(src_tensors, dst_tensors, src_to_dst)``: per layer, src = (k_cache,
+    v_cache) device caches, dst = (cpu_k, cpu_v) host pools, and src_to_dst the
+    [N, 2] int64 (gpu_slot, cpu_block) table.  Blocks are sealed on the device
+    (gather, codec quantise, AES-GCM), copied to pinned memory on the library's
+    D2H stream and authenticated + decrypted into the host pools by the worker
+    pool.  Raises if any record fails host verification (it is zeroed).
+    """
+
+    def __init__(self, session: GcmSession, shape: LayerShape, group_blocks: int = 16,
+                 stream=None):
+        self.session = session
+        self.shape = shape
+        self.group_blocks = max(1, int(group_blocks))
+        self.stream = stream
+
+    def store(self, src_tensors, dst_tensors, src_to_dst, layers=None) -> None:
+        mapping = src_to_dst.to(device="cpu", dtype=torch.int64).contiguous()
+        n = int(mapping.shape[0])
+        layers = list(range(len(src_tensors))) if layers is None else list(layers)
+        stream = _stream(self.stream)
+        L = lib()
+        if L.secure_infer_d2h_batch_begin(n * len(src_tensors) * 2) <= 0:
+            raise RuntimeError("d2h_batch_begin failed")
+        try:
+            for layer, src, dst in zip(layers, src_tensors, dst_tensors):
+                for kind in (0, 1):
+                    s_cache, d_pool = src[kind], dst[kind]
+                    _dev(s_cache, "source cache")
+                    if d_pool.is_cuda or not d_pool.is_contiguous():
+                        raise ValueError("host pools must be contiguous CPU tensors")
+                    for b0 in range(0, n, self.group_blocks):
+                        part = mapping[b0:b0 + self.group_blocks].contiguous()
+                        if L.secure_infer_d2h_group_begin(part.shape[0]) <= 0:
+                            raise RuntimeError("d2h_group_begin failed")
+                        try:
+                            _check(L.secure_infer_d2h_swap(
+                                stream, self.session._h, ct.c_void_p(s_cache.data_ptr()),
+                                s_cache[0].numel() * s_cache.element_size(), s_cache.shape[0],
+                                ct.c_void_p(d_pool.data_ptr()), d_pool[0].numel() * d_pool.element_size(),
+                                ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer,
+                                self.shape.codec_bits, self.shape.heads, self.shape.head_dim),
+                                "d2h_swap")
+                        finally:
+                            _check(L.secure_infer_d2h_group_end(), "d2h_group_end")
+            _check(L.secure_infer_d2h_batch_device_barrier(), "d2h_batch_device_barrier")
+        finally:
+            rc = L.secure_infer_d2h_batch_end()
+        if rc != 0:
+            raise RuntimeError("d2h batch: host authentication failed")

@@ -272,7 +272,7 @@ def test_native_transfer_wait_layer():
                             [0] * nb + [1] * nb, layer, [10, 11, 12] * 2, t0)
         if layer == 1:
             wire[W.align32(shape.record_bytes)] ^= 1  # tag of record 0
-        nt.single_layer_kv_transfer((dev(wire), mapping), (ck, cv), ticket_base=t0)
+        nt.single_layer_wire_transfer((dev(wire), mapping), (ck, cv), ticket_base=t0)
         tickets.append(blocks)
     assert nt.wait_layer(0) == 0
     assert nt.wait_layer(1) == -1
