@@ -132,6 +132,66 @@ def cpu_baseline(op: str, wire_host: np.ndarray, stride: int, nbytes: int, nrec:
                 us_per_layer=round(med * 1e6, 1), statuses_match_gpu=ok, matches_gpu=bool(same))
 
 
+def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer, steps, truth):
+    """The same layers through the host-memory path: reload = host OpenSSL seal
+    into the pinned ring, H2D on the library's copy stream, fused kernel;
+    writeback = fused kernel, D2H, host authentication into host pools.  Wall
+    time of whole steps after one warm-up step (PCIe included; never `value`)."""
+    L, H, D, NB, bits = cfg["layers"], cfg["heads"], cfg["dim"], cfg["blocks"], cfg["bits"]
+    shape = si.LayerShape(H, D, bits)
+    dev = cache.device
+    mapping_rl = [torch.stack([torch.arange(NB), slots[l].cpu()], 1).contiguous() for l in range(L)]
+    if bits == 0:
+        pool = lambda: torch.zeros((NB, 128, H, D), dtype=torch.bfloat16)
+    else:
+        pool = lambda: torch.zeros((NB, nbytes), dtype=torch.uint8)
+    hosts = [(pool(), pool()) for _ in range(L)]
+    si.clear_host_ranges()
+    for l in range(L):
+        si.register_host_range(hosts[l][0], l, 0)
+        si.register_host_range(hosts[l][1], l, 1)
+    d2h = si.D2HTransfer(sess, shape, group_blocks=NB)
+    wb_map = [torch.stack([slots[l].cpu(), torch.arange(NB)], 1).contiguous() for l in range(L)]
+    # host pools hold what a writeback produced (bf16 blocks or codec packets)
+    for l in range(L):
+        d2h.store([(cache[l, 0], cache[l, 1])], [hosts[l]], wb_map[l], layers=[l])
+    out = {"host_threads": int(si._lib.load().secure_infer_host_threads())}
+    if op == "reload":
+        cache.zero_()
+        nt = si.NativeTransfer(sess, shape)
+
+        def step():
+            nt.layer = 0
+            for l in range(L):
+                nt.single_layer_kv_transfer((hosts[l], mapping_rl[l]), (cache[l, 0], cache[l, 1]))
+            return all(nt.wait_layer(l) == 0 for l in range(L))
+        ok = step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ok &= step()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        if truth is not None:
+            got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
+            ok &= bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
+        what = "host OpenSSL seal + pinned ring + H2D (copy stream) + fused verify/decrypt/scatter"
+    else:
+        ok = True
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            for l in range(L):
+                d2h.store([(cache[l, 0], cache[l, 1])], [hosts[l]], wb_map[l], layers=[l])
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        what = "fused gather/quantise/seal + D2H + host OpenSSL authenticate/decrypt into host pools"
+    si.clear_host_ranges()
+    out.update({"us_per_layer": round(dt * 1e6 / L, 1), "GB_s": round(algo_layer * L / dt / 1e9, 2),
+                "steps": steps, "ok": bool(ok), "path": what})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +201,8 @@ def main():
     ap.add_argument("--chunk-rows", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--e2e-steps", type=int, default=3,
+                    help="steps of the host-memory path (host seal + pinned ring + PCIe); 0 = skip")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC byte calibration)")
     args = ap.parse_args()
@@ -312,6 +374,9 @@ def main():
             wh.reshape(nrec, stride)[:, :tag_off + 16] = 0  # the host recomputes ciphertext and tags
         res["cpu_baseline"] = cpu_baseline(op, wh, stride, nbytes, nrec, n_k, key, ivs, H, D, bits, layer,
                                            args.cpu_budget, algo_layer, planes, gw)
+    if args.e2e_steps > 0:
+        res["end_to_end"] = end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer,
+                                       args.e2e_steps, truth if (op == "reload" and bits == 0) else None)
     print(json.dumps(res), flush=True)
 
 

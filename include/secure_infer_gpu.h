@@ -237,6 +237,11 @@ int secure_infer_h2d_swap(hipStream_t stream, si_session* session, const void* h
                           uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim,
                           uint32_t* fail_count);
 
+/* Threads of the host crypto pool (the calling thread included): the CPUs of
+ * the process affinity mask, or SECURE_INFER_HOST_THREADS.  No reference
+ * counterpart (its pools are sized by PIPE_D2H_CPU_WORKERS, :2568-2629). */
+int secure_infer_host_threads(void);
+
 /* D2H batch / group API (same names, thread-local contexts and returns as
  * secure_infer.cpp:2707-2970): batch_begin returns 1 (-1 when nested),
  * group_begin 1 (-1 without a batch or inside a group), group_end and

@@ -63,6 +63,7 @@ SIGNATURES = {
     "secure_infer_h2d_layer_group_end": ([], _i),
     "secure_infer_recovery_wait_layer_authentication": ([_u32], _i),
     "secure_infer_recovery_track_layer": ([_u32, _v, _v], _i),
+    "secure_infer_host_threads": ([], _i),
     "secure_infer_h2d_swap": ([_v, _v, _v, _u64, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32, _u32,
                                _u32, _v], _i),
     "secure_infer_d2h_batch_begin": ([_sz], _i),

@@ -19,6 +19,7 @@
 #include "si_host.h"
 
 #include <openssl/evp.h>
+#include <sched.h>
 
 #include <algorithm>
 #include <atomic>
@@ -90,7 +91,11 @@ public:
 private:
     Pool()
     {
+        // CPUs this process may run on (the affinity mask, not the machine).
         unsigned n = std::thread::hardware_concurrency();
+        cpu_set_t set;
+        CPU_ZERO(&set);
+        if (sched_getaffinity(0, sizeof(set), &set) == 0) n = unsigned(CPU_COUNT(&set));
         if (const char* e = std::getenv("SECURE_INFER_HOST_THREADS")) n = unsigned(std::atoi(e));
         if (n == 0) n = 1;
         if (n > 64) n = 64;
@@ -111,6 +116,10 @@ private:
         }
     }
 
+public:
+    size_t threads() const { return threads_.size() + 1; }
+
+private:
     std::vector<std::thread> threads_;
     std::deque<std::function<void()>> q_;
     std::mutex m_;
@@ -349,6 +358,8 @@ void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
 }  // namespace
 
 extern "C" {
+
+int secure_infer_host_threads(void) { return int(Pool::get().threads()); }
 
 int secure_infer_h2d_swap(hipStream_t stream, si_session* s, const void* host_base,
                           uint64_t host_block_bytes, void* dev_cache, uint64_t slot_bytes,
