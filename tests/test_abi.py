@@ -80,3 +80,65 @@ def test_host_iv_and_aad_match_oracle():
     si.clear_host_ranges()
     with pytest.raises(ValueError):
         si.build_gcm_aad(blk.data_ptr(), 16, 3, 1)
+
+
+def test_error_returns_before_any_device_work():
+    """The reference's error contract (0 / -1, launcher.asc returns -1 on null or
+    zero arguments): invalid calls are rejected on the host, so they run here
+    without a GPU."""
+    import ctypes as ct
+
+    from secure_infer_amd import _lib
+    L = _lib.load()
+    v = ct.c_void_p
+    one = v(1)
+    # kernel mirrors: null pointers / zero sizes
+    assert L.secure_infer_gpu_gcm_decrypt_verify_aad_do(None, None, one, one, one, one, one, 16,
+                                                        0, 0, 0, 2, None, 0) == -1
+    assert L.secure_infer_gpu_gcm_decrypt_verify_aad_do(None, one, one, one, one, one, one, 0,
+                                                        0, 0, 0, 2, None, 0) == -1
+    assert L.secure_infer_gpu_gcm_decrypt_verify_aad_do(None, one, one, one, one, one, one, 16,
+                                                        0, 0, 0, 2, None, 64) == -1  # AAD length, no AAD
+    assert L.secure_infer_gpu_gcm_encrypt_tag_do(None, None, one, one, one, one, 16, 0, 0, 0, 2,
+                                                 None, 0) == -1
+    # sessions and layer entry points
+    out = v()
+    assert L.secure_infer_gpu_session_create(None, None, 0, 1024, ct.byref(out)) == -1
+    assert L.secure_infer_gpu_reload_layer(None, None, None) == -1
+    assert L.secure_infer_gpu_writeback_layer(None, None, None) == -1
+    desc = _lib.SiReloadDesc(nrec=0)
+    assert L.secure_infer_gpu_reload_layer(None, None, ct.byref(desc)) == -1
+    assert L.secure_infer_h2d_swap(None, None, one, 16, one, 16, 1, one, 0, 0, 0, 0, 0, 0, None) == -1
+    # D2H brackets without a batch (secure_infer.cpp:2707-2970 semantics)
+    assert L.secure_infer_d2h_group_begin(1) == -1
+    assert L.secure_infer_d2h_group_end() == 0
+    assert L.secure_infer_d2h_batch_device_barrier() == -1
+    assert L.secure_infer_d2h_batch_end() == 0
+    assert L.secure_infer_d2h_swap(None, None, one, 16, 1, one, 16, one, 1, 0, 0, 0, 0, 0) == -1
+    # layer-group nesting is thread-local
+    assert L.secure_infer_h2d_layer_group_begin(4) == 0
+    assert L.secure_infer_h2d_layer_group_begin(4) == -1
+    assert L.secure_infer_h2d_layer_group_end() == 0
+    assert L.secure_infer_h2d_layer_group_end() == -1
+    errors = []
+
+    def other_thread():
+        errors.append(L.secure_infer_h2d_layer_group_end())  # no group on this thread
+    import threading
+    assert L.secure_infer_h2d_layer_group_begin(2) == 0
+    t = threading.Thread(target=other_thread)
+    t.start()
+    t.join()
+    assert errors == [-1]
+    assert L.secure_infer_h2d_layer_group_end() == 0
+    # tracking and tuning
+    assert L.secure_infer_recovery_track_layer(0, None, one) == -1
+    assert L.secure_infer_gpu_set_chunk_rows(0) == -1
+    assert L.secure_infer_gpu_set_chunk_rows(257) == -1
+    assert L.secure_infer_gpu_set_chunk_rows(8) == 0
+    # IV / AAD builders
+    iv = (ct.c_uint8 * 16)()
+    assert L.secure_infer_derive_transfer_iv(iv, 0, 0, 0, iv) == -1          # ticket 0 is reserved
+    aad = (ct.c_uint8 * 64)()
+    assert L.secure_infer_build_gcm_aad(one, 16, 3, 1, 0, 0, aad) == 0      # direction must be 1 or 2
+    assert L.secure_infer_build_gcm_aad(one, 16, 1, 0, 0, 0, aad) == 0      # ticket 0
