@@ -268,11 +268,16 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* session, const void* d
 
 /* Library build / device information. */
 const char* secure_infer_gpu_version(void);
-/* Tuning: minimum rows (blocks per thread) of one workgroup's chunk of a
- * record, 1..256 (default 8); a launch splits each record into as many chunks
- * as fill two workgroups per CU.  No reference counterpart; used by the
- * benchmark sweep and the tests (small values force many chunks). */
+/* Tuning: minimum rows (of 256 blocks) of one workgroup's share of a layer's
+ * rows, 1..256 (default 3); a launch spreads the rows of all records over one
+ * workgroup per CU.  No reference counterpart; used by the benchmark sweep and
+ * the tests (small values force shares that straddle records). */
 int secure_infer_gpu_set_chunk_rows(int jmax);
+/* Tuning: cost, in rows, charged to a workgroup share that straddles two
+ * records when the launch lays out its shares, 0..256 (default 10); 0 lets
+ * shares straddle wherever a record ends inside one.  No reference
+ * counterpart; used by the tests to force straddling shares. */
+int secure_infer_gpu_set_straddle_rows(int rows);
 
 #ifdef __cplusplus
 }

@@ -9,4 +9,4 @@ from .gcm import (  # noqa: F401
     D2HTransfer, NativeTransfer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
     derive_transfer_iv, gcm_decrypt_verify, gcm_encrypt_tag, gcm_verify_only, gcm_verify_xor,
     iv_words, keystream, new_transfer_ticket, register_host_range, replay_reserve,
-    set_chunk_rows, wire_stride, wire_tag_offset)
+    set_chunk_rows, set_straddle_rows, wire_stride, wire_tag_offset)

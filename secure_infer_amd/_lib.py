@@ -75,6 +75,7 @@ SIGNATURES = {
                                _u32], _i),
     "secure_infer_gpu_version": ([], ct.c_char_p),
     "secure_infer_gpu_set_chunk_rows": ([_i], _i),
+    "secure_infer_gpu_set_straddle_rows": ([_i], _i),
 }
 
 _lib: ct.CDLL | None = None

@@ -204,30 +204,35 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
     Blk p{};
     p.b[0] = 0x80;  // H^0 = 1
     auto* pow = reinterpret_cast<uint8_t*>(c + 1);
-    Blk ht{}, ht2{};
     for (uint32_t e = 0; e < npow; ++e) {
         memcpy(pow + 16 * size_t(e), p.b, 16);
-        if (e == SI_T) ht = p;
-        if (e == 2 * SI_T) ht2 = p;
         p = mh(p);
     }
-    if (npow <= 2 * SI_T) {
+    // Fixed multipliers of the record kernel: H^T, H^2T, H^UT, H^2UT.
+    Blk ht{}, ht2{}, htu{}, htu2{};
+    {
         Blk q{};
         q.b[0] = 0x80;
-        for (int e = 1; e <= 2 * SI_T; ++e) {
+        for (int e = 1; e <= 2 * SI_U * SI_T; ++e) {
             q = mh(q);
             if (e == SI_T) ht = q;
+            if (e == 2 * SI_T) ht2 = q;
+            if (e == SI_U * SI_T) htu = q;
         }
-        ht2 = q;
+        htu2 = q;
     }
-    const FixedMul mt(ht), mt2(ht2);
-    for (int pos = 0; pos < 32; ++pos)
-        for (int v = 0; v < 16; ++v) {
-            const Blk& e = mt.t[pos][v];
-            c->gh4[pos * 16 + v] = make_uint4(le32(e.b), le32(e.b + 4), le32(e.b + 8), le32(e.b + 12));
-            const Blk& f = mt2.t[pos][v];
-            c->gh4b[pos * 16 + v] = make_uint4(le32(f.b), le32(f.b + 4), le32(f.b + 8), le32(f.b + 12));
-        }
+    auto put = [](uint4* dst, const Blk& m) {
+        const FixedMul mt(m);
+        for (int pos = 0; pos < 32; ++pos)
+            for (int v = 0; v < 16; ++v) {
+                const Blk& e = mt.t[pos][v];
+                dst[pos * 16 + v] = make_uint4(le32(e.b), le32(e.b + 4), le32(e.b + 8), le32(e.b + 12));
+            }
+    };
+    put(c->gh4, ht);
+    put(c->gh4b, ht2);
+    put(c->gh4u, htu);
+    put(c->gh4u2, htu2);
     auto out = std::make_unique<DevCtx>();
     if (hipMalloc(&out->dev, img.size()) != hipSuccess) return nullptr;
     if (hipMemcpy(out->dev, img.data(), img.size(), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
@@ -237,22 +242,27 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
     return out;
 }
 
-int g_min_rows = 8;
+int g_min_rows = 3;
+// Cost, in rows, of a share that straddles two records (its second set of
+// boundary rows, the second placement table and the two-product shares);
+// MI355X, bf16 Llama-3-8B layer: 37.8 / 36.6 / 34.2 / 36.2 / 37.2 us per
+// layer at 4 / 7 / 10 / 12 / 16.
+uint32_t g_straddle_rows = 10;
 
-// Workgroup slots of the GCM kernel on the current device: two per CU (its
+// Compute units of the current device (one record-kernel workgroup each: its
 // LDS use).
-uint32_t gcm_slots()
+uint32_t cu_count()
 {
     static int cus[64] = {0};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
     if (!cus[dev]) {
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             n = 256;
         cus[dev] = n;
     }
-    return uint32_t(2 * cus[dev]);
+    return uint32_t(cus[dev]);
 }
 
 si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
@@ -265,13 +275,54 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
     s.n = uint32_t((bytes + 15) / 16);
     const uint64_t m = uint64_t(s.a) + s.n + 1;
     s.rows = uint32_t((m + SI_T - 1) / SI_T);
-    // K chunks per record: as many as fill the slots once, none shorter than
-    // g_min_rows rows (K = 1 when the records alone fill the device).
-    uint64_t k = gcm_slots() / (nrec ? nrec : 1);
-    const uint64_t kmax = (uint64_t(s.rows) + uint64_t(g_min_rows) - 1) / uint64_t(g_min_rows);
-    if (k > kmax) k = kmax;
-    if (k < 1) k = 1;
-    s.k = uint32_t(k);
+    // W workgroups, one per CU, none with fewer than g_min_rows rows, and at
+    // least nrec of them (rounded to whole rounds of one per CU) so that no
+    // share spans more than R rows, i.e. two records at most.
+    const uint64_t G = uint64_t(nrec) * s.rows;
+    const uint64_t cus = cu_count();
+    uint64_t w = (G + uint64_t(g_min_rows) - 1) / uint64_t(g_min_rows);
+    if (w > cus) w = cus;
+    if (w < nrec) w = (uint64_t(nrec) + cus - 1) / cus * cus;
+    if (w > G) w = G;
+    s.nwg = uint32_t(w);
+    s.use_starts = 0;
+    if (w > 0 && w <= SI_MAX_WG) {
+        // Shares of at most T rows; a share that would end inside a record
+        // continues into the next one only if it still gains rows after
+        // paying the straddle cost Z (boundary rows, a second placement);
+        // T is the least that fits W shares.
+        const uint32_t R = s.rows, Z = g_straddle_rows;
+        auto lay = [&](uint32_t T, bool store) -> uint64_t {
+            uint64_t n = 0, r = 0, q = 0;
+            if (store) s.starts[0] = 0;
+            while (r < nrec) {
+                const uint64_t rem = R - q;
+                if (rem >= T) {
+                    q += T;
+                    if (q == R) { ++r; q = 0; }
+                } else if (T > Z + rem && r + 1 < nrec) {
+                    q = T - Z - rem;
+                    ++r;
+                } else {
+                    ++r;
+                    q = 0;
+                }
+                ++n;
+                if (store && n <= w) s.starts[n] = uint32_t(r * R + q);
+            }
+            return n;
+        };
+        uint32_t lo = uint32_t((G + w - 1) / w), hi = R;
+        if (lo > hi) lo = hi;
+        while (lo < hi) {
+            const uint32_t T = lo + (hi - lo) / 2;
+            if (lay(T, false) <= w) hi = T;
+            else lo = T + 1;
+        }
+        const uint64_t n = lay(lo, true);
+        for (uint64_t i = n + 1; i <= w; ++i) s.starts[i] = uint32_t(G);
+        s.use_starts = 1;
+    }
     return s;
 }
 
@@ -846,6 +897,13 @@ int secure_infer_gpu_set_chunk_rows(int jmax)
 {
     if (jmax < 1 || jmax > 256) return -1;
     g_min_rows = jmax;
+    return 0;
+}
+
+int secure_infer_gpu_set_straddle_rows(int rows)
+{
+    if (rows < 0 || rows > 256) return -1;
+    g_straddle_rows = uint32_t(rows);
     return 0;
 }
 

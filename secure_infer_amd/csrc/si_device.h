@@ -15,15 +15,19 @@
 //          wave64 lookup touches each of the 32 banks once per half-wave.  The
 //          address is produced by ONE v_perm_b32: byte1 <- state byte, byte0 <-
 //          the lane's copy offset.
-//   GHASH: 4-bit per-position tables of H^T and H^2T (T = threads per
-//          workgroup): position p (nibble p of the block, p = 0..31), value v:
-//          16 bytes at p*256 + v*16.  Y*H^T = XOR_p table[p][nibble_p(Y)].
+//   GHASH: 4-bit per-position tables of H^(UT), H^(2UT) (a unit's row
+//          step and row pair), H^T and H^2T (combining the units' partials);
+//          T = threads per unit = blocks per row, U = units per workgroup.
+//          Position p (nibble p of the block, p = 0..31), value v: 16 bytes
+//          at p*256 + v*16.  Y*H^e = XOR_p table[p][nibble_p(Y)].
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#define SI_T 256  // threads per workgroup of the GCM kernels
+#define SI_T 256            // threads per unit = blocks per row
+#define SI_U 3              // units per workgroup of the record kernel
+#define SI_NT (SI_T * SI_U) // threads per workgroup of the record kernel
 
 namespace si {
 
@@ -37,6 +41,8 @@ struct GcmCtx {
     uint32_t reserved[3];
     uint4 gh4[32 * 16];   // 4-bit tables of H^SI_T
     uint4 gh4b[32 * 16];  // 4-bit tables of H^(2*SI_T)
+    uint4 gh4u[32 * 16];  // 4-bit tables of H^(SI_U*SI_T)
+    uint4 gh4u2[32 * 16]; // 4-bit tables of H^(2*SI_U*SI_T)
     // followed by uint4 hpow[npow]: hpow[e] = H^e in memory byte order
 };
 
@@ -395,12 +401,16 @@ __device__ __forceinline__ void be_mulx(uint32_t a[4])
     a[0] = (a[0] >> 1) ^ ((0u - carry) & 0xe1000000u);
 }
 
-// z = x * y for per-lane x, y (memory byte order in and out).  Shoup's 4-bit
-// method with the lane's 16-entry table of multiples of y in LDS:
-// tbl + (v * stride + lane_slot) * 16 bytes, v = 0..15.
-__device__ __forceinline__ void gh_mul_generic(const uint32_t x_mem[4], const uint32_t y_mem[4],
-                                               uint4* tbl, uint32_t slot, uint32_t stride,
-                                               uint32_t z_mem[4])
+// z = x * y for per-lane x, y (memory byte order in and out), shared by three
+// threads: Shoup's 4-bit method with a per-lane table of the multiples v*y in
+// LDS.  Each thread writes its share of the table (entries v = c, c+3, ...
+// for c = 0..2; v = 0 is not stored: entry v >= 1 sits at
+// tbl[(v - 1) * stride + slot] and a shared zero word stands for v = 0), and
+// after a barrier each evaluates the nibbles j = c (mod 3) of x with its own
+// Horner chain (step x^12), then shifts by x^(4c).  XORing the three results
+// gives x * y; each chain is a third as long as one whole product's.
+__device__ __forceinline__ void gh_table_share(const uint32_t y_mem[4], uint32_t c, uint4* tbl,
+                                               uint32_t slot, uint32_t stride)
 {
     uint32_t m8[4] = {bswap32(y_mem[0]), bswap32(y_mem[1]), bswap32(y_mem[2]), bswap32(y_mem[3])};
     uint32_t m4[4] = {m8[0], m8[1], m8[2], m8[3]};
@@ -410,48 +420,75 @@ __device__ __forceinline__ void gh_mul_generic(const uint32_t x_mem[4], const ui
     uint32_t m1[4] = {m2[0], m2[1], m2[2], m2[3]};
     be_mulx(m1);
 #pragma unroll
-    for (uint32_t v = 0; v < 16; ++v) {
-        uint32_t e[4];
+    for (uint32_t i = 0; i < 6; ++i) {
+        const uint32_t v = c + 3u * i;
+        if (v != 0u && v < 16u) {
+            const uint32_t s8 = 0u - ((v >> 3) & 1u), s4 = 0u - ((v >> 2) & 1u);
+            const uint32_t s2 = 0u - ((v >> 1) & 1u), s1 = 0u - (v & 1u);
+            uint32_t e[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t t = 0;
-            if (v & 8u) t ^= m8[k];
-            if (v & 4u) t ^= m4[k];
-            if (v & 2u) t ^= m2[k];
-            if (v & 1u) t ^= m1[k];
-            e[k] = t;
+            for (int k = 0; k < 4; ++k) e[k] = (m8[k] & s8) ^ (m4[k] & s4) ^ (m2[k] & s2) ^ (m1[k] & s1);
+            tbl[(v - 1u) * stride + slot] = make_uint4(e[0], e[1], e[2], e[3]);
         }
-        tbl[v * stride + slot] = make_uint4(e[0], e[1], e[2], e[3]);
     }
-    const uint32_t xb[4] = {bswap32(x_mem[0]), bswap32(x_mem[1]), bswap32(x_mem[2]),
-                            bswap32(x_mem[3])};
-    // Horner over the nibbles of x from the last (x^124..x^127) to the first.
-    uint32_t a[4];
-    {
-        const uint4 t = tbl[(xb[3] & 0xfu) * stride + slot];
-        a[0] = t.x; a[1] = t.y; a[2] = t.z; a[3] = t.w;
+}
+
+// a <- a * x^S (big-endian words, S = 4 or 12): shift right by S and fold the
+// S bits that left x^127 back in, x^(128+i) = x^i (x^7 + x^2 + x + 1).
+template <int S>
+__device__ __forceinline__ void be_mulx_s(uint32_t a[4])
+{
+    static_assert(S == 4 || S == 12, "reduction fits the top word");
+    const uint32_t rem = a[3] & ((1u << S) - 1u);
+    a[3] = __builtin_amdgcn_alignbit(a[2], a[3], S);
+    a[2] = __builtin_amdgcn_alignbit(a[1], a[2], S);
+    a[1] = __builtin_amdgcn_alignbit(a[0], a[1], S);
+    const uint32_t red = (rem << (25 - S)) ^ xor3(rem << (30 - S), rem << (31 - S), rem << (32 - S));
+    a[0] = (a[0] >> S) ^ red;
+}
+
+// Part C of x * y (C < K) for NS independent products at once (their
+// chains interleave): z[s] = XOR_{j = C mod K} T_s[nibble j of x[s]] * x^(4j),
+// Horner over those nibbles with step x^(4K).  K = 1 is the whole product,
+// K = 3 a third of it (gh_table_share's layout: entry v >= 1 at
+// tbl[(v - 1) * stride + slot], `zero` for v = 0).
+template <int K, int C, int NS>
+__device__ __forceinline__ void gh_mul_part(const uint32_t (&x_mem)[NS][4], const uint4* const (&tbl)[NS],
+                                            const uint4* zero, uint32_t slot, uint32_t stride,
+                                            uint32_t (&z_mem)[NS][4])
+{
+    static_assert((K == 1 || K == 3) && C < K, "one or three parts");
+    constexpr int kTop = C + K * ((31 - C) / K);
+    uint32_t xb[NS][4], a[NS][4];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xb[s][k] = bswap32(x_mem[s][k]);
+    const auto entry = [&](int s, int j) -> const uint4* {
+        const uint32_t v = (xb[s][j >> 3] >> (28 - 4 * (j & 7))) & 0xfu;
+        return v ? tbl[s] + ((v - 1u) * stride + slot) : zero;
+    };
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const uint4 q = *entry(s, kTop);
+        a[s][0] = q.x; a[s][1] = q.y; a[s][2] = q.z; a[s][3] = q.w;
     }
 #pragma unroll
-    for (int j = 30; j >= 0; --j) {
-        const uint32_t nib = (xb[j >> 3] >> (28 - 4 * (j & 7))) & 0xfu;
-        // a <- a * x^4: shift right by 4 and fold the 4 bits that left x^127
-        // back in: x^(128+i) = x^i (x^7 + x^2 + x + 1), i.e. the 16-bit
-        // reduction value clmul(rem, 0x1c20) placed in the top half-word.
-        const uint32_t rem = a[3] & 0xfu;
-        a[3] = __builtin_amdgcn_alignbit(a[2], a[3], 4);
-        a[2] = __builtin_amdgcn_alignbit(a[1], a[2], 4);
-        a[1] = __builtin_amdgcn_alignbit(a[0], a[1], 4);
-        const uint32_t red = (rem << 21) ^ xor3(rem << 26, rem << 27, rem << 28);
-        const uint4 t = tbl[nib * stride + slot];
-        a[0] = xor3(a[0] >> 4, red, t.x);
-        a[1] ^= t.y;
-        a[2] ^= t.z;
-        a[3] ^= t.w;
+    for (int j = kTop - K; j >= C; j -= K) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const uint4 q = *entry(s, j);
+            be_mulx_s<4 * K>(a[s]);
+            a[s][0] ^= q.x; a[s][1] ^= q.y; a[s][2] ^= q.z; a[s][3] ^= q.w;
+        }
     }
-    z_mem[0] = bswap32(a[0]);
-    z_mem[1] = bswap32(a[1]);
-    z_mem[2] = bswap32(a[2]);
-    z_mem[3] = bswap32(a[3]);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+        for (int i = 0; i < C; ++i) be_mulx_s<4>(a[s]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) z_mem[s][k] = bswap32(a[s][k]);
+    }
 }
 
 // XOR-reduce four words across a wave64.

@@ -34,42 +34,76 @@ enum Mode : int {
     MODE_VERIFY_XOR = 3,  // verify + XOR with a given keystream
 };
 
+// Record buffers are device (global) memory.  The record views are rebuilt
+// from LDS words, which loses that fact; accessing them through generic
+// pointers would emit FLAT instructions, which also count on the LDS wait
+// counter and so force the LDS pipeline to drain behind every HBM access.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const T* p)
+{
+    return (const __attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gmem(T* p)
+{
+    return (__attribute__((address_space(1))) T*)p;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 gload4(const void* p)
+{
+    const u32x4 v = *gmem(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void gstore4(void* p, uint4 w)
+{
+    u32x4 v;
+    v.x = w.x; v.y = w.y; v.z = w.z; v.w = w.w;
+    *gmem(reinterpret_cast<u32x4*>(p)) = v;
+}
+
 template <bool kAligned>
 __device__ __forceinline__ void load_block(const uint8_t* p, uint32_t valid, uint32_t w[4])
 {
     if (kAligned && valid == 16u) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        const uint4 v = gload4(p);
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
         return;
     }
     w[0] = w[1] = w[2] = w[3] = 0;
-    for (uint32_t b = 0; b < valid; ++b) w[b >> 2] |= uint32_t(p[b]) << (8 * (b & 3));
+    const auto* g = gmem(p);
+    for (uint32_t b = 0; b < valid; ++b) w[b >> 2] |= uint32_t(g[b]) << (8 * (b & 3));
 }
 
 template <bool kAligned>
 __device__ __forceinline__ void store_block(uint8_t* p, uint32_t valid, const uint32_t w[4])
 {
     if (kAligned && valid == 16u) {
-        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+        gstore4(p, make_uint4(w[0], w[1], w[2], w[3]));
         return;
     }
-    for (uint32_t b = 0; b < valid; ++b) p[b] = uint8_t(w[b >> 2] >> (8 * (b & 3)));
+    auto* g = gmem(p);
+    for (uint32_t b = 0; b < valid; ++b) g[b] = uint8_t(w[b >> 2] >> (8 * (b & 3)));
 }
 
 __device__ __forceinline__ void zero_bytes(uint8_t* p, uint64_t bytes, uint32_t tid,
                                            uint32_t nthreads)
 {
     const bool aligned = (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+    auto* g = gmem(p);
     if (aligned) {
         const uint64_t full = bytes >> 4;
-        for (uint64_t i = tid; i < full; i += nthreads)
-            reinterpret_cast<uint4*>(p)[i] = make_uint4(0, 0, 0, 0);
-        for (uint64_t i = (full << 4) + tid; i < bytes; i += nthreads) p[i] = 0;
+        for (uint64_t i = tid; i < full; i += nthreads) gstore4(p + 16 * i, make_uint4(0, 0, 0, 0));
+        for (uint64_t i = (full << 4) + tid; i < bytes; i += nthreads) g[i] = 0;
     } else {
-        for (uint64_t i = tid; i < bytes; i += nthreads) p[i] = 0;
+        for (uint64_t i = tid; i < bytes; i += nthreads) g[i] = 0;
     }
 }
 
+// Everything the kernel body needs about one record (80 bytes, kept in LDS
+// so the batch's kernel arguments are dead after the set-up).
 struct RecView {
     const uint8_t* src;  // ciphertext (decrypt/verify) or plaintext (encrypt)
     uint8_t* dst;        // plaintext out (decrypt) or ciphertext out (encrypt)
@@ -77,9 +111,12 @@ struct RecView {
     uint8_t* tag;        // expected tag, or tag output (encrypt)
     uint32_t* status;
     const uint8_t* ks;   // keystream (verify_xor)
+    uint32_t* fail_count;
     uint32_t iv[4];
-    bool bad;            // block-table entry out of range: touch no cache memory
+    uint32_t bad;        // block-table entry out of range: the record fails
+    uint32_t skip;       // bad and no staging: touch no cache memory
 };
+static_assert(sizeof(RecView) == 80, "five 16-byte LDS words");
 
 __device__ __forceinline__ RecView view_of(const RecBatch& b, uint32_t r)
 {
@@ -92,13 +129,16 @@ __device__ __forceinline__ RecView view_of(const RecBatch& b, uint32_t r)
         v.status = b.status;
         v.ks = b.ks;
         v.iv[0] = b.iv[0]; v.iv[1] = b.iv[1]; v.iv[2] = b.iv[2]; v.iv[3] = b.iv[3];
-        v.bad = false;
+        v.fail_count = b.fail_count;
+        v.bad = v.skip = 0;
         return v;
     }
     uint8_t* wire = const_cast<uint8_t*>(b.wire) + uint64_t(r) * b.wire_stride;
     const uint32_t kind = r < b.n_k ? 0u : 1u;
     const int64_t sid = b.slots[r];
-    v.bad = sid < 0 || sid >= b.nslots;
+    v.bad = (sid < 0 || sid >= b.nslots) ? 1u : 0u;
+    v.skip = v.bad && !b.staging ? 1u : 0u;
+    v.fail_count = b.fail_count;
     uint8_t* slot = b.cache[kind] + uint64_t(v.bad ? 0 : sid) * b.slot_bytes;
     uint8_t* stage = b.staging ? b.staging + uint64_t(r) * b.staging_stride : nullptr;
     uint8_t* plain = stage ? stage : slot;
@@ -126,8 +166,6 @@ __device__ __forceinline__ RecView view_of(const RecBatch& b, uint32_t r)
     return v;
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 // Write-through (sc1) 16-byte store: agent-coherent once s_waitcnt drains it,
 // and measured faster than plain or non-temporal stores for this stream.
 __device__ __forceinline__ void st_wt(__amdgpu_buffer_rsrc_t rsrc, uint64_t k, uint4 v)
@@ -145,7 +183,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p)
 // One general row: any mix of AAD / ciphertext / length blocks, partial
 // blocks and unaligned buffers.  Used for the few rows at a record's ends.
 template <int kMode, bool kAligned, bool kWT>
-__device__ __forceinline__ void row_general(const RecBatch& batch, const Sched& sch, const RecView& v,
+__device__ __forceinline__ void row_general(const Sched& sch, const RecView& v,
                                             const uint32_t* aes, AesLane lane, const AesKeys& keys,
                                             uint32_t n0, uint32_t n1, uint32_t n2, int64_t i,
                                             uint32_t tail, uint32_t aad_tail, uint32_t y[4])
@@ -153,7 +191,7 @@ __device__ __forceinline__ void row_general(const RecBatch& batch, const Sched& 
     if (i < 0) return;
     uint32_t x[4];
     if (i >= int64_t(sch.a) && i < int64_t(sch.a) + int64_t(sch.n)) {
-        if (v.bad && !batch.staging) return;
+        if (v.skip) return;
         const uint64_t k = uint64_t(i - sch.a);
         const uint32_t valid = k == uint64_t(sch.n) - 1 ? tail : 16u;
         uint32_t in[4];
@@ -306,31 +344,33 @@ __device__ __forceinline__ void load_rows(const uint4* __restrict__ src, const u
 {
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-        in[r] = src[k[r]];
-        if (kMode == MODE_VERIFY_XOR) ksin[r] = ksrc[k[r]];
+        in[r] = gload4(src + k[r]);
+        if (kMode == MODE_VERIFY_XOR) ksin[r] = gload4(ksrc + k[r]);
     }
 }
 
-// Full-ciphertext rows [j0, j1) of this thread, two rows per step.  Ping-pong
-// buffers: the loads of the next step are issued before the current step's
-// keystreams, so HBM latency hides behind the AES work.
+// Full-ciphertext rows i in [i0, i1) of this thread's unit (block k = kb +
+// i*S, S = SI_U*SI_T), two rows per step.  Ping-pong buffers: the loads of
+// the next step are issued before the current step's keystreams, so HBM
+// latency hides behind the AES work.  Horner with gh = H^S, gh2 = H^2S.
 template <int kMode, bool kCached>
 __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, const uint4* gh2,
                                           const uint32_t* aes, AesLane lane, const AesKeys& keys,
                                           const CtrCache& cc, uint32_t n0, uint32_t n1, uint32_t n2,
-                                          uint64_t k0, uint32_t j0, uint32_t j1, uint32_t y[4])
+                                          uint64_t kb, uint32_t i0, uint32_t i1, uint32_t y[4])
 {
     constexpr int kP = 2;
+    constexpr uint64_t kS = uint64_t(SI_U) * SI_T;
     const uint4* __restrict__ src = reinterpret_cast<const uint4*>(v.src);
     const uint4* __restrict__ ksrc = reinterpret_cast<const uint4*>(v.ks);
     const __amdgpu_buffer_rsrc_t dst = rsrc_of(v.dst);
-    const uint32_t nsteps = (j1 - j0) / kP;
-    const uint32_t jend = j0 + nsteps * kP;
+    const uint32_t nsteps = (i1 - i0) / kP;
+    const uint32_t iend = i0 + nsteps * kP;
     if (nsteps) {
         auto rows_of = [&](uint32_t step, uint64_t (&k)[kP]) {
             const uint32_t s = step < nsteps ? step : nsteps - 1;  // clamped prefetch
 #pragma unroll
-            for (int r = 0; r < kP; ++r) k[r] = k0 + uint64_t(j0 + s * kP + r) * SI_T;
+            for (int r = 0; r < kP; ++r) k[r] = kb + uint64_t(i0 + s * kP + r) * kS;
         };
         // Encrypt folds each pair's ciphertext into GHASH during the next
         // pair, so its first pair only makes keystreams.
@@ -340,7 +380,7 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
         if (kDelay) {
             uint64_t k2[kP];
             rows_of(0, k2);
-            const uint4 p0 = src[k2[0]], p1 = src[k2[1]];
+            const uint4 p0 = gload4(src + k2[0]), p1 = gload4(src + k2[1]);
             uint32_t s0[4], s1[4];
             keystream_block<true>(aes, lane, keys, cc, n0, n1, n2, v.iv[3] + uint32_t(k2[0]), s0);
             keystream_block<true>(aes, lane, keys, cc, n0, n1, n2, v.iv[3] + uint32_t(k2[1]), s1);
@@ -351,21 +391,30 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
             st0 = 1;
         }
         if (st0 < nsteps) {
-            uint64_t ka[kP], kb[kP];
+            uint64_t ka[kP], kb2[kP];
             uint4 a[kP], qa[kP], b[kP], qb[kP];
             rows_of(st0, ka);
             load_rows<kMode, kP>(src, ksrc, ka, a, qa);
             for (uint32_t st = st0; st < nsteps; st += 2) {
-                rows_of(st + 1, kb);
-                load_rows<kMode, kP>(src, ksrc, kb, b, qb);
+                // Waves that are ahead yield issue priority to the ones
+                // behind (the arbiter otherwise favours the oldest wave), so
+                // the units of a workgroup finish their rows together.
+                const uint32_t left = nsteps - st;
+                if (left >= 6) __builtin_amdgcn_s_setprio(3);
+                else if (left >= 4) __builtin_amdgcn_s_setprio(2);
+                else if (left >= 2) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+                rows_of(st + 1, kb2);
+                load_rows<kMode, kP>(src, ksrc, kb2, b, qb);
                 __builtin_amdgcn_sched_barrier(0);
                 rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, ka, a, qa, y, pend);
                 if (st + 1 >= nsteps) break;
                 rows_of(st + 2, ka);
                 load_rows<kMode, kP>(src, ksrc, ka, a, qa);
                 __builtin_amdgcn_sched_barrier(0);
-                rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, kb, b, qb, y, pend);
+                rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, kb2, b, qb, y, pend);
             }
+            __builtin_amdgcn_s_setprio(0);
         }
         if (kDelay) {
             uint32_t u[4], w4[4];
@@ -375,8 +424,8 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
             for (int w = 0; w < 4; ++w) y[w] = xor3(u[w], w4[w], pend.b[w]);
         }
     }
-    for (uint32_t j = jend; j < j1; ++j) {
-        uint64_t k1[1] = {k0 + uint64_t(j) * SI_T};
+    for (uint32_t i = iend; i < i1; ++i) {
+        uint64_t k1[1] = {kb + uint64_t(i) * kS};
         uint4 a1[1], q1[1];
         load_rows<kMode, 1>(src, ksrc, k1, a1, q1);
         PendPair none;
@@ -384,27 +433,28 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
     }
 }
 
-// Rows [q0, q1) of one record: Horner with H^T over the thread's blocks into
-// y.  Row q holds blocks m - (R - q)*T + t (row R-1 ends with the length
-// block).  The owner of the length block also returns the tag mask E_K(J0).
+// Rows [qa, qb) of one record, shared by the workgroup's SI_U units: unit u
+// takes the segment rows j = u + SI_U*i, i = 0..nu-1, and runs Horner with
+// H^(SI_U*T) over them into y.  Row q of the record holds blocks
+// m - (R - q)*T + t (row R-1 ends with the length block).
 template <int kMode, bool kAligned, bool kWT>
-__device__ __forceinline__ void segment_rows(const GcmCtx* __restrict__ ctx, const RecBatch& batch,
-                                             const Sched& sch, const RecView& v, const uint4* gh,
-                                             const uint4* gh2, const uint32_t* aes, AesLane lane,
-                                             const AesKeys& keys, uint32_t tid, uint32_t q0,
-                                             uint32_t q1, uint32_t y[4], uint32_t ek[4])
+__device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const Sched& sch, const RecView& v, const uint4* gh,
+                                          const uint4* gh2, const uint32_t* aes, AesLane lane,
+                                          const AesKeys& keys, uint32_t t, uint32_t u, uint32_t qa,
+                                          uint32_t qb, uint32_t y[4])
 {
     const uint32_t n0 = bswap32(v.iv[0]) ^ ctx->rk[0];
     const uint32_t n1 = bswap32(v.iv[1]) ^ ctx->rk[1];
     const uint32_t n2 = bswap32(v.iv[2]) ^ ctx->rk[2];
     const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
-    const int64_t base = m - int64_t(sch.rows - q0) * SI_T;
-    const uint32_t J = q1 - q0;
+    const int64_t base = m - int64_t(sch.rows - qa) * SI_T;  // first block of segment row 0
+    const uint32_t J = qb - qa;
+    const uint32_t nu = u < J ? (J - u + SI_U - 1) / SI_U : 0u;
     const uint32_t tail = uint32_t(sch.bytes - (uint64_t(sch.n) - 1) * 16u);  // bytes in last block
     const uint32_t aad_tail = sch.aad_bytes ? uint32_t(sch.aad_bytes - (uint64_t(sch.a) - 1) * 16u) : 0u;
 
-    // Rows whose blocks are all full ciphertext blocks for every thread of
-    // the workgroup take the fast path: i in [a, a + nfull) for all t.
+    // Segment rows whose blocks are all full ciphertext blocks for every
+    // thread of a unit take the fast path: i in [a, a + nfull) for all t.
     const int64_t nfull = int64_t(sch.bytes / 16);
     int64_t jf0 = int64_t(sch.a) - base;                      // first fast row: base + j*T >= a
     jf0 = jf0 <= 0 ? 0 : (jf0 + SI_T - 1) / SI_T;
@@ -412,166 +462,336 @@ __device__ __forceinline__ void segment_rows(const GcmCtx* __restrict__ ctx, con
     jf1 = jf1 < 0 ? 0 : jf1 / SI_T + 1;
     if (jf1 > int64_t(J)) jf1 = J;
     if (jf0 > jf1) jf0 = jf1;
-    const bool fast_ok = kAligned && !(v.bad && !batch.staging);
+    const bool fast_ok = kAligned && !v.skip;
     if (!fast_ok) jf0 = jf1 = J;
+    // The unit's rows inside [jf0, jf1): i in [i0, i1).
+    const auto first_at = [&](int64_t j) -> uint32_t {
+        return j <= int64_t(u) ? 0u : uint32_t((j - int64_t(u) + SI_U - 1) / SI_U);
+    };
+    uint32_t i1 = first_at(jf1), i0 = first_at(jf0);
+    if (i1 > nu) i1 = nu;
+    if (i0 > i1) i0 = i1;
 
     y[0] = y[1] = y[2] = y[3] = 0;
-    for (uint32_t j = 0; j < uint32_t(jf0); ++j) {
-        if (j != 0) gh_mul_table(gh, y);
-        row_general<kMode, kAligned, kWT>(batch, sch, v, aes, lane, keys, n0, n1, n2,
-                                          base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
+    for (uint32_t i = 0; i < i0; ++i) {
+        if (i != 0) gh_mul_table(gh, y);
+        row_general<kMode, kAligned, kWT>(sch, v, aes, lane, keys, n0, n1, n2,
+                                          base + int64_t(u + SI_U * i) * SI_T + t, tail, aad_tail, y);
     }
-    if (jf1 > jf0) {
+    if (i1 > i0) {
         // Drain the key / descriptor loads so the loop's memory waits only
         // track the ciphertext stream.
         __builtin_amdgcn_s_waitcnt(0);
-        const uint64_t k0 = uint64_t(base + tid - int64_t(sch.a));  // block of row 0 (may wrap; rows >= jf0 are valid)
-        // Counter bytes 12..13 constant over the fast rows of the whole workgroup?
+        const uint64_t k0 = uint64_t(base + t - int64_t(sch.a));  // block of segment row 0 (may wrap; fast rows are valid)
+        // Counter bytes 12..13 constant over the fast rows of all units?
         const uint32_t clo = v.iv[3] + uint32_t(base + jf0 * SI_T - int64_t(sch.a));
         const uint32_t chi = v.iv[3] + uint32_t(base + jf1 * SI_T - 1 - int64_t(sch.a));
         const bool cached = (kMode == MODE_DECRYPT || kMode == MODE_ENCRYPT) && chi >= clo &&
                             (clo >> 16) == (chi >> 16);
+        const uint64_t kb = k0 + uint64_t(u) * SI_T;
         if (cached) {
-            const uint32_t s3 = bswap32(v.iv[3] + uint32_t(k0 + uint64_t(jf0) * SI_T)) ^ keys.rk3;
+            const uint32_t s3 = bswap32(v.iv[3] + uint32_t(kb + uint64_t(i0) * SI_U * SI_T)) ^ keys.rk3;
             const CtrCache cc = ctr_cache(aes, lane, ctx, n0, n1, n2, s3);
-            rows_fast<kMode, true>(v, gh, gh2, aes, lane, keys, cc, n0, n1, n2, k0, uint32_t(jf0),
-                                   uint32_t(jf1), y);
+            rows_fast<kMode, true>(v, gh, gh2, aes, lane, keys, cc, n0, n1, n2, kb, i0, i1, y);
         } else {
             const CtrCache cc{};
-            rows_fast<kMode, false>(v, gh, gh2, aes, lane, keys, cc, n0, n1, n2, k0, uint32_t(jf0),
-                                    uint32_t(jf1), y);
+            rows_fast<kMode, false>(v, gh, gh2, aes, lane, keys, cc, n0, n1, n2, kb, i0, i1, y);
         }
     }
-    for (uint32_t j = uint32_t(jf1); j < J; ++j) {
-        if (j != 0) gh_mul_table(gh, y);
-        row_general<kMode, kAligned, kWT>(batch, sch, v, aes, lane, keys, n0, n1, n2,
-                                          base + int64_t(j) * SI_T + tid, tail, aad_tail, y);
+    for (uint32_t i = i1; i < nu; ++i) {
+        if (i != 0) gh_mul_table(gh, y);
+        row_general<kMode, kAligned, kWT>(sch, v, aes, lane, keys, n0, n1, n2,
+                                          base + int64_t(u + SI_U * i) * SI_T + t, tail, aad_tail, y);
     }
-    ek[0] = ek[1] = ek[2] = ek[3] = 0;
-    if (q1 == sch.rows && tid == SI_T - 1) aes_ctr_block(aes, lane, keys, n0, n1, n2, 1u, ek);
 }
 
-// Workgroup w = r*K + c owns rows [c*R/K, (c+1)*R/K) of record r (K chunks
-// per record, chosen by the host so that the grid fills two workgroups per
-// CU without a chunk ever spanning two records).
+// Placement multiplier of thread position t for a segment ending at row qb:
+// H^((R - qb)*T + T - t), the exponent of the thread's last block in the
+// segment; a thread whose blocks all precede X carries zero and takes H^0.
+__device__ __forceinline__ uint4 placement_power(const GcmCtx* __restrict__ ctx, const Sched& sch,
+                                                 uint32_t qb, uint32_t t)
+{
+    const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
+    const int64_t l = m - int64_t(sch.rows - qb + 1) * SI_T + t;
+    const uint64_t e = l >= 0 ? uint64_t(sch.rows - qb) * SI_T + SI_T - t : 0u;
+    return reinterpret_cast<const uint4*>(ctx + 1)[e];
+}
+
+// Record view r of the batch -> LDS (five 16-byte words).
+__device__ __forceinline__ void put_view(uint4* dst, const RecView& v)
+{
+    const uint4* w = reinterpret_cast<const uint4*>(&v);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) dst[i] = w[i];
+}
+
+// LDS -> record view in scalar registers (the view is uniform).
+__device__ __forceinline__ RecView get_view(const uint4* src)
+{
+    RecView v;
+    uint32_t* w = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const uint4 q = src[i];
+        w[4 * i] = __builtin_amdgcn_readfirstlane(q.x);
+        w[4 * i + 1] = __builtin_amdgcn_readfirstlane(q.y);
+        w[4 * i + 2] = __builtin_amdgcn_readfirstlane(q.z);
+        w[4 * i + 3] = __builtin_amdgcn_readfirstlane(q.w);
+    }
+    return v;
+}
+
+// Workgroup w owns a contiguous share of the records' concatenated row
+// sequence (laid out by the host so that a share that straddles two records,
+// which pays a second set of boundary rows and placements, takes fewer
+// rows).  A share spans at most R rows: one or two segments.
+// Phases, separated by workgroup barriers:
+//   1. rows: every unit runs its rows of each segment; its Horner partial is
+//      multiplied by H^(d*T) (d = segment rows after the unit's last one, <
+//      SI_U), which puts all units of a segment on the same exponent grid;
+//   2. combine: the units that do not place a segment hand their products
+//      to the one that does (unit s places segment s) through LDS;
+//   3. placement: the placing thread t multiplies the sum by
+//      H^((R - qb)*T + T - t) (qb = end row of the segment) from the power
+//      table; wave XOR-reduction into LDS (the owner of the record's last
+//      block adds the tag mask E_K(J0) there);
+//   4. ticket: per segment, device atomics XOR the partial into the record's
+//      accumulator and add the segment's rows to its row count; the
+//      workgroup that completes R rows finalises the record.
 template <int kMode, bool kAligned, bool kWT>
-__global__ __launch_bounds__(SI_T) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(SI_NT) __attribute__((amdgpu_waves_per_eu(SI_U, SI_U)))
 void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sch,
                         RecAcc* __restrict__ acc)
 {
-    // Exactly 80 KiB so two workgroups share a CU:
-    // [0, 8 KiB) GHASH tables of H^T, [8, 16 KiB) of H^2T, [16, 80 KiB) AES
-    // Te0/Te1 copies.  After the row work the AES region holds the per-lane
-    // tables of the placement multiply and the H^T region the reduction.
-    __shared__ uint4 s_lds[1024 + 4096];
-    uint4* const gh = s_lds;
-    uint4* const gh2 = s_lds + 512;
+    // 160 KiB, in 16-byte words.  During the rows:
+    //   [0, 1024)      H^UT, H^2UT tables (row steps; below 64 KiB, so every
+    //                  table read takes its offset as an immediate)
+    //   [1024, 5120)   AES Te0/Te1 copies
+    //   [5120, 6144)   H^T, H^2T tables (unit combine)
+    // after them:
+    //   [0, 768)       the units' products of the last segment
+    //   [768, 783)     its wave sums, the record sums, last flags
+    //   [1024, 4864)   placement table of segment 1
+    // throughout: [6144, 9984) the placement table of segment 0 (built in
+    // the set-up; a straddling workgroup keeps segment 0's products and both
+    // multipliers there until after the rows), 9984 a zero word, [9985, 9995) the two record views,
+    // [9995, 9997) their tag masks E_K(J0), [9997, 10009) the wave sums of a
+    // straddling workgroup's segment 0.
+    __shared__ uint4 s_lds[10240];
+    const uint4* const g_u = s_lds;
+    const uint4* const g_u2 = s_lds + 512;
     uint32_t* const aes = reinterpret_cast<uint32_t*>(s_lds + 1024);
-    uint32_t(*const s_red)[4] = reinterpret_cast<uint32_t(*)[4]>(s_lds);
-    uint32_t* const s_last = reinterpret_cast<uint32_t*>(s_lds + SI_T / 64);
+    const uint4* const g_1 = s_lds + 5120;
+    const uint4* const g_2 = s_lds + 5632;
+    uint4* const xs = s_lds;
+    uint4* const s_red = s_lds + 768;
+    uint32_t(*const s_fin)[4] = reinterpret_cast<uint32_t(*)[4]>(s_lds + 768 + SI_NT / 64);
+    uint32_t* const s_last = reinterpret_cast<uint32_t*>(s_lds + 768 + SI_NT / 64 + 2);
+    uint4* const ptab1 = s_lds + 1024;
+    uint4* const ptab0 = s_lds + 6144;
+    uint4* const s_zp = s_lds + 6144 + SI_NT;  // straddling workgroups, during the rows
+    uint4* const s_zero = s_lds + 9984;
+    uint4* const s_view = s_lds + 9985;
+    uint4* const s_ek = s_lds + 9995;
+    uint4* const s_c0 = s_lds + 9997;
 
     constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
     const uint32_t tid = threadIdx.x;
-    {
-        // Every global load of the set-up is issued before the first LDS
-        // write, so the whole fill costs about one L2 round trip.
-        const uint4 g0 = ctx->gh4[tid], g1 = ctx->gh4[tid + SI_T];
-        const uint4 g2 = ctx->gh4b[tid], g3 = ctx->gh4b[tid + SI_T];
+    // Unit index: uniform over a wave (SI_T is a multiple of 64).
+    const uint32_t u = __builtin_amdgcn_readfirstlane(tid / SI_T), t = tid % SI_T;
+
+    // This workgroup's share of the records' concatenated rows.
+    const uint64_t G = uint64_t(sch.nrec) * sch.rows;
+    const uint64_t g0 = sch.use_starts ? sch.starts[blockIdx.x] : uint64_t(blockIdx.x) * G / sch.nwg;
+    const uint64_t g1 = sch.use_starts ? sch.starts[blockIdx.x + 1] : (uint64_t(blockIdx.x) + 1) * G / sch.nwg;
+    if (g1 == g0) return;  // an empty share
+    const uint32_t r0 = uint32_t(g0 / sch.rows);
+    const uint32_t qa0 = uint32_t(g0 - uint64_t(r0) * sch.rows);
+    const uint32_t qb0 = g1 - uint64_t(r0) * sch.rows < sch.rows ? uint32_t(g1 - uint64_t(r0) * sch.rows) : sch.rows;
+    const uint32_t nseg = g1 > (uint64_t(r0) + 1) * sch.rows ? 2u : 1u;
+    const uint32_t qb1 = uint32_t(g1 - (uint64_t(r0) + 1) * sch.rows);  // segment 1: rows [0, qb1) of r0 + 1
+
+    // A one-segment workgroup's placement multiplier, loaded with the tables
+    // below (its placement table is built in the set-up).
+    // A straddling workgroup's two multipliers wait in LDS (after segment 0's
+    // parked products) until its tables are built after the rows.
+    uint4 zp0 = make_uint4(0, 0, 0, 0), zp1 = make_uint4(0, 0, 0, 0);
+    zp0 = placement_power(ctx, sch, qb0, t);
+    if (nseg == 2 && u == 0) zp1 = placement_power(ctx, sch, qb1, t);
+    if (tid < SI_T) {
         aes_fill_lds(aes, ctx->te0, tid);
-        gh[tid] = g0; gh[tid + SI_T] = g1;
-        gh2[tid] = g2; gh2[tid + SI_T] = g3;
+    } else {
+        // Every global load of the set-up is issued before the first LDS
+        // write, so the fill costs about one L2 round trip.
+        const uint32_t i = tid - SI_T;  // 0..511: one entry of each table
+        const uint4 a0 = ctx->gh4u[i], a1 = ctx->gh4u2[i], a2 = ctx->gh4[i], a3 = ctx->gh4b[i];
+        s_lds[i] = a0;
+        s_lds[512 + i] = a1;
+        s_lds[5120 + i] = a2;
+        s_lds[5632 + i] = a3;
+    }
+    if (tid < nseg) put_view(s_view + 5 * tid, view_of(batch, r0 + tid));
+    if (tid == 0) *s_zero = make_uint4(0, 0, 0, 0);
+    // One segment: its placement table now (thread (u, t) writes its third
+    // of the multiples of H^((R - qb)*T + T - t)).  Two segments: the region
+    // holds segment 0's products while segment 1 runs; both tables are built
+    // after the rows.
+    if (nseg == 1) {
+        const uint32_t z[4] = {zp0.x, zp0.y, zp0.z, zp0.w};
+        gh_table_share(z, u, ptab0, t, SI_T);
+    } else if (u == 0) {
+        s_zp[t] = zp0;
+        s_zp[SI_T + t] = zp1;
     }
     AesKeys keys;
     load_keys(ctx, keys);
     __syncthreads();
+    // Tag masks E_K(J0) of the records whose last row ends a segment here
+    // (lanes 0 and 1 of wave 0, before their rows, so nobody waits on them).
+    if (tid < nseg && (tid ? qb1 : qb0) == sch.rows) {
+        const RecView v = get_view(s_view + 5 * tid);
+        uint32_t ek[4];
+        aes_ctr_block(aes, aes_lane(tid), keys, bswap32(v.iv[0]) ^ ctx->rk[0], bswap32(v.iv[1]) ^ ctx->rk[1],
+                      bswap32(v.iv[2]) ^ ctx->rk[2], 1u, ek);
+        s_ek[tid] = make_uint4(ek[0], ek[1], ek[2], ek[3]);
+    }
 
-    const uint32_t r = blockIdx.x / sch.k;
-    const uint32_t c = blockIdx.x % sch.k;
-    const uint32_t q0 = uint32_t(uint64_t(c) * sch.rows / sch.k);
-    const uint32_t q1 = uint32_t(uint64_t(c + 1) * sch.rows / sch.k);
-    const RecView v = view_of(batch, r);
-    uint32_t y[4], ek[4];
-    segment_rows<kMode, kAligned, kWT>(ctx, batch, sch, v, gh, gh2, aes, aes_lane(tid & 63u), keys, tid,
-                                       q0, q1, y, ek);
+    const AesLane lane = aes_lane(tid & 63u);
+    uint4* const s_p0 = ptab0;  // two segments: segment 0's products during segment 1
+    // Rows of segment s; the unit's partial, moved onto the segment's
+    // exponent grid.  A straddling workgroup parks segment 0's in s_p0.
+    auto segment = [&](const uint32_t s) __attribute__((always_inline)) -> uint4 {
+        const uint32_t qa = s ? 0u : qa0, qb = s ? qb1 : qb0;
+        const RecView v = get_view(s_view + 5 * s);
+        uint32_t y[4];
+        unit_rows<kMode, kAligned, kWT>(ctx, sch, v, g_u, g_u2, aes, lane, keys, t, u, qa, qb, y);
+        // d = segment rows after the unit's last row (0 when it has none).
+        const uint32_t J = qb - qa;
+        const uint32_t d = u < J ? (J - 1 - u) % SI_U : 0u;
+        uint32_t pr[4];
+        if (d == 1) gh_mul(g_1, y, pr);
+        else if (d == 2) gh_mul(g_2, y, pr);
+        else { pr[0] = y[0]; pr[1] = y[1]; pr[2] = y[2]; pr[3] = y[3]; }
+        const uint4 r = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        if (s == 0 && nseg == 2) s_p0[tid] = r;
+        return r;
+    };
+    uint4 p = segment(0);
+    if (nseg == 2) p = segment(1);
     __syncthreads();  // AES and GHASH tables are dead from here on
 
-    // Thread t's partial covers blocks whose last one has exponent
-    // (R - q1)*T + T - t; threads whose blocks all precede X carry zero.
-    uint32_t q[4] = {0, 0, 0, 0};
-    {
-        const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
-        const int64_t i_last = m - int64_t(sch.rows - q1 + 1) * SI_T + tid;
-        const uint64_t e = i_last >= 0 ? uint64_t(sch.rows - q1) * SI_T + SI_T - tid : 0u;
-        const uint4 zp = reinterpret_cast<const uint4*>(ctx + 1)[e];
-        const uint32_t z[4] = {zp.x, zp.y, zp.z, zp.w};
-        gh_mul_generic(y, z, reinterpret_cast<uint4*>(aes), tid, SI_T, q);
-    }
-    q[0] ^= ek[0]; q[1] ^= ek[1]; q[2] ^= ek[2]; q[3] ^= ek[3];
-    wave_xor4(q);
-    // Every wave's data stores must be complete (write-through) or at least
-    // in L2 (before thread 0's release) when the ticket is taken; s_barrier
-    // does not wait for them.
-    __builtin_amdgcn_s_waitcnt(0);
-    if ((tid & 63u) == 0) {
-        s_red[tid >> 6][0] = q[0]; s_red[tid >> 6][1] = q[1];
-        s_red[tid >> 6][2] = q[2]; s_red[tid >> 6][3] = q[3];
-    }
+    // The last segment's products to LDS; placement t is shared by the three
+    // threads (u, t): one table, three nibble classes.
+    xs[u * SI_T + t] = p;
     __syncthreads();
-    RecAcc* ra = acc + r;
-    if (tid == 0) {
-        uint32_t t[4] = {0, 0, 0, 0};
+    uint32_t w[2][4];
+    {
+        const uint4 a = xs[t], b = xs[SI_T + t], c = xs[2 * SI_T + t];
+        w[1][0] = xor3(a.x, b.x, c.x); w[1][1] = xor3(a.y, b.y, c.y);
+        w[1][2] = xor3(a.z, b.z, c.z); w[1][3] = xor3(a.w, b.w, c.w);
+    }
+    uint32_t q[2][4];
+    if (nseg == 1) {  // uniform over the workgroup; the table is ready
+        const uint32_t(&x1)[1][4] = reinterpret_cast<const uint32_t(&)[1][4]>(w[1]);
+        uint32_t(&o1)[1][4] = reinterpret_cast<uint32_t(&)[1][4]>(q[1]);
+        const uint4* const tb[1] = {ptab0};
+        if (u == 0) gh_mul_part<3, 0, 1>(x1, tb, s_zero, t, SI_T, o1);
+        else if (u == 1) gh_mul_part<3, 1, 1>(x1, tb, s_zero, t, SI_T, o1);
+        else gh_mul_part<3, 2, 1>(x1, tb, s_zero, t, SI_T, o1);
+    } else {
+        {
+            const uint4 a = s_p0[t], b = s_p0[SI_T + t], c = s_p0[2 * SI_T + t];
+            w[0][0] = xor3(a.x, b.x, c.x); w[0][1] = xor3(a.y, b.y, c.y);
+            w[0][2] = xor3(a.z, b.z, c.z); w[0][3] = xor3(a.w, b.w, c.w);
+        }
+        const uint4 z0 = s_zp[t], z1 = s_zp[SI_T + t];
+        __syncthreads();  // s_p0 and s_zp are read; the region takes segment 0's table
+        {
+            const uint32_t za[4] = {z0.x, z0.y, z0.z, z0.w}, zb[4] = {z1.x, z1.y, z1.z, z1.w};
+            gh_table_share(za, u, ptab0, t, SI_T);
+            gh_table_share(zb, u, ptab1, t, SI_T);
+        }
+        __syncthreads();
+        const uint4* const tb[2] = {ptab0, ptab1};
+        if (u == 0) gh_mul_part<3, 0, 2>(w, tb, s_zero, t, SI_T, q);
+        else if (u == 1) gh_mul_part<3, 1, 2>(w, tb, s_zero, t, SI_T, q);
+        else gh_mul_part<3, 2, 2>(w, tb, s_zero, t, SI_T, q);
+        wave_xor4(q[0]);
+        if ((tid & 63u) == 0) s_c0[tid >> 6] = make_uint4(q[0][0], q[0][1], q[0][2], q[0][3]);
+    }
+    wave_xor4(q[1]);
+    if ((tid & 63u) == 0) s_red[tid >> 6] = make_uint4(q[1][0], q[1][1], q[1][2], q[1][3]);
+    // Every wave's data stores must be complete (write-through) or at least
+    // in L2 (before the ticket's release) when the ticket is taken;
+    // s_barrier does not wait for them.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid < nseg) {
+        const uint32_t s = tid;
+        const uint32_t qa = s ? 0u : qa0, qb = s ? qb1 : qb0;
+        uint32_t r4[4] = {0, 0, 0, 0};
+        const uint4* red = (s == 0 && nseg == 2) ? s_c0 : s_red;
 #pragma unroll
-        for (int w = 0; w < SI_T / 64; ++w)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) t[k] ^= s_red[w][k];
-        if (sch.k == 1) {
-            s_red[0][0] = t[0]; s_red[0][1] = t[1]; s_red[0][2] = t[2]; s_red[0][3] = t[3];
-            *s_last = 1;
-        } else {
+        for (int w = 0; w < SI_NT / 64; ++w) {
+            const uint4 e = red[w];
+            r4[0] ^= e.x; r4[1] ^= e.y; r4[2] ^= e.z; r4[3] ^= e.w;
+        }
+        if (qb == sch.rows) {  // the record's tag mask
+            const uint4 e = s_ek[s];
+            r4[0] ^= e.x; r4[1] ^= e.y; r4[2] ^= e.z; r4[3] ^= e.w;
+        }
+        uint32_t last = 1;
+        if (qa != 0 || qb != sch.rows) {
+            RecAcc* ra = acc + r0 + s;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                __hip_atomic_fetch_xor(&ra->w[k], t[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            // Take a ticket once this workgroup's data stores and XORs are
+                __hip_atomic_fetch_xor(&ra->w[k], r4[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // Count this segment's rows once its data stores and XORs are
             // performed.  Write-through stores are complete after s_waitcnt;
             // byte-granular stores need the agent-scope release (L2 write-back).
             uint32_t prev;
             if (kNeedRelease) {
-                prev = __hip_atomic_fetch_add(&ra->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+                prev = __hip_atomic_fetch_add(&ra->count, qb - qa, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 __builtin_amdgcn_s_waitcnt(0);
-                prev = __hip_atomic_fetch_add(&ra->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                prev = __hip_atomic_fetch_add(&ra->count, qb - qa, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            *s_last = prev == sch.k - 1 ? 1u : 0u;
-            if (*s_last) {
+            last = prev + (qb - qa) == sch.rows ? 1u : 0u;
+            if (last) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    s_red[0][k] = __hip_atomic_exchange(&ra->w[k], 0u, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT);
+                    r4[k] = __hip_atomic_exchange(&ra->w[k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&ra->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        s_last[s] = last;
+        s_fin[s][0] = r4[0]; s_fin[s][1] = r4[1]; s_fin[s][2] = r4[2]; s_fin[s][3] = r4[3];
     }
     __syncthreads();
-    if (!*s_last) return;
-    
-    // Finalise the record.
-    if (kMode == MODE_ENCRYPT) {
-        if (tid == 0 && v.bad && batch.fail_count) atomicAdd(batch.fail_count, 1u);
-        if (tid < 4) {
-            const uint32_t w = s_red[0][tid];
-            for (int b = 0; b < 4; ++b) v.tag[4 * tid + b] = uint8_t(w >> (8 * b));
+
+    // Finalise the records completed here.
+#pragma unroll 1
+    for (uint32_t s = 0; s < nseg; ++s) {
+        if (!s_last[s]) continue;
+        const RecView v = get_view(s_view + 5 * s);
+        if (kMode == MODE_ENCRYPT) {
+            if (tid == 0 && v.bad && v.fail_count) atomicAdd(v.fail_count, 1u);
+            if (tid < 4) {
+                const uint32_t w = s_fin[s][tid];
+                for (int b = 0; b < 4; ++b) gmem(v.tag)[4 * tid + b] = uint8_t(w >> (8 * b));
+            }
+            continue;
         }
-        return;
-    }
-    uint32_t diff = 0;
+        uint32_t diff = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) diff |= uint32_t(uint8_t(s_red[0][k >> 2] >> (8 * (k & 3))) ^ v.tag[k]);
-    const uint32_t ok = (diff == 0 && !v.bad) ? 1u : 0u;
-    if (tid == 0) {
-        *v.status = ok;
-        if (!ok && batch.fail_count) atomicAdd(batch.fail_count, 1u);
+        for (int k = 0; k < 16; ++k) diff |= uint32_t(uint8_t(s_fin[s][k >> 2] >> (8 * (k & 3))) ^ gmem(v.tag)[k]);
+        const uint32_t ok = (diff == 0 && !v.bad) ? 1u : 0u;
+        if (tid == 0) {
+            *gmem(v.status) = ok;
+            if (!ok && v.fail_count) atomicAdd(v.fail_count, 1u);
+        }
+        if (!ok && kMode != MODE_VERIFY && !v.skip) zero_bytes(v.dst, sch.bytes, tid, SI_NT);
     }
-    if (!ok && kMode != MODE_VERIFY && !(v.bad && !batch.staging)) zero_bytes(v.dst, sch.bytes, tid, SI_T);
 }
 
 __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ctx,
@@ -618,7 +838,8 @@ template <int kMode>
 static hipError_t launch_mode(hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                               const Sched& s, RecAcc* acc, bool aligned)
 {
-    const dim3 grid(s.nrec * s.k), block(SI_T);
+    if (s.nwg == 0) return hipSuccess;
+    const dim3 grid(s.nwg), block(SI_NT);
     if (aligned && s.bytes % 16 == 0)
         hipLaunchKernelGGL((gcm_records_kernel<kMode, true, true>), grid, block, 0, stream, ctx, b, s, acc);
     else if (aligned)

@@ -39,11 +39,17 @@ struct RecBatch {
     uint32_t* fail_count;
 };
 
+// Most workgroups whose shares the host lays out one by one (kernel
+// argument space); larger launches split the rows equally.
+#define SI_MAX_WG 768
+
 // Work decomposition shared by all records of a batch (uniform sizes).
 struct Sched {
     uint32_t nrec;       // records
     uint32_t rows;       // R: rows of T blocks per record, ceil((a + n + 1) / T)
-    uint32_t k;          // workgroups (row chunks) per record, 1..R
+    uint32_t nwg;        // W workgroups, W >= nrec (a share never spans more than R rows)
+    uint32_t use_starts; // 1: workgroup w owns rows [starts[w], starts[w+1]); 0: an equal split
+    uint32_t starts[SI_MAX_WG + 1];  // share boundaries in the records' concatenated rows
     uint32_t a;          // AAD blocks
     uint32_t n;          // payload blocks
     uint32_t aad_bytes;

@@ -292,8 +292,18 @@ class GcmSession:
                "writeback_layer")
 
 
+DEFAULT_CHUNK_ROWS = 3
+DEFAULT_STRADDLE_ROWS = 10
+
+
 def set_chunk_rows(jmax: int) -> None:
+    """Minimum rows (of 256 blocks) per workgroup share of a layer (1..256)."""
     _check(lib().secure_infer_gpu_set_chunk_rows(jmax), "set_chunk_rows")
+
+
+def set_straddle_rows(rows: int) -> None:
+    """Cost, in rows, charged to a share that straddles two records (0..256)."""
+    _check(lib().secure_infer_gpu_set_straddle_rows(rows), "set_straddle_rows")
 
 
 class NativeTransfer:

@@ -149,8 +149,8 @@ def make_caches(nslots, heads, dim, fill=0x3C):
     return k, v
 
 
-@pytest.mark.parametrize("chunk_rows", [16, 1, 3, 64])
-def test_reload_layer_bf16(chunk_rows):
+@pytest.mark.parametrize("chunk_rows,straddle", [(16, 10), (1, 10), (3, 0), (16, 0), (64, 0)])
+def test_reload_layer_bf16(chunk_rows, straddle):
     rng = np.random.default_rng(21)
     heads, dim, nb, nslots, layer = 8, 128, 6, 32, 4
     blocks = W.bf16_blocks(rng, 2 * nb, heads, dim)
@@ -166,13 +166,15 @@ def test_reload_layer_bf16(chunk_rows):
     sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=payloads[0].size)
     fail = torch.zeros(1, dtype=torch.int32, device=DEV)
     si.set_chunk_rows(chunk_rows)
+    si.set_straddle_rows(straddle)
     try:
         dw = dev(wire)
         sess.reload_layer(dw, payloads[0].size, 2 * nb, nb, ck, cv, slots, ticket_base=ticket0,
                           fail_count=fail)
         kk, vv, ww = host(ck), host(cv), host(dw)
     finally:
-        si.set_chunk_rows(16)
+        si.set_chunk_rows(si.gcm.DEFAULT_CHUNK_ROWS)
+        si.set_straddle_rows(si.gcm.DEFAULT_STRADDLE_ROWS)
     st = W.stride(payloads[0].size)
     toff = W.align32(payloads[0].size)
     statuses = [int(ww[r * st + toff + 16:r * st + toff + 20].view(np.uint32)[0]) for r in range(2 * nb)]
@@ -248,6 +250,41 @@ def test_writeback_layer(bits):
                          ticket_base=ticket0, codec_bits=bits, heads=heads, head_dim=dim,
                          layer=layer, staging=staging)
     ww = host(dw)
+    expect = W.build_wire(KEY, SALT, plain, kinds, layer, list(range(2 * nb)), ticket0, direction=2)
+    st, toff = W.stride(n), W.align32(n)
+    for r in range(2 * nb):
+        o = r * st
+        assert np.array_equal(ww[o:o + n], expect[o:o + n]), f"record {r} ciphertext"
+        assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
+
+
+@pytest.mark.parametrize("chunk_rows", [3, 16, 64])
+def test_writeback_layer_straddling_shares(chunk_rows):
+    """Encrypt with workgroup shares that straddle two records (straddle cost
+    0, shares of at least chunk_rows rows), bf16 records of 65 rows."""
+    rng = np.random.default_rng(61 + chunk_rows)
+    heads, dim, nb, nslots, layer = 8, 128, 5, 16, 2
+    ck, cv = make_caches(nslots, heads, dim)
+    data = O.f32_to_bf16(rng.standard_normal((2, nslots, 128, heads, dim), dtype=np.float32))
+    ck.copy_(dev(data[0].view(np.int16)))
+    cv.copy_(dev(data[1].view(np.int16)))
+    slots_np = rng.permutation(nslots)[:nb].astype(np.int64)
+    kinds = [0] * nb + [1] * nb
+    plain = [data[kinds[r]][slots_np[r % nb]].view(np.uint8).reshape(-1) for r in range(2 * nb)]
+    n = plain[0].size
+    ticket0 = 500
+    wire = W.wire_aads(KEY, SALT, n, kinds, layer, list(range(2 * nb)), ticket0)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    dw = dev(wire)
+    si.set_chunk_rows(chunk_rows)
+    si.set_straddle_rows(0)
+    try:
+        sess.writeback_layer(dw, n, 2 * nb, nb, ck, cv, dev(np.concatenate([slots_np, slots_np])),
+                             ticket_base=ticket0, codec_bits=0, heads=heads, head_dim=dim, layer=layer)
+        ww = host(dw)
+    finally:
+        si.set_chunk_rows(si.gcm.DEFAULT_CHUNK_ROWS)
+        si.set_straddle_rows(si.gcm.DEFAULT_STRADDLE_ROWS)
     expect = W.build_wire(KEY, SALT, plain, kinds, layer, list(range(2 * nb)), ticket0, direction=2)
     st, toff = W.stride(n), W.align32(n)
     for r in range(2 * nb):
