@@ -116,6 +116,14 @@ __global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint
     }
 }
 
+// Another lane's value by a DPP move: 0xb1 swaps lanes 2i / 2i+1, 0x4e swaps
+// pairs within a quad, 0x141 mirrors each 8-lane half-row.
+template <int kCtrl>
+__device__ __forceinline__ float lane_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
 {
     const float s = __fdiv_rn(__fsub_rn(hi, lo), qmax);
@@ -234,13 +242,17 @@ __global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
 #pragma unroll
         for (int k = 0; k < 8; ++k) { lo[k] = fminf(lo[k], x[k]); hi[k] = fmaxf(hi[k], x[k]); }
     }
+    // Min / max over the eight lanes of a chunk with DPP moves: swap within
+    // pairs, then within quads, then mirror the 8-lane half-row.
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            lo[k] = fminf(lo[k], __shfl_xor(lo[k], m));
-            hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], m));
-        }
+    for (int k = 0; k < 8; ++k) {
+        lo[k] = fminf(lo[k], lane_dpp<0xb1>(lo[k]));
+        hi[k] = fmaxf(hi[k], lane_dpp<0xb1>(hi[k]));
+        lo[k] = fminf(lo[k], lane_dpp<0x4e>(lo[k]));
+        hi[k] = fmaxf(hi[k], lane_dpp<0x4e>(hi[k]));
+        lo[k] = fminf(lo[k], lane_dpp<0x141>(lo[k]));
+        hi[k] = fmaxf(hi[k], lane_dpp<0x141>(hi[k]));
+    }
     float sc[8], rc[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -266,46 +278,61 @@ __global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
     }
 }
 
-// V: eight lanes per (token, head, dim group of 64), 8 elements each; the
-// group's min / max is reduced across the eight lanes.  Grid (x, V record).
+
+// V: two lanes per (token, head, dim group of 64), 32 consecutive elements
+// each; the group's min / max meets in one DPP swap, and the group's scale
+// and reciprocal are formed once per 32 elements.  Grid (x, V record).
 __global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b)
 {
     const uint32_t r = b.n_k + blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
     const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     const uint32_t ngroups = 2u * hd;  // 128 * hd / 64
-    // Whole 8-lane groups take the same branch, so the shuffles below see
-    // only active partners.
-    if (idx >= ngroups * 8u) return;
+    // Lane pairs (2i, 2i+1) take the same branch, so the swap below always
+    // meets an active partner.
+    if (idx >= ngroups * 2u) return;
     const int64_t sid = b.slots[r];
     if (sid < 0 || sid >= b.nslots) return;
-    const uint32_t gi = idx >> 3, l8 = idx & 7u;
+    const uint32_t gi = idx >> 1, half = idx & 1u;
     const float qmax = float((1u << b.bits) - 1u);
     const uint8_t* slot = b.cache[1] + uint64_t(sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
     if (idx == 0) store_header(b, pkt, 1u);
-    const uint32_t e = gi * 64u + l8 * 8u;
-    float x[8];
-    unpack8(*reinterpret_cast<const uint4*>(slot + uint64_t(e) * 2u), x);
+    const uint32_t e = gi * 64u + half * 32u;
+    uint4 raw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) raw[k] = *reinterpret_cast<const uint4*>(slot + uint64_t(e + 8u * k) * 2u);
+    float x[32];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) unpack8(raw[k], x + 8 * k);
     float lo = x[0], hi = x[0];
 #pragma unroll
-    for (int k = 1; k < 8; ++k) { lo = fminf(lo, x[k]); hi = fmaxf(hi, x[k]); }
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, m));
-        hi = fmaxf(hi, __shfl_xor(hi, m));
-    }
+    for (int k = 1; k < 32; ++k) { lo = fminf(lo, x[k]); hi = fmaxf(hi, x[k]); }
+    lo = fminf(lo, lane_dpp<0xb1>(lo));
+    hi = fmaxf(hi, lane_dpp<0xb1>(hi));
     const float s = quant_scale(lo, hi, qmax);
     const float y = recip_rn(s);
-    if (l8 == 0) {
+    if (half == 0) {
         reinterpret_cast<float*>(pkt + b.qbytes)[gi] = s;
         reinterpret_cast<float*>(pkt + b.qbytes + b.sbytes)[gi] = lo;
     }
-    uint32_t q[8], w[2];
+    uint32_t w[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) q[k] = quant_one(x[k], lo, s, y, qmax);
-    pack8(q, b.bits, w);
-    store_q8(pkt, e, b.bits, w);
+    for (int k = 0; k < 4; ++k) {
+        uint32_t q[8], p2[2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = quant_one(x[8 * k + i], lo, s, y, qmax);
+        pack8(q, b.bits, p2);
+        w[2 * k] = p2[0];
+        w[2 * k + 1] = p2[1];
+    }
+    if (b.bits == 8) {
+        uint4* dst = reinterpret_cast<uint4*>(pkt + e);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    } else {
+        *reinterpret_cast<uint4*>(pkt + e / 2u) = make_uint4(w[0], w[2], w[4], w[6]);
+    }
 }
 
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b)
@@ -330,7 +357,7 @@ hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b)
     if (b.n_k)
         hipLaunchKernelGGL(quant_k_kernel, dim3((2u * hd + 255u) / 256u, b.n_k), dim3(256), 0, stream, b);
     if (nv)
-        hipLaunchKernelGGL(quant_v_kernel, dim3((16u * hd + 255u) / 256u, nv), dim3(256), 0, stream, b);
+        hipLaunchKernelGGL(quant_v_kernel, dim3((4u * hd + 255u) / 256u, nv), dim3(256), 0, stream, b);
     return hipGetLastError();
 }
 
