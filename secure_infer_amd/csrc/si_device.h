@@ -264,17 +264,59 @@ __device__ __forceinline__ void aes_combine_last(const uint32_t q[16], const uin
                                              rk[j], 0x56);
 }
 
+// Byte offset (nibble * 16) of 4-bit position P of the 128-bit value `in`
+// in P's 256-byte table: position P = 8w + 2b + h is the low (h = 0) or high
+// (h = 1) nibble of byte b of word w.  One SDWA instruction each:
+//   low:  (byte_b << 4) truncated to a byte = low nibble * 16;
+//   high: byte_b & 0xf0 = high nibble * 16.
+template <int P>
+__device__ __forceinline__ uint32_t nib_off(const uint32_t in[4])
+{
+    constexpr int w = P >> 3, b = (P & 7) >> 1;
+    const uint32_t x = in[w];
+    uint32_t d;
+#define SI_NIB_LO(B)                                                                              \
+    asm volatile("v_lshlrev_b32_sdwa %0, 4, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD "        \
+        "src1_sel:BYTE_" #B : "=v"(d) : "v"(x))
+#define SI_NIB_HI(B)                                                                              \
+    asm volatile("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_" #B          \
+        " src1_sel:DWORD" : "=v"(d) : "v"(x), "s"(0xf0u))
+    if constexpr (P & 1) {
+        if constexpr (b == 0) SI_NIB_HI(0);
+        else if constexpr (b == 1) SI_NIB_HI(1);
+        else if constexpr (b == 2) SI_NIB_HI(2);
+        else SI_NIB_HI(3);
+    } else {
+        if constexpr (b == 0) SI_NIB_LO(0);
+        else if constexpr (b == 1) SI_NIB_LO(1);
+        else if constexpr (b == 2) SI_NIB_LO(2);
+        else SI_NIB_LO(3);
+    }
+#undef SI_NIB_LO
+#undef SI_NIB_HI
+    return d;
+}
+
+template <int P>
+__device__ __forceinline__ uint4 gh_read(const char* base, const uint32_t in[4])
+{
+    return *reinterpret_cast<const uint4*>(base + P * 256 + nib_off<P>(in));
+}
+
+template <int P, int P1>
+__device__ __forceinline__ void gh_issue_at(const char* base, const uint32_t in[4], uint4 g[])
+{
+    if constexpr (P < P1) {
+        g[0] = gh_read<P>(base, in);
+        gh_issue_at<P + 1, P1>(base, in, g + 1);
+    }
+}
+
 // Reads [P0, P1) of in * H^k (4-bit per-position tables) into g.
 template <int P0, int P1>
 __device__ __forceinline__ void gh_issue(const uint4* tbl, const uint32_t in[4], uint4 g[])
 {
-    const char* base = reinterpret_cast<const char*>(tbl);
-#pragma unroll
-    for (int p = P0; p < P1; ++p) {
-        const int w = p >> 3, b = (p & 7) >> 1;
-        const uint32_t sh = (p & 1) ? (in[w] & 0xf0f0f0f0u) : ((in[w] << 4) & 0xf0f0f0f0u);
-        g[p - P0] = *reinterpret_cast<const uint4*>(base + p * 256 + ((sh >> (8 * b)) & 0xffu));
-    }
+    gh_issue_at<P0, P1>(reinterpret_cast<const char*>(tbl), in, g);
 }
 
 template <int N>

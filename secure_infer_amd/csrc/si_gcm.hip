@@ -2,21 +2,23 @@
 //
 // One launch processes a batch of records.  Each record's GHASH input is the
 // block sequence X = AAD || C || L (SP 800-38D), m = a + n + 1 blocks, and
-// GHASH = XOR_k X_k * H^(m-k).  X is cut into R rows of T blocks counted from
-// its end (row R-1 ends with L; row 0 may start before X), and thread t of a
-// workgroup owns block t of each of its rows, so every row is one coalesced
-// 4 KiB sweep.  Each record's rows are split into K contiguous chunks, one
-// per workgroup.  Per thread:
+// GHASH = XOR_k X_k * H^(m-k).  X is cut into R rows of T = 256 blocks
+// counted from its end (row R-1 ends with L; row 0 may start before X).  A
+// workgroup of three 256-thread units takes a contiguous share of the
+// records' concatenated rows (laid out by the host; one or two records);
+// thread t of a unit owns block t of each of its rows, so every row is one
+// coalesced 4 KiB sweep, and the units interleave the share's rows.  Per
+// thread:
 //   * CTR: keystream of counter iv3 + k for ciphertext block k (32-bit wrap,
 //     ghash.aicpu:174-221), XORed into the data and stored;
-//   * GHASH: Horner with H^T over the thread's blocks (LDS tables), then one
-//     generic multiply by H^((R - q1)*T + T - t) from the per-key power table
-//     (q1 = end row of the chunk), which places the
-//     thread's partial at its true exponent.
+//   * GHASH: Horner with H^768 over the unit's rows (LDS tables), a move onto
+//     the segment's exponent grid (H^256 or H^512), and a placement multiply
+//     by H^((R - qb)*T + T - t) (qb = end row of the segment) shared by the
+//     three threads of position t.
 // Partials are XOR-reduced over the workgroup and then across workgroups with
-// device-scope atomics; a ticket names the workgroup that completes a
-// record, which compares the tag in constant time, writes the
-// status and, on failure, zeroes the record's output before the kernel ends.
+// device-scope atomics; a row count names the workgroup that completes a
+// record, which compares the tag in constant time, writes the status and, on
+// failure, zeroes the record's output before the kernel ends.
 // The zeroing must land after every plaintext store of the record:
 // full-block stores are issued write-through (sc1, agent-coherent) and
 // drained (s_waitcnt) before a workgroup takes its ticket; byte-granular
@@ -349,6 +351,19 @@ __device__ __forceinline__ void load_rows(const uint4* __restrict__ src, const u
     }
 }
 
+// Issue priority of a wave with `left` pair steps to go (this one included).
+// The arbiter otherwise favours the oldest wave: it runs one unit's rows to
+// the end while the others wait, then leaves the last unit alone on the SIMDs
+// with too few waves to hide latency.  Dropping a step's priority as a wave
+// gets ahead keeps the units of a workgroup within about a step of each other.
+__device__ __forceinline__ void step_priority(uint32_t left)
+{
+    if (left >= 4) __builtin_amdgcn_s_setprio(3);
+    else if (left == 3) __builtin_amdgcn_s_setprio(2);
+    else if (left == 2) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // Full-ciphertext rows i in [i0, i1) of this thread's unit (block k = kb +
 // i*S, S = SI_U*SI_T), two rows per step.  Ping-pong buffers: the loads of
 // the next step are issued before the current step's keystreams, so HBM
@@ -396,22 +411,16 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
             rows_of(st0, ka);
             load_rows<kMode, kP>(src, ksrc, ka, a, qa);
             for (uint32_t st = st0; st < nsteps; st += 2) {
-                // Waves that are ahead yield issue priority to the ones
-                // behind (the arbiter otherwise favours the oldest wave), so
-                // the units of a workgroup finish their rows together.
-                const uint32_t left = nsteps - st;
-                if (left >= 6) __builtin_amdgcn_s_setprio(3);
-                else if (left >= 4) __builtin_amdgcn_s_setprio(2);
-                else if (left >= 2) __builtin_amdgcn_s_setprio(1);
-                else __builtin_amdgcn_s_setprio(0);
                 rows_of(st + 1, kb2);
                 load_rows<kMode, kP>(src, ksrc, kb2, b, qb);
                 __builtin_amdgcn_sched_barrier(0);
+                step_priority(nsteps - st);
                 rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, ka, a, qa, y, pend);
                 if (st + 1 >= nsteps) break;
                 rows_of(st + 2, ka);
                 load_rows<kMode, kP>(src, ksrc, ka, a, qa);
                 __builtin_amdgcn_sched_barrier(0);
+                step_priority(nsteps - st - 1);
                 rows_body<kMode, kCached, kP>(v, dst, gh, gh2, aes, lane, keys, cc, n0, n1, n2, kb2, b, qb, y, pend);
             }
             __builtin_amdgcn_s_setprio(0);
