@@ -11,7 +11,9 @@ records tampered, which must fail closed) and a Llama-3-70B int4 writeback.
 
 Prints ONE JSON line.  `value` is GB/s of algorithmic bytes over the timed
 region (reload, per record: ciphertext read + bf16 write + tag + AAD + status;
-writeback: bf16 read + ciphertext write + tag + AAD).
+writeback: bf16 read + ciphertext write + tag + AAD).  `roofline.traffic` and
+`issue` (VALU / LDS issue fractions of the GCM kernel) come from the committed
+rocprofv3 counter summaries under profiles/.
 """
 from __future__ import annotations
 
@@ -69,6 +71,26 @@ def load_traffic(workload: str):
             return d.get("traffic_bytes_per_launch")
         except Exception:
             return None
+    return None
+
+
+def load_issue(workload: str):
+    """VALU / LDS issue fractions of the workload's GCM kernel from the committed
+    rocprofv3 counter summary (profiles/<workload>_issue.json), or None."""
+    path = ROOT / "profiles" / f"{workload}_issue.json"
+    if not path.exists():
+        return None
+    try:
+        d = json.loads(path.read_text())
+    except Exception:
+        return None
+    for kernel, row in d.items():
+        if "gcm_records_kernel" in kernel:
+            return {"kernel": kernel, "valu_issue_frac": row.get("valu_issue_frac"),
+                    "lds_active_frac": row.get("lds_active_frac"),
+                    "lds_bank_conflict_frac": row.get("lds_bank_conflict_frac"),
+                    "valu_busy_rocprof_pct": row.get("valu_busy_rocprof_pct"),
+                    "source": f"profiles/{workload}_issue.md"}
     return None
 
 
@@ -362,6 +384,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(args.config)},
+        "issue": load_issue(args.config),
     }
     if not args.no_cpu:
         layer = 0
