@@ -38,11 +38,33 @@ __device__ __forceinline__ uint32_t udiv_small(uint32_t n, uint32_t d)
     return q;
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two decoded elements fl(fl(q*s) + o) as packed bf16.  With finite s and o
+// no result is NaN (q is a small integer), and v_cvt_pk_bf16_f32 rounds every
+// non-NaN float to nearest even exactly like f32_to_bf16 (checked on every
+// float bit pattern); a NaN would keep its sign and payload instead of
+// becoming 0x7fc0, so non-finite parameters take the scalar conversion.
+template <bool kFinite>
 __device__ __forceinline__ uint32_t dq2(float q0, float s0, float o0, float q1, float s1, float o1)
 {
     const float v0 = __fadd_rn(__fmul_rn(q0, s0), o0);
     const float v1 = __fadd_rn(__fmul_rn(q1, s1), o1);
-    return f32_to_bf16(v0) | (f32_to_bf16(v1) << 16);
+    if constexpr (kFinite) {
+        f32x2 v;
+        v.x = v0;
+        v.y = v1;
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    } else {
+        return f32_to_bf16(v0) | (f32_to_bf16(v1) << 16);
+    }
+}
+
+// 0 for finite x, NaN otherwise (x - x).
+__device__ __forceinline__ float nonfinite(float x)
+{
+    return __fsub_rn(x, x);
 }
 
 // One thread -> 16 consecutive columns (h, d) of `tpt` consecutive tokens
@@ -70,6 +92,7 @@ __global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint
     uint8_t* slot = b.cache[kind] + uint64_t(sid) * b.slot_bytes;
 
     float ks[16], ko[16];
+    bool kfin = true;
     if (kind == 0) {
         const uint32_t p = (tg * tpt >> 6) * hd + col;
         const float4* s4 = reinterpret_cast<const float4*>(scale + p);
@@ -80,6 +103,10 @@ __global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint
             ks[4 * k] = sv.x; ks[4 * k + 1] = sv.y; ks[4 * k + 2] = sv.z; ks[4 * k + 3] = sv.w;
             ko[4 * k] = ov.x; ko[4 * k + 1] = ov.y; ko[4 * k + 2] = ov.z; ko[4 * k + 3] = ov.w;
         }
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __fadd_rn(acc, __fadd_rn(nonfinite(ks[k]), nonfinite(ko[k])));
+        kfin = acc == 0.0f;
     }
     const uint32_t hh = udiv_small(col, b.dim);
     const uint32_t vgroup = hh * (b.dim / 64u) + (col - hh * b.dim) / 64u;
@@ -101,14 +128,25 @@ __global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint
         }
         uint32_t out[8];
         if (kind == 0) {
+            if (kfin) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                out[k] = dq2(q[2 * k], ks[2 * k], ko[2 * k], q[2 * k + 1], ks[2 * k + 1], ko[2 * k + 1]);
+                for (int k = 0; k < 8; ++k)
+                    out[k] = dq2<true>(q[2 * k], ks[2 * k], ko[2 * k], q[2 * k + 1], ks[2 * k + 1], ko[2 * k + 1]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    out[k] = dq2<false>(q[2 * k], ks[2 * k], ko[2 * k], q[2 * k + 1], ks[2 * k + 1], ko[2 * k + 1]);
+            }
         } else {
             const uint32_t p = t * (hd / 64u) + vgroup;  // (t, h, dim-group) row-major
             const float sv = scale[p], ov = low[p];
+            if (__fadd_rn(nonfinite(sv), nonfinite(ov)) == 0.0f) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) out[k] = dq2(q[2 * k], sv, ov, q[2 * k + 1], sv, ov);
+                for (int k = 0; k < 8; ++k) out[k] = dq2<true>(q[2 * k], sv, ov, q[2 * k + 1], sv, ov);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) out[k] = dq2<false>(q[2 * k], sv, ov, q[2 * k + 1], sv, ov);
+            }
         }
         uint4* dst = reinterpret_cast<uint4*>(slot + uint64_t(e0) * 2u);
         dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
@@ -122,6 +160,20 @@ template <int kCtrl>
 __device__ __forceinline__ float lane_dpp(float v)
 {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
+// v[k] = lane k's value of this lane's 8-lane group (k = 0..7): ds_swizzle
+// in bit mode, lane' = (lane & 0x18) | k within each 32 lanes.
+template <int K>
+__device__ __forceinline__ float swz8(float v)
+{
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (K << 5)));
+}
+
+__device__ __forceinline__ void group8_bcast(float v, float out[8])
+{
+    out[0] = swz8<0>(v); out[1] = swz8<1>(v); out[2] = swz8<2>(v); out[3] = swz8<3>(v);
+    out[4] = swz8<4>(v); out[5] = swz8<5>(v); out[6] = swz8<6>(v); out[7] = swz8<7>(v);
 }
 
 __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
@@ -155,13 +207,18 @@ __device__ __forceinline__ float div_rn(float a, float s, float y)
     return fmaf(fmaf(-q, s, a), y, q);
 }
 
-// q = clamp(rne(RN((x - lo) / s)), 0, qmax) as an integer: the clamp commutes
-// with rounding (integer bounds), and adding 2^23 rounds half-to-even into
-// the low mantissa bits.
-__device__ __forceinline__ uint32_t quant_one(float x, float lo, float s, float y, float qmax)
+// RN((x - lo) / s) rounded half-to-even, clamped to [0, qmax] and inserted
+// as byte K of acc: v_cvt_pk_u8_f32 rounds to nearest even, saturates to
+// [0, 255] and sends NaN to 0 (checked on every float bit pattern against
+// clamp(rne(f), 0, 255)), so int8 needs no clamp of its own; int4 clamps to
+// [0, 15] first (the clamp commutes with rounding: integer bounds).
+template <int K>
+__device__ __forceinline__ uint32_t quant_byte(float x, float lo, float s, float y, uint32_t bits,
+                                               uint32_t acc)
 {
-    const float v = __builtin_amdgcn_fmed3f(div_rn(__fsub_rn(x, lo), s, y), 0.0f, qmax);
-    return __float_as_uint(__fadd_rn(v, 8388608.0f)) & 0xffu;
+    float v = div_rn(__fsub_rn(x, lo), s, y);
+    if (bits != 8) v = __builtin_amdgcn_fmed3f(v, 0.0f, 15.0f);
+    return __builtin_amdgcn_cvt_pk_u8_f32(v, K, acc);
 }
 
 __device__ __forceinline__ void unpack8(uint4 w, float x[8])
@@ -174,17 +231,29 @@ __device__ __forceinline__ void unpack8(uint4 w, float x[8])
     }
 }
 
-// 8 quantised values -> int8 bytes (2 dwords) or int4 nibbles (1 dword,
-// element 2i in the low nibble).
-__device__ __forceinline__ void pack8(const uint32_t q[8], uint32_t bits, uint32_t out[2])
+// 8 consecutive elements -> int8 bytes (2 dwords) or int4 nibbles (1 dword,
+// element 2i in the low nibble).  Column-dependent parameters come in
+// lo[k] / s[k] / y[k] with stride `ps` (1: per element, 0: shared).
+template <int PS>
+__device__ __forceinline__ void quant8(const float x[8], const float* lo, const float* s, const float* y,
+                                       uint32_t bits, uint32_t out[2])
 {
+    uint32_t d0 = 0, d1 = 0;
+    d0 = quant_byte<0>(x[0], lo[0], s[0], y[0], bits, d0);
+    d0 = quant_byte<1>(x[1], lo[PS], s[PS], y[PS], bits, d0);
+    d0 = quant_byte<2>(x[2], lo[2 * PS], s[2 * PS], y[2 * PS], bits, d0);
+    d0 = quant_byte<3>(x[3], lo[3 * PS], s[3 * PS], y[3 * PS], bits, d0);
+    d1 = quant_byte<0>(x[4], lo[4 * PS], s[4 * PS], y[4 * PS], bits, d1);
+    d1 = quant_byte<1>(x[5], lo[5 * PS], s[5 * PS], y[5 * PS], bits, d1);
+    d1 = quant_byte<2>(x[6], lo[6 * PS], s[6 * PS], y[6 * PS], bits, d1);
+    d1 = quant_byte<3>(x[7], lo[7 * PS], s[7 * PS], y[7 * PS], bits, d1);
     if (bits == 8) {
-        out[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-        out[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+        out[0] = d0;
+        out[1] = d1;
     } else {
-        out[0] = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) out[0] |= q[k] << (4 * k);
+        // bytes q0..q3 (each <= 15) -> byte 0 = q0 | q1 << 4, byte 2 = q2 | q3 << 4
+        const uint32_t t0 = d0 | (d0 >> 4), t1 = d1 | (d1 >> 4);
+        out[0] = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
         out[1] = 0;
     }
 }
@@ -253,27 +322,29 @@ __global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
         lo[k] = fminf(lo[k], lane_dpp<0x141>(lo[k]));
         hi[k] = fmaxf(hi[k], lane_dpp<0x141>(hi[k]));
     }
-    float sc[8], rc[8];
+    // Lane l8 forms column l8's scale and reciprocal (and stores the
+    // column's parameters); the eight lanes then share them by swizzles,
+    // which run on the LDS crossbar instead of the VALU.
+    float lo_l = lo[0], hi_l = hi[0];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        sc[k] = quant_scale(lo[k], hi[k], qmax);
-        rc[k] = recip_rn(sc[k]);
+    for (int k = 1; k < 8; ++k)
+        if (l8 == uint32_t(k)) { lo_l = lo[k]; hi_l = hi[k]; }
+    const float sc_l = quant_scale(lo_l, hi_l, qmax);
+    const float rc_l = recip_rn(sc_l);
+    {
+        const uint32_t p = g * hd + col + l8;
+        reinterpret_cast<float*>(pkt + b.qbytes)[p] = sc_l;
+        reinterpret_cast<float*>(pkt + b.qbytes + b.sbytes)[p] = lo_l;
     }
-    if (l8 == 0) {
-        const uint32_t p = g * hd + col;
-        float4* sp = reinterpret_cast<float4*>(pkt + b.qbytes) + p / 4u;
-        float4* lp = reinterpret_cast<float4*>(pkt + b.qbytes + b.sbytes) + p / 4u;
-        sp[0] = make_float4(sc[0], sc[1], sc[2], sc[3]); sp[1] = make_float4(sc[4], sc[5], sc[6], sc[7]);
-        lp[0] = make_float4(lo[0], lo[1], lo[2], lo[3]); lp[1] = make_float4(lo[4], lo[5], lo[6], lo[7]);
-    }
+    float sc[8], rc[8];
+    group8_bcast(sc_l, sc);
+    group8_bcast(rc_l, rc);
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt) {
         float x[8];
         unpack8(raw[tt], x);
-        uint32_t q[8], w[2];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = quant_one(x[k], lo[k], sc[k], rc[k], qmax);
-        pack8(q, b.bits, w);
+        uint32_t w[2];
+        quant8<1>(x, lo, sc, rc, b.bits, w);
         store_q8(pkt, (t0 + tt) * hd + col, b.bits, w);
     }
 }
@@ -319,10 +390,8 @@ __global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b)
     uint32_t w[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        uint32_t q[8], p2[2];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = quant_one(x[8 * k + i], lo, s, y, qmax);
-        pack8(q, b.bits, p2);
+        uint32_t p2[2];
+        quant8<0>(x + 8 * k, &lo, &s, &y, b.bits, p2);
         w[2 * k] = p2[0];
         w[2 * k + 1] = p2[1];
     }
