@@ -266,6 +266,7 @@ def np_codec_encode(block_bf16: np.ndarray, bits: int, kind: int, layer: int) ->
         scale = np.maximum(scale, np.float32(1e-12))
         q = np.rint(((g - low) / scale).astype(np.float32))
     q = np.clip(q, 0, (1 << bits) - 1).reshape(-1)
+    q = np.where(np.isnan(q), 0, q)  # torch's NaN -> uint8 cast gives 0 on x86
     if bits == 4:
         q = q[0::2] + 16 * q[1::2]
     q = q.astype(np.uint8)
@@ -298,8 +299,9 @@ def np_codec_decode(packet: np.ndarray, heads: int, dim: int, bits: int, kind: i
         shape, pshape = (128, heads, dim // 64, 64), (128, heads, dim // 64, 1)
     scale = params[qb // 4:(qb + sb) // 4].reshape(pshape)
     off = params[(qb + sb) // 4:(qb + 2 * sb) // 4].reshape(pshape)
-    v = (full.reshape(shape) * scale).astype(np.float32)
-    v = (v + off).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):  # 0 * inf, inf - inf -> NaN, as in torch
+        v = (full.reshape(shape) * scale).astype(np.float32)
+        v = (v + off).astype(np.float32)
     return f32_to_bf16(v.reshape(128, heads, dim))
 
 

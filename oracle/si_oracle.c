@@ -337,6 +337,17 @@ static uint64_t param_index(uint32_t kind, uint32_t heads, uint32_t dim, uint32_
     return ((uint64_t)t * heads + hh) * (dim / SI_GROUP) + dd / SI_GROUP;
 }
 
+/* x.amin / x.amax as torch computes them for a group: a NaN anywhere makes
+ * the result NaN (transport_codec.py:30-31); equal zeros order -0 < +0
+ * (IEEE 754-2019 minimum / maximum).  lo/hi start at +inf / -inf.        */
+static void minmax_update(float x, float* lo, float* hi)
+{
+    if (isnan(*lo)) return;
+    if (isnan(x)) { *lo = x; *hi = x; return; }
+    if (x < *lo || (x == *lo && signbit(x) && !signbit(*lo))) *lo = x;
+    if (x > *hi || (x == *hi && !signbit(x) && signbit(*hi))) *hi = x;
+}
+
 void si_or_codec_encode(const uint16_t* block_bf16, uint32_t heads, uint32_t dim,
                         uint32_t bits, uint32_t kind, uint32_t layer, uint8_t* packet)
 {
@@ -358,8 +369,7 @@ void si_or_codec_encode(const uint16_t* block_bf16, uint32_t heads, uint32_t dim
             for (uint32_t dd = 0; dd < dim; ++dd) {
                 float x = bf16_to_f32(block_bf16[(uint64_t)t * hd + (uint64_t)hh * dim + dd]);
                 uint64_t p = param_index(kind, heads, dim, t, hh, dd);
-                if (x < lo[p]) lo[p] = x;
-                if (x > hi[p]) hi[p] = x;
+                minmax_update(x, &lo[p], &hi[p]);
             }
     /* scale = ((high-low)/(2^bits-1)).clamp_min(1e-12), float32 throughout */
     const float floor_scale = 1e-12f;
@@ -380,7 +390,9 @@ void si_or_codec_encode(const uint16_t* block_bf16, uint32_t heads, uint32_t dim
         float q = rintf(r);
         if (q < 0.0f) q = 0.0f;
         if (q > qmax) q = qmax;
-        uint32_t qi = (uint32_t)q;
+        /* round().clamp() keeps NaN; torch's float -> uint8 cast then gives 0
+         * (the x86 conversion yields 0x80000000, whose low byte is 0). */
+        uint32_t qi = isnan(q) ? 0u : (uint32_t)q;
         if (bits == 8) {
             packet[e] = (uint8_t)qi;
         } else {

@@ -12,6 +12,9 @@
 // scale = max(fl((hi-lo)/(2^bits-1)), 1e-12f), q = clamp(rne(fl(fl(x-lo)/scale))),
 // with fl(a/scale) formed from the correctly rounded reciprocal of the
 // group's scale and one FMA correction (bit-identical to IEEE division).
+// Non-finite KV follows torch: x.amin / x.amax propagate NaN, so a group with
+// a NaN gets NaN scale and low and quantises to 0; decoding a NaN gives the
+// bf16 NaN 0x7fc0.  The bit patterns of NaN parameters are not specified.
 #include "si_kernels.h"
 
 namespace si {
@@ -162,6 +165,12 @@ __device__ __forceinline__ float lane_dpp(float v)
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
 }
 
+// x.amin / x.amax semantics (transport_codec.py:30-31): a NaN anywhere in the
+// group makes the result NaN; equal zeros order -0 < +0.  v_minimum3_f32 /
+// v_maximum3_f32 (IEEE 754-2019 minimum / maximum).
+__device__ __forceinline__ float nmin(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float nmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // v[k] = lane k's value of this lane's 8-lane group (k = 0..7): ds_swizzle
 // in bit mode, lane' = (lane & 0x18) | k within each 32 lanes.
 template <int K>
@@ -176,6 +185,7 @@ __device__ __forceinline__ void group8_bcast(float v, float out[8])
     out[4] = swz8<4>(v); out[5] = swz8<5>(v); out[6] = swz8<6>(v); out[7] = swz8<7>(v);
 }
 
+// ((hi - lo) / qmax).clamp_min(1e-12): a NaN passes through, as in torch.
 __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
 {
     const float s = __fdiv_rn(__fsub_rn(hi, lo), qmax);
@@ -309,18 +319,18 @@ __global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
         float x[8];
         unpack8(raw[tt], x);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) { lo[k] = fminf(lo[k], x[k]); hi[k] = fmaxf(hi[k], x[k]); }
+        for (int k = 0; k < 8; ++k) { lo[k] = nmin(lo[k], x[k]); hi[k] = nmax(hi[k], x[k]); }
     }
     // Min / max over the eight lanes of a chunk with DPP moves: swap within
     // pairs, then within quads, then mirror the 8-lane half-row.
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        lo[k] = fminf(lo[k], lane_dpp<0xb1>(lo[k]));
-        hi[k] = fmaxf(hi[k], lane_dpp<0xb1>(hi[k]));
-        lo[k] = fminf(lo[k], lane_dpp<0x4e>(lo[k]));
-        hi[k] = fmaxf(hi[k], lane_dpp<0x4e>(hi[k]));
-        lo[k] = fminf(lo[k], lane_dpp<0x141>(lo[k]));
-        hi[k] = fmaxf(hi[k], lane_dpp<0x141>(hi[k]));
+        lo[k] = nmin(lo[k], lane_dpp<0xb1>(lo[k]));
+        hi[k] = nmax(hi[k], lane_dpp<0xb1>(hi[k]));
+        lo[k] = nmin(lo[k], lane_dpp<0x4e>(lo[k]));
+        hi[k] = nmax(hi[k], lane_dpp<0x4e>(hi[k]));
+        lo[k] = nmin(lo[k], lane_dpp<0x141>(lo[k]));
+        hi[k] = nmax(hi[k], lane_dpp<0x141>(hi[k]));
     }
     // Lane l8 forms column l8's scale and reciprocal (and stores the
     // column's parameters); the eight lanes then share them by swizzles,
@@ -378,9 +388,9 @@ __global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b)
     for (int k = 0; k < 4; ++k) unpack8(raw[k], x + 8 * k);
     float lo = x[0], hi = x[0];
 #pragma unroll
-    for (int k = 1; k < 32; ++k) { lo = fminf(lo, x[k]); hi = fmaxf(hi, x[k]); }
-    lo = fminf(lo, lane_dpp<0xb1>(lo));
-    hi = fmaxf(hi, lane_dpp<0xb1>(hi));
+    for (int k = 1; k < 32; ++k) { lo = nmin(lo, x[k]); hi = nmax(hi, x[k]); }
+    lo = nmin(lo, lane_dpp<0xb1>(lo));
+    hi = nmax(hi, lane_dpp<0xb1>(hi));
     const float s = quant_scale(lo, hi, qmax);
     const float y = recip_rn(s);
     if (half == 0) {

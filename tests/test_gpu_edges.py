@@ -1,6 +1,7 @@
 """GPU edge cases of the layer entry points: out-of-range slot ids, K-only /
 V-only layers, record sizes that are not whole blocks, explicit IV words with
-a 32-bit counter wrap, every record tampered, codec parameter tampering.
+a 32-bit counter wrap, every record tampered, codec parameter tampering,
+NaN and infinities in the KV of the codec paths.
 All comparisons are bit-exact against OpenSSL / the oracle."""
 import numpy as np
 import pytest
@@ -203,3 +204,73 @@ def test_codec_reload_parameter_tamper(where):
     assert np.array_equal(vv[1].view(np.uint16), O.codec_decode(packets[3], heads, dim, bits, 1))
     for i, s in enumerate(slots):
         assert np.array_equal(kk[s].view(np.uint16), O.codec_decode(packets[i], heads, dim, bits, 0))
+
+
+def nonfinite_block(rng, heads, dim):
+    """bf16 block with NaN and +-inf in a few K groups / V rows."""
+    x = rng.standard_normal((128, heads, dim), dtype=np.float32)
+    x[5, 0, 3] = np.nan
+    x[70, 1, 9] = np.inf
+    x[20, 1, 100], x[30, 1, 100] = np.inf, -np.inf
+    x[99, 0, 64] = -np.inf
+    return O.f32_to_bf16(x)
+
+
+def params_match(a, b):
+    """float32 parameters equal bit for bit, NaN payloads aside."""
+    fa, fb = a.view(np.float32), b.view(np.float32)
+    na, nb_ = np.isnan(fa), np.isnan(fb)
+    return bool(np.array_equal(na, nb_) and np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb_]))
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_codec_nonfinite_kv(bits):
+    # NaN / inf in the KV: the quantisers propagate NaN through the group's
+    # min / max like x.amin / x.amax, the dequantiser turns NaN results into
+    # bf16 0x7fc0.  Writeback packets (staging) against the oracle, their
+    # ciphertext checked by the oracle's GCM decrypt; reload of the oracle's
+    # packets bit-exact against the oracle's decode.
+    rng = np.random.default_rng(77 + bits)
+    heads, dim, nb, nslots, layer = 2, 128, 2, 6, 4
+    data = np.stack([np.stack([nonfinite_block(rng, heads, dim) for _ in range(nslots)]) for _ in range(2)])
+    ck, cv = dev(data[0].view(np.int16)), dev(data[1].view(np.int16))
+    slots_np = np.array([4, 1], np.int64)
+    kinds = [0] * nb + [1] * nb
+    expect = [O.codec_encode(data[kinds[r]][slots_np[r % nb]], bits, kinds[r], layer) for r in range(2 * nb)]
+    n = expect[0].size
+    qb, sb, _ = O.codec_sizes(bits, heads, dim)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    ticket0 = 700
+    wire = W.wire_aads(KEY, SALT, n, kinds, layer, list(range(2 * nb)), ticket0)
+    staging = torch.zeros(2 * nb * W.align32(n), dtype=torch.uint8, device=DEV)
+    dw = dev(wire)
+    slots2 = dev(np.concatenate([slots_np, slots_np]))
+    sess.writeback_layer(dw, n, 2 * nb, nb, ck, cv, slots2, ticket_base=ticket0, codec_bits=bits,
+                         heads=heads, head_dim=dim, layer=layer, staging=staging)
+    st_h, ww = host(staging), host(dw)
+    h = O.hash_subkey(KEY)
+    st, toff = W.stride(n), W.align32(n)
+    for r in range(2 * nb):
+        pkt = st_h[r * toff:r * toff + n]
+        assert np.array_equal(pkt[:qb], expect[r][:qb]), f"record {r} q"
+        assert params_match(pkt[qb:qb + 2 * sb], expect[r][qb:qb + 2 * sb]), f"record {r} params"
+        assert np.array_equal(pkt[qb + 2 * sb:], expect[r][qb + 2 * sb:]), f"record {r} header"
+        o = r * st
+        status, plain = O.gcm_decrypt_verify(KEY, h, W.record_iv(SALT, ticket0 + r), ww[o + toff + 32:o + toff + 96],
+                                             ww[o:o + n], ww[o + toff:o + toff + 16].tobytes())
+        assert status == 1 and np.array_equal(plain, pkt), f"record {r} ciphertext / tag"
+    # reload of the oracle's packets
+    wire2 = W.build_wire(KEY, SALT, expect, kinds, layer, list(range(2 * nb)), ticket0 + 10)
+    ck2 = torch.zeros_like(ck)
+    cv2 = torch.zeros_like(cv)
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    stage2 = torch.zeros(2 * nb * W.align32(n), dtype=torch.uint8, device=DEV)
+    sess.reload_layer(dev(wire2), n, 2 * nb, nb, ck2, cv2, slots2, ticket_base=ticket0 + 10, codec_bits=bits,
+                      heads=heads, head_dim=dim, layer=layer, staging=stage2, fail_count=fail)
+    kk, vv = host(ck2).view(np.uint16), host(cv2).view(np.uint16)
+    assert int(host(fail)[0]) == 0
+    for i in range(nb):
+        s = slots_np[i]
+        assert np.array_equal(kk[s], O.codec_decode(expect[i], heads, dim, bits, 0)), f"K slot {s}"
+        assert np.array_equal(vv[s], O.codec_decode(expect[nb + i], heads, dim, bits, 1)), f"V slot {s}"
+        assert (kk[s] == 0x7FC0).any() and (vv[s] == 0x7FC0).any()

@@ -239,6 +239,54 @@ def test_codec_constant_group():
             assert np.array_equal(O.codec_decode(pkt, 1, 128, bits, kind), x)
 
 
+def nonfinite_block(seed: int, heads: int = 2, dim: int = 128) -> np.ndarray:
+    """bf16 block with NaN and +-inf in a few K groups / V rows."""
+    x = np.random.default_rng(seed).standard_normal((128, heads, dim), dtype=np.float32)
+    x[5, 0, 3] = np.nan                        # K (t 0-63, h0, d3);   V (t5, h0, d 0-63)
+    x[70, 1, 9] = np.inf                       # K (t 64-127, h1, d9); V (t70, h1, d 0-63)
+    x[20, 1, 100], x[30, 1, 100] = np.inf, -np.inf  # K (t 0-63, h1, d100); V (t20 / t30, h1, d 64-127)
+    x[99, 0, 64] = -np.inf                     # K (t 64-127, h0, d64); V (t99, h0, d 64-127)
+    return O.f32_to_bf16(x)
+
+
+def params_match(a: np.ndarray, b: np.ndarray) -> bool:
+    """float32 parameter arrays equal bit for bit, NaN payloads aside."""
+    fa, fb = a.view(np.float32), b.view(np.float32)
+    na, nb_ = np.isnan(fa), np.isnan(fb)
+    return bool(np.array_equal(na, nb_) and np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb_]))
+
+
+@pytest.mark.parametrize("bits,kind", [(8, 0), (8, 1), (4, 0), (4, 1)])
+def test_codec_nonfinite_inputs(bits, kind):
+    # x.amin / x.amax propagate NaN (transport_codec.py:30-31): a group with a
+    # NaN gets NaN scale and low, its q are 0 (round().clamp() keeps NaN and
+    # the uint8 cast gives 0) and it decodes to NaN; an inf makes the scale
+    # inf and the group decodes to NaN (0 * inf).  C and NumPy agree.
+    x = nonfinite_block(7 + bits + kind)
+    a = O.codec_encode(x, bits, kind, 1)
+    b = O.np_codec_encode(x, bits, kind, 1)
+    qb, sb, width = O.codec_sizes(bits, 2, 128)
+    assert np.array_equal(a[:qb], b[:qb])
+    assert params_match(a[qb:qb + 2 * sb], b[qb:qb + 2 * sb])
+    assert np.array_equal(a[qb + 2 * sb:], b[qb + 2 * sb:])
+    scale = a[qb:qb + sb].view(np.float32)
+    low = a[qb + sb:qb + 2 * sb].view(np.float32)
+    if kind == 0:
+        nan_p, inf_p = (0 * 2 + 0) * 128 + 3, (1 * 2 + 1) * 128 + 9   # param (group, h, d)
+    else:
+        nan_p, inf_p = (5 * 2 + 0) * 2 + 0, (70 * 2 + 1) * 2 + 0      # param (t, h, dim group)
+    assert np.isnan(scale[nan_p]) and np.isnan(low[nan_p])
+    assert np.isinf(scale[inf_p])
+    y = O.codec_decode(a, 2, 128, bits, kind)
+    assert np.array_equal(y, O.np_codec_decode(a, 2, 128, bits, kind))
+    if kind == 0:
+        assert np.all(y[0:64, 0, 3] == 0x7FC0) and np.all(y[64:128, 1, 9] == 0x7FC0)
+    else:
+        assert np.all(y[5, 0, 0:64] == 0x7FC0) and np.all(y[70, 1, 0:64] == 0x7FC0)
+    fin = np.isfinite(O.bf16_to_f32(y))
+    assert fin.sum() > 0.9 * fin.size
+
+
 def test_codec_widths_match_reference_shapes():
     assert O.codec_sizes(8, 8, 128)[2] == 147472
     assert O.codec_sizes(4, 8, 128)[2] == 81936
