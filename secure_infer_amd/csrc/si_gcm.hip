@@ -585,7 +585,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     // the set-up; a straddling workgroup keeps segment 0's products and both
     // multipliers there until after the rows), 9984 a zero word, [9985, 9995) the two record views,
     // [9995, 9997) their tag masks E_K(J0), [9997, 10009) the wave sums of a
-    // straddling workgroup's segment 0.
+    // straddling workgroup's segment 0, [10009, 10011) the expected tags.
     __shared__ uint4 s_lds[10240];
     const uint4* const g_u = s_lds;
     const uint4* const g_u2 = s_lds + 512;
@@ -603,6 +603,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     uint4* const s_view = s_lds + 9985;
     uint4* const s_ek = s_lds + 9995;
     uint4* const s_c0 = s_lds + 9997;
+    uint4* const s_tag = s_lds + 10009;  // expected tags of the two records (decrypt, verify)
 
     constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
     const uint32_t tid = threadIdx.x;
@@ -687,6 +688,23 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     };
     uint4 p = segment(0);
     if (nseg == 2) p = segment(1);
+    // The expected tag of each record, loaded now so that the read is off the
+    // finalising workgroup's critical path (it is needed after the ticket).
+    // Lanes 0 and 1 read different views, so the pointer stays per lane
+    // (RecView::tag is bytes 24..31 of the view: word 1, .z/.w).
+    uint4 tag_pre = make_uint4(0, 0, 0, 0);
+    if (kMode != MODE_ENCRYPT && tid < nseg) {
+        static_assert(offsetof(RecView, tag) == 24, "view word 1, high half");
+        const uint4 w1 = s_view[5 * tid + 1];
+        const uint8_t* tp = reinterpret_cast<const uint8_t*>(uint64_t(w1.z) | (uint64_t(w1.w) << 32));
+        if ((reinterpret_cast<uintptr_t>(tp) & 15u) == 0) {
+            tag_pre = gload4(tp);
+        } else {
+            uint32_t w4[4];
+            load_block<false>(tp, 16u, w4);
+            tag_pre = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+    }
     __syncthreads();  // AES and GHASH tables are dead from here on
 
     // The last segment's products to LDS; placement t is shared by the three
@@ -775,6 +793,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         }
         s_last[s] = last;
         s_fin[s][0] = r4[0]; s_fin[s][1] = r4[1]; s_fin[s][2] = r4[2]; s_fin[s][3] = r4[3];
+        s_tag[s] = tag_pre;
     }
     __syncthreads();
 
@@ -791,9 +810,8 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
             }
             continue;
         }
-        uint32_t diff = 0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) diff |= uint32_t(uint8_t(s_fin[s][k >> 2] >> (8 * (k & 3))) ^ gmem(v.tag)[k]);
+        const uint4 et = s_tag[s];
+        const uint32_t diff = (s_fin[s][0] ^ et.x) | (s_fin[s][1] ^ et.y) | (s_fin[s][2] ^ et.z) | (s_fin[s][3] ^ et.w);
         const uint32_t ok = (diff == 0 && !v.bad) ? 1u : 0u;
         if (tid == 0) {
             *gmem(v.status) = ok;
