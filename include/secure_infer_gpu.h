@@ -274,7 +274,7 @@ const char* secure_infer_gpu_version(void);
  * the tests (small values force shares that straddle records). */
 int secure_infer_gpu_set_chunk_rows(int jmax);
 /* Tuning: cost, in rows, charged to a workgroup share that straddles two
- * records when the launch lays out its shares, 0..256 (default 10); 0 lets
+ * records when the launch lays out its shares, 0..256 (default 6); 0 lets
  * shares straddle wherever a record ends inside one.  No reference
  * counterpart; used by the tests to force straddling shares. */
 int secure_infer_gpu_set_straddle_rows(int rows);

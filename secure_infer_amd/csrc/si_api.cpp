@@ -245,9 +245,10 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
 int g_min_rows = 3;
 // Cost, in rows, of a share that straddles two records (its second set of
 // boundary rows, the second placement table and the two-product shares);
-// MI355X, bf16 Llama-3-8B layer: 37.8 / 36.6 / 34.2 / 36.2 / 37.2 us per
-// layer at 4 / 7 / 10 / 12 / 16.
-uint32_t g_straddle_rows = 10;
+// MI355X, bf16 Llama-3-8B layer: 35.1 / 34.8 / 32.2 / 32.2 / 32.6 / 32.7 /
+// 33.9 us per layer at 2 / 4 / 6 / 7 / 8 / 10 / 13 (int4 Qwen2.5-7B: 35.8 us
+// at 4, 26.6 at 2 and 6..13; int8 and the 70B writeback flat from 6 to 10).
+uint32_t g_straddle_rows = 6;
 
 // Compute units of the current device (one record-kernel workgroup each: its
 // LDS use).
@@ -265,7 +266,10 @@ uint32_t cu_count()
     return uint32_t(cus[dev]);
 }
 
-si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
+// The rows cover AAD || C; the length block L, the last block of the GHASH
+// input, adds L * H to every record's sum (the same for the whole batch), and
+// the kernel's placement exponents count one more for it.
+si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, const uint8_t h[16])
 {
     si::Sched s{};
     s.nrec = nrec;
@@ -273,8 +277,16 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
     s.aad_bytes = uint32_t(aad_bytes);
     s.a = uint32_t((aad_bytes + 15) / 16);
     s.n = uint32_t((bytes + 15) / 16);
-    const uint64_t m = uint64_t(s.a) + s.n + 1;
-    s.rows = uint32_t((m + SI_T - 1) / SI_T);
+    const uint64_t m = uint64_t(s.a) + s.n;
+    s.rows = m ? uint32_t((m + SI_T - 1) / SI_T) : 1u;
+    {
+        Blk len{}, hb;
+        put_be64(len.b, aad_bytes * 8u);
+        put_be64(len.b + 8, bytes * 8u);
+        memcpy(hb.b, h, 16);
+        const Blk lh = gf_mul(len, hb);
+        for (int k = 0; k < 4; ++k) s.lh[k] = le32(lh.b + 4 * k);
+    }
     // W workgroups, one per CU, none with fewer than g_min_rows rows, and at
     // least nrec of them (rounded to whole rounds of one per CU) so that no
     // share spans more than R rows, i.e. two records at most.
@@ -397,7 +409,7 @@ int run_single(int mode, hipStream_t stream, void* src, void* key, void* h, void
     b.status = static_cast<uint32_t*>(status);
     b.ks = static_cast<const uint8_t*>(ks);
     for (int k = 0; k < 4; ++k) b.iv[k] = iv[k];
-    const si::Sched s = make_sched(1, bytes, aad_bytes);
+    const si::Sched s = make_sched(1, bytes, aad_bytes, c->h);
     const bool al = aligned16(src) && (!dst || aligned16(dst)) && (!ks || aligned16(ks));
     return si::launch_gcm(mode, stream, c->dev, b, s, acc, al) == hipSuccess ? 0 : -1;
 }
@@ -561,7 +573,7 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
         b.staging = static_cast<uint8_t*>(d->staging);
         b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
     }
-    const si::Sched sc = make_sched(d->nrec, d->bytes, 64);
+    const si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     if (si::launch_gcm(0, stream, s->ctx->dev, b, sc, acc, al) != hipSuccess) return -1;
     if (codec) {
@@ -638,7 +650,7 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
         cb.width = d->bytes;
         if (si::launch_gather_quant(stream, cb) != hipSuccess) return -1;
     }
-    const si::Sched sc = make_sched(d->nrec, d->bytes, 64);
+    const si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     return si::launch_gcm(1, stream, s->ctx->dev, b, sc, acc, al) == hipSuccess ? 0 : -1;
 }

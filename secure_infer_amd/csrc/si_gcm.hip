@@ -2,8 +2,10 @@
 //
 // One launch processes a batch of records.  Each record's GHASH input is the
 // block sequence X = AAD || C || L (SP 800-38D), m = a + n + 1 blocks, and
-// GHASH = XOR_k X_k * H^(m-k).  X is cut into R rows of T = 256 blocks
-// counted from its end (row R-1 ends with L; row 0 may start before X).  A
+// GHASH = XOR_k X_k * H^(m-k).  AAD || C (m - 1 blocks) is cut into R rows
+// of T = 256 blocks counted from its end (row R-1 ends with the last
+// ciphertext block; row 0 may start before X); the length block L adds L * H,
+// the same for every record of a batch (passed in by the host).  A
 // workgroup of three 256-thread units takes a contiguous share of the
 // records' concatenated rows (laid out by the host; one or two records);
 // thread t of a unit owns block t of each of its rows, so every row is one
@@ -182,8 +184,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
 }
 
-// One general row: any mix of AAD / ciphertext / length blocks, partial
-// blocks and unaligned buffers.  Used for the few rows at a record's ends.
+// One general row: any mix of padding, AAD and ciphertext blocks, partial
+// blocks and unaligned buffers.  Used for the rows at a record's ends.
 template <int kMode, bool kAligned, bool kWT>
 __device__ __forceinline__ void row_general(const Sched& sch, const RecView& v,
                                             const uint32_t* aes, AesLane lane, const AesKeys& keys,
@@ -232,13 +234,7 @@ __device__ __forceinline__ void row_general(const Sched& sch, const RecView& v,
         const uint32_t valid = uint32_t(i) == sch.a - 1 ? aad_tail : 16u;
         load_block<false>(v.aad + 16 * i, valid, x);
     } else {
-        // length block [len(A)]_64 || [len(C)]_64 in bits, big-endian
-        const uint64_t abits = uint64_t(sch.aad_bytes) * 8u;
-        const uint64_t cbits = sch.bytes * 8u;
-        x[0] = bswap32(uint32_t(abits >> 32));
-        x[1] = bswap32(uint32_t(abits));
-        x[2] = bswap32(uint32_t(cbits >> 32));
-        x[3] = bswap32(uint32_t(cbits));
+        return;  // past the ciphertext (the rows end with it)
     }
     y[0] ^= x[0]; y[1] ^= x[1]; y[2] ^= x[2]; y[3] ^= x[3];
 }
@@ -445,7 +441,8 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
 // Rows [qa, qb) of one record, shared by the workgroup's SI_U units: unit u
 // takes the segment rows j = u + SI_U*i, i = 0..nu-1, and runs Horner with
 // H^(SI_U*T) over them into y.  Row q of the record holds blocks
-// m - (R - q)*T + t (row R-1 ends with the length block).
+// m' - (R - q)*T + t of AAD || C (m' = a + n; row R-1 ends with the last
+// ciphertext block).
 template <int kMode, bool kAligned, bool kWT>
 __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const Sched& sch, const RecView& v, const uint4* gh,
                                           const uint4* gh2, const uint32_t* aes, AesLane lane,
@@ -455,7 +452,7 @@ __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const 
     const uint32_t n0 = bswap32(v.iv[0]) ^ ctx->rk[0];
     const uint32_t n1 = bswap32(v.iv[1]) ^ ctx->rk[1];
     const uint32_t n2 = bswap32(v.iv[2]) ^ ctx->rk[2];
-    const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
+    const int64_t m = int64_t(sch.a) + int64_t(sch.n);  // AAD || C
     const int64_t base = m - int64_t(sch.rows - qa) * SI_T;  // first block of segment row 0
     const uint32_t J = qb - qa;
     const uint32_t nu = u < J ? (J - u + SI_U - 1) / SI_U : 0u;
@@ -515,14 +512,15 @@ __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const 
 }
 
 // Placement multiplier of thread position t for a segment ending at row qb:
-// H^((R - qb)*T + T - t), the exponent of the thread's last block in the
-// segment; a thread whose blocks all precede X carries zero and takes H^0.
+// H^((R - qb)*T + T - t + 1), the exponent of the thread's last block in the
+// segment (+1: the length block follows the ciphertext); a thread whose
+// blocks all precede X carries zero and takes H^0.
 __device__ __forceinline__ uint4 placement_power(const GcmCtx* __restrict__ ctx, const Sched& sch,
                                                  uint32_t qb, uint32_t t)
 {
-    const int64_t m = int64_t(sch.a) + int64_t(sch.n) + 1;
+    const int64_t m = int64_t(sch.a) + int64_t(sch.n);
     const int64_t l = m - int64_t(sch.rows - qb + 1) * SI_T + t;
-    const uint64_t e = l >= 0 ? uint64_t(sch.rows - qb) * SI_T + SI_T - t : 0u;
+    const uint64_t e = l >= 0 ? uint64_t(sch.rows - qb) * SI_T + SI_T - t + 1 : 0u;
     return reinterpret_cast<const uint4*>(ctx + 1)[e];
 }
 
@@ -763,9 +761,10 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
             const uint4 e = red[w];
             r4[0] ^= e.x; r4[1] ^= e.y; r4[2] ^= e.z; r4[3] ^= e.w;
         }
-        if (qb == sch.rows) {  // the record's tag mask
+        if (qb == sch.rows) {  // the record's tag mask and its length block's term
             const uint4 e = s_ek[s];
-            r4[0] ^= e.x; r4[1] ^= e.y; r4[2] ^= e.z; r4[3] ^= e.w;
+            r4[0] ^= e.x ^ sch.lh[0]; r4[1] ^= e.y ^ sch.lh[1];
+            r4[2] ^= e.z ^ sch.lh[2]; r4[3] ^= e.w ^ sch.lh[3];
         }
         uint32_t last = 1;
         if (qa != 0 || qb != sch.rows) {

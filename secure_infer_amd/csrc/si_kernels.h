@@ -46,7 +46,7 @@ struct RecBatch {
 // Work decomposition shared by all records of a batch (uniform sizes).
 struct Sched {
     uint32_t nrec;       // records
-    uint32_t rows;       // R: rows of T blocks per record, ceil((a + n + 1) / T)
+    uint32_t rows;       // R: rows of T blocks per record, ceil((a + n) / T) (at least 1)
     uint32_t nwg;        // W workgroups, W >= nrec (a share never spans more than R rows)
     uint32_t use_starts; // 1: workgroup w owns rows [starts[w], starts[w+1]); 0: an equal split
     uint32_t starts[SI_MAX_WG + 1];  // share boundaries in the records' concatenated rows
@@ -54,6 +54,7 @@ struct Sched {
     uint32_t n;          // payload blocks
     uint32_t aad_bytes;
     uint64_t bytes;      // payload bytes
+    uint32_t lh[4];      // L * H, L = [len(A)]_64 || [len(C)]_64: the length block's GHASH term
 };
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                       const Sched& s, RecAcc* acc, bool aligned);

@@ -293,7 +293,7 @@ class GcmSession:
 
 
 DEFAULT_CHUNK_ROWS = 3
-DEFAULT_STRADDLE_ROWS = 10
+DEFAULT_STRADDLE_ROWS = 6
 
 
 def set_chunk_rows(jmax: int) -> None:

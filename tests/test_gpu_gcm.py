@@ -149,7 +149,7 @@ def make_caches(nslots, heads, dim, fill=0x3C):
     return k, v
 
 
-@pytest.mark.parametrize("chunk_rows,straddle", [(16, 10), (1, 10), (3, 0), (16, 0), (64, 0)])
+@pytest.mark.parametrize("chunk_rows,straddle", [(16, 10), (1, 10), (3, 6), (3, 0), (16, 0), (64, 0)])
 def test_reload_layer_bf16(chunk_rows, straddle):
     rng = np.random.default_rng(21)
     heads, dim, nb, nslots, layer = 8, 128, 6, 32, 4
