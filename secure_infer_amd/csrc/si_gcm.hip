@@ -232,7 +232,10 @@ __device__ __forceinline__ void row_general(const Sched& sch, const RecView& v,
         }
     } else if (i < int64_t(sch.a)) {
         const uint32_t valid = uint32_t(i) == sch.a - 1 ? aad_tail : 16u;
-        load_block<false>(v.aad + 16 * i, valid, x);
+        if ((reinterpret_cast<uintptr_t>(v.aad) & 15u) == 0)  // the wire record's AAD is
+            load_block<true>(v.aad + 16 * i, valid, x);       // 32-byte aligned
+        else
+            load_block<false>(v.aad + 16 * i, valid, x);
     } else {
         return;  // past the ciphertext (the rows end with it)
     }
