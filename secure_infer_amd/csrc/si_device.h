@@ -533,13 +533,28 @@ __device__ __forceinline__ void gh_mul_part(const uint32_t (&x_mem)[NS][4], cons
     }
 }
 
-// XOR-reduce four words across a wave64.
-__device__ __forceinline__ void wave_xor4(uint32_t v[4])
+// XOR of four words over a wave64, valid in lane 63, by DPP moves only (no
+// LDS crossbar round trips): swap within pairs and quads, mirror 8 and 16
+// lanes (every lane then holds its row's XOR), then row_bcast:15 into rows 1
+// and 3 and row_bcast:31 into rows 2 and 3.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_xor(uint32_t v)
+{
+    return v ^ uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kCtrl, kRowMask, 0xf, false));
+}
+
+__device__ __forceinline__ void wave_xor4_to63(uint32_t v[4])
 {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] ^= __shfl_xor(v[k], off, 64);
+    for (int k = 0; k < 4; ++k) {
+        uint32_t x = v[k];
+        x = dpp_xor<0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
+        x = dpp_xor<0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
+        x = dpp_xor<0x141, 0xf>(x);  // row_half_mirror
+        x = dpp_xor<0x140, 0xf>(x);  // row_mirror
+        x = dpp_xor<0x142, 0xa>(x);  // row_bcast:15 -> rows 1, 3
+        x = dpp_xor<0x143, 0xc>(x);  // row_bcast:31 -> rows 2, 3
+        v[k] = x;
     }
 }
 

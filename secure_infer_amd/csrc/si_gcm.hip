@@ -744,11 +744,11 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         if (u == 0) gh_mul_part<3, 0, 2>(w, tb, s_zero, t, SI_T, q);
         else if (u == 1) gh_mul_part<3, 1, 2>(w, tb, s_zero, t, SI_T, q);
         else gh_mul_part<3, 2, 2>(w, tb, s_zero, t, SI_T, q);
-        wave_xor4(q[0]);
-        if ((tid & 63u) == 0) s_c0[tid >> 6] = make_uint4(q[0][0], q[0][1], q[0][2], q[0][3]);
+        wave_xor4_to63(q[0]);
+        if ((tid & 63u) == 63u) s_c0[tid >> 6] = make_uint4(q[0][0], q[0][1], q[0][2], q[0][3]);
     }
-    wave_xor4(q[1]);
-    if ((tid & 63u) == 0) s_red[tid >> 6] = make_uint4(q[1][0], q[1][1], q[1][2], q[1][3]);
+    wave_xor4_to63(q[1]);
+    if ((tid & 63u) == 63u) s_red[tid >> 6] = make_uint4(q[1][0], q[1][1], q[1][2], q[1][3]);
     // Every wave's data stores must be complete (write-through) or at least
     // in L2 (before the ticket's release) when the ticket is taken;
     // s_barrier does not wait for them.
