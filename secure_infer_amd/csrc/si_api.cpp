@@ -280,6 +280,10 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, const ui
     const uint64_t m = uint64_t(s.a) + s.n;
     s.rows = m ? uint32_t((m + SI_T - 1) / SI_T) : 1u;
     {
+        const uint64_t pad = uint64_t(s.rows) * SI_T - m;  // blocks of row 0 before X
+        s.ek_row0 = (s.a >= 1 && s.n >= 1 && pad + s.a <= SI_T - 1) ? 1u : 0u;
+    }
+    {
         Blk len{}, hb;
         put_be64(len.b, aad_bytes * 8u);
         put_be64(len.b + 8, bytes * 8u);

@@ -185,30 +185,35 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p)
 }
 
 // One general row: any mix of padding, AAD and ciphertext blocks, partial
-// blocks and unaligned buffers.  Used for the rows at a record's ends.
+// blocks and unaligned buffers.  Used for the rows at a record's ends.  When
+// ek_dst is given (the record's row 0), the lane of AAD block a-1 forms the
+// tag mask E_K(J0) (counter 1) in the same keystream pass as the ciphertext
+// lanes and stores it there.
 template <int kMode, bool kAligned, bool kWT>
 __device__ __forceinline__ void row_general(const Sched& sch, const RecView& v,
                                             const uint32_t* aes, AesLane lane, const AesKeys& keys,
                                             uint32_t n0, uint32_t n1, uint32_t n2, int64_t i,
-                                            uint32_t tail, uint32_t aad_tail, uint32_t y[4])
+                                            uint32_t tail, uint32_t aad_tail, uint4* ek_dst,
+                                            uint32_t y[4])
 {
     if (i < 0) return;
+    const bool ct = i >= int64_t(sch.a) && i < int64_t(sch.a) + int64_t(sch.n);
+    const bool ek = ek_dst != nullptr && i == int64_t(sch.a) - 1;
+    if (ct && v.skip) return;
+    const uint64_t k = ct ? uint64_t(i - sch.a) : 0u;
+    uint32_t ks[4] = {0, 0, 0, 0};
+    if ((ct && (kMode == MODE_DECRYPT || kMode == MODE_ENCRYPT)) || ek)
+        aes_ctr_block(aes, lane, keys, n0, n1, n2, ek ? 1u : v.iv[3] + uint32_t(k), ks);
+    if (ek) *ek_dst = make_uint4(ks[0], ks[1], ks[2], ks[3]);
     uint32_t x[4];
-    if (i >= int64_t(sch.a) && i < int64_t(sch.a) + int64_t(sch.n)) {
-        if (v.skip) return;
-        const uint64_t k = uint64_t(i - sch.a);
+    if (ct) {
         const uint32_t valid = k == uint64_t(sch.n) - 1 ? tail : 16u;
         uint32_t in[4];
         load_block<kAligned>(v.src + 16 * k, valid, in);
         if (kMode == MODE_VERIFY) {
             x[0] = in[0]; x[1] = in[1]; x[2] = in[2]; x[3] = in[3];
         } else {
-            uint32_t ks[4];
-            if (kMode == MODE_VERIFY_XOR) {
-                load_block<kAligned>(v.ks + 16 * k, valid, ks);
-            } else {
-                aes_ctr_block(aes, lane, keys, n0, n1, n2, v.iv[3] + uint32_t(k), ks);
-            }
+            if (kMode == MODE_VERIFY_XOR) load_block<kAligned>(v.ks + 16 * k, valid, ks);
             uint32_t out[4] = {in[0] ^ ks[0], in[1] ^ ks[1], in[2] ^ ks[2], in[3] ^ ks[3]};
             if (kWT)  // every payload block is a full aligned block
                 st_wt(rsrc_of(v.dst), k, make_uint4(out[0], out[1], out[2], out[3]));
@@ -450,7 +455,7 @@ template <int kMode, bool kAligned, bool kWT>
 __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const Sched& sch, const RecView& v, const uint4* gh,
                                           const uint4* gh2, const uint32_t* aes, AesLane lane,
                                           const AesKeys& keys, uint32_t t, uint32_t u, uint32_t qa,
-                                          uint32_t qb, uint32_t y[4])
+                                          uint32_t qb, uint4* ek_slot, uint32_t y[4])
 {
     const uint32_t n0 = bswap32(v.iv[0]) ^ ctx->rk[0];
     const uint32_t n1 = bswap32(v.iv[1]) ^ ctx->rk[1];
@@ -481,11 +486,15 @@ __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const 
     if (i1 > nu) i1 = nu;
     if (i0 > i1) i0 = i1;
 
+    // Record row 0 (qa = 0: unit 0's first row; general, before or after the
+    // fast rows) carries the tag-mask job when the batch puts it there.
+    uint4* const ek_row = (sch.ek_row0 && qa == 0 && u == 0) ? ek_slot : nullptr;
     y[0] = y[1] = y[2] = y[3] = 0;
     for (uint32_t i = 0; i < i0; ++i) {
         if (i != 0) gh_mul_table(gh, y);
         row_general<kMode, kAligned, kWT>(sch, v, aes, lane, keys, n0, n1, n2,
-                                          base + int64_t(u + SI_U * i) * SI_T + t, tail, aad_tail, y);
+                                          base + int64_t(u + SI_U * i) * SI_T + t, tail, aad_tail,
+                                          i == 0 ? ek_row : nullptr, y);
     }
     if (i1 > i0) {
         // Drain the key / descriptor loads so the loop's memory waits only
@@ -510,7 +519,8 @@ __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const 
     for (uint32_t i = i1; i < nu; ++i) {
         if (i != 0) gh_mul_table(gh, y);
         row_general<kMode, kAligned, kWT>(sch, v, aes, lane, keys, n0, n1, n2,
-                                          base + int64_t(u + SI_U * i) * SI_T + t, tail, aad_tail, y);
+                                          base + int64_t(u + SI_U * i) * SI_T + t, tail, aad_tail,
+                                          i == 0 ? ek_row : nullptr, y);
     }
 }
 
@@ -657,9 +667,11 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     AesKeys keys;
     load_keys(ctx, keys);
     __syncthreads();
-    // Tag masks E_K(J0) of the records whose last row ends a segment here
-    // (lanes 0 and 1 of wave 0, before their rows, so nobody waits on them).
-    if (tid < nseg && (tid ? qb1 : qb0) == sch.rows) {
+    // Tag masks E_K(J0): formed in row 0's keystream pass when that row has
+    // ciphertext lanes (the segment that starts a record adds it); otherwise
+    // here, for the record whose last row ends a segment (lanes 0 and 1 of
+    // wave 0, before their rows).
+    if (!sch.ek_row0 && tid < nseg && (tid ? qb1 : qb0) == sch.rows) {
         const RecView v = get_view(s_view + 5 * tid);
         uint32_t ek[4];
         aes_ctr_block(aes, aes_lane(tid), keys, bswap32(v.iv[0]) ^ ctx->rk[0], bswap32(v.iv[1]) ^ ctx->rk[1],
@@ -675,7 +687,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         const uint32_t qa = s ? 0u : qa0, qb = s ? qb1 : qb0;
         const RecView v = get_view(s_view + 5 * s);
         uint32_t y[4];
-        unit_rows<kMode, kAligned, kWT>(ctx, sch, v, g_u, g_u2, aes, lane, keys, t, u, qa, qb, y);
+        unit_rows<kMode, kAligned, kWT>(ctx, sch, v, g_u, g_u2, aes, lane, keys, t, u, qa, qb, s_ek + s, y);
         // d = segment rows after the unit's last row (0 when it has none).
         const uint32_t J = qb - qa;
         const uint32_t d = u < J ? (J - 1 - u) % SI_U : 0u;
@@ -764,10 +776,12 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
             const uint4 e = red[w];
             r4[0] ^= e.x; r4[1] ^= e.y; r4[2] ^= e.z; r4[3] ^= e.w;
         }
-        if (qb == sch.rows) {  // the record's tag mask and its length block's term
+        if (sch.ek_row0 ? qa == 0 : qb == sch.rows) {  // the record's tag mask
             const uint4 e = s_ek[s];
-            r4[0] ^= e.x ^ sch.lh[0]; r4[1] ^= e.y ^ sch.lh[1];
-            r4[2] ^= e.z ^ sch.lh[2]; r4[3] ^= e.w ^ sch.lh[3];
+            r4[0] ^= e.x; r4[1] ^= e.y; r4[2] ^= e.z; r4[3] ^= e.w;
+        }
+        if (qb == sch.rows) {  // the length block's term
+            r4[0] ^= sch.lh[0]; r4[1] ^= sch.lh[1]; r4[2] ^= sch.lh[2]; r4[3] ^= sch.lh[3];
         }
         uint32_t last = 1;
         if (qa != 0 || qb != sch.rows) {

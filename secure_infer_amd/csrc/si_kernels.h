@@ -55,6 +55,8 @@ struct Sched {
     uint32_t aad_bytes;
     uint64_t bytes;      // payload bytes
     uint32_t lh[4];      // L * H, L = [len(A)]_64 || [len(C)]_64: the length block's GHASH term
+    uint32_t ek_row0;    // 1: row 0 holds AAD block a-1 and a ciphertext block, and the tag
+                         // mask E_K(J0) rides on row 0's keystream pass
 };
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                       const Sched& s, RecAcc* acc, bool aligned);
