@@ -283,13 +283,12 @@ __device__ __forceinline__ void store_header(const CodecBatch& b, uint8_t* pkt, 
 
 // K: eight lanes per (token group of 64, 8 consecutive columns), each lane 8
 // tokens held in registers; the column min / max is reduced across the eight
-// lanes, so the slot is read once.  Grid (x, K record).
-__global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
+// lanes, so the slot is read once.  Workgroup bx of K record r.
+__device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, uint32_t bx)
 {
-    const uint32_t r = blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nch = hd / 8u;
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t idx = bx * 256u + threadIdx.x;
     // Whole 8-lane groups take the same branch (shuffle partners stay active).
     if (idx >= 2u * nch * 8u) return;
     const int64_t sid = b.slots[r];
@@ -362,12 +361,11 @@ __global__ __launch_bounds__(256) void quant_k_kernel(CodecBatch b)
 
 // V: two lanes per (token, head, dim group of 64), 32 consecutive elements
 // each; the group's min / max meets in one DPP swap, and the group's scale
-// and reciprocal are formed once per 32 elements.  Grid (x, V record).
-__global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b)
+// and reciprocal are formed once per 32 elements.  Workgroup bx of V record r.
+__device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, uint32_t bx)
 {
-    const uint32_t r = b.n_k + blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t idx = bx * 256u + threadIdx.x;
     const uint32_t ngroups = 2u * hd;  // 128 * hd / 64
     // Lane pairs (2i, 2i+1) take the same branch, so the swap below always
     // meets an active partner.
@@ -414,6 +412,22 @@ __global__ __launch_bounds__(256) void quant_v_kernel(CodecBatch b)
     }
 }
 
+// Both kinds in one launch: the kx workgroups of each K record, then the vx
+// of each V record.  The K blocks are bound by their strided slot reads (8
+// token rows per lane), the V blocks stream; in one grid the V blocks fill
+// the machine while the K blocks drain (MI355X, Llama-3-70B int4 layer: 22.7
+// + 18.8 us as two launches, 6.5 us less per layer as one).
+__global__ __launch_bounds__(256) void quant_kernel(CodecBatch b, uint32_t kx, uint32_t vx)
+{
+    const uint32_t nkb = kx * b.n_k;
+    if (blockIdx.x < nkb) {
+        quant_k_block(b, blockIdx.x / kx, blockIdx.x % kx);
+    } else {
+        const uint32_t v = blockIdx.x - nkb;
+        quant_v_block(b, b.n_k + v / vx, v % vx);
+    }
+}
+
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b)
 {
     // Tokens per thread: the most that still leaves >= 1024 workgroups (four
@@ -433,10 +447,9 @@ hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b)
 {
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nv = b.nrec - b.n_k;
-    if (b.n_k)
-        hipLaunchKernelGGL(quant_k_kernel, dim3((2u * hd + 255u) / 256u, b.n_k), dim3(256), 0, stream, b);
-    if (nv)
-        hipLaunchKernelGGL(quant_v_kernel, dim3((4u * hd + 255u) / 256u, nv), dim3(256), 0, stream, b);
+    const uint32_t kx = (2u * hd + 255u) / 256u, vx = (4u * hd + 255u) / 256u;
+    if (b.n_k + nv)
+        hipLaunchKernelGGL(quant_kernel, dim3(kx * b.n_k + vx * nv), dim3(256), 0, stream, b, kx, vx);
     return hipGetLastError();
 }
 
