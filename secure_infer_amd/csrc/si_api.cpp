@@ -249,6 +249,11 @@ int g_min_rows = 3;
 // 33.9 us per layer at 2 / 4 / 6 / 7 / 8 / 10 / 13 (int4 Qwen2.5-7B: 35.8 us
 // at 4, 26.6 at 2 and 6..13; int8 and the 70B writeback flat from 6 to 10).
 uint32_t g_straddle_rows = 6;
+// Fixed cost of a record-kernel workgroup, in rows (MI355X: set-up ~3.2 us,
+// placement ~1.5 us and finalisation ~0.35 us at ~1 us per row per CU), and
+// whether shares of two whole records may be laid out.
+uint32_t g_wg_fixed_rows = 5;
+bool g_pair_records = true;
 
 // Compute units of the current device (one record-kernel workgroup each: its
 // LDS use).
@@ -338,6 +343,21 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, const ui
         const uint64_t n = lay(lo, true);
         for (uint64_t i = n + 1; i <= w; ++i) s.starts[i] = uint32_t(G);
         s.use_starts = 1;
+        // More records than CUs: the layout above runs in rounds, each
+        // workgroup paying the fixed cost.  A workgroup that takes two whole
+        // records pays it once for both (one placement table serves both, as
+        // each ends at row R); taken when its estimated time per CU is lower.
+        if (g_pair_records && nrec > cus) {
+            const uint64_t wp = (uint64_t(nrec) + 1) / 2, F = g_wg_fixed_rows;
+            const uint64_t cost_rows = (w + cus - 1) / cus * (lo + F);
+            const uint64_t cost_pairs = (wp + cus - 1) / cus * (2ull * R + F + 1);
+            if (cost_pairs < cost_rows && wp <= SI_MAX_WG) {
+                s.nwg = uint32_t(wp);
+                for (uint64_t i = 0; i <= wp; ++i)
+                    s.starts[i] = uint32_t((2 * i < nrec ? 2 * i : nrec) * R);
+                s.pairs = 1;
+            }
+        }
     }
     return s;
 }
@@ -350,10 +370,13 @@ uint32_t npow_for(uint64_t bytes, uint64_t aad_bytes)
 std::mutex g_lock;
 std::vector<std::unique_ptr<DevCtx>> g_ctx_cache;  // compat entry points, keyed by (key, H)
 
-// Per-stream accumulator workspaces.
+// Per-stream accumulator workspaces (and the parking area of two-record
+// shares).
 struct Workspace {
     si::RecAcc* acc = nullptr;
     size_t cap = 0;
+    uint4* park = nullptr;
+    size_t park_cap = 0;
 };
 std::unordered_map<hipStream_t, Workspace> g_ws;
 
@@ -373,6 +396,23 @@ si::RecAcc* workspace(hipStream_t stream, size_t nrec)
     if (hipMemset(w.acc, 0, cap * sizeof(si::RecAcc)) != hipSuccess) return nullptr;
     w.cap = cap;
     return w.acc;
+}
+
+// Parking area for nwg two-record workgroups (one uint4 per thread).
+uint4* park_area(hipStream_t stream, size_t nwg)
+{
+    Workspace& w = g_ws[stream];
+    const size_t need = nwg * SI_NT;
+    if (w.park_cap >= need) return w.park;
+    if (w.park) {
+        if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+        (void)hipFree(w.park);
+        w.park = nullptr;
+        w.park_cap = 0;
+    }
+    if (hipMalloc(&w.park, need * sizeof(uint4)) != hipSuccess) return nullptr;
+    w.park_cap = need;
+    return w.park;
 }
 
 DevCtx* ctx_for_device_key(hipStream_t stream, const void* key, const void* h, uint32_t npow)
@@ -577,7 +617,8 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
         b.staging = static_cast<uint8_t*>(d->staging);
         b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
     }
-    const si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    if (sc.pairs && !(sc.park = park_area(stream, sc.nwg))) return -1;
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     if (si::launch_gcm(0, stream, s->ctx->dev, b, sc, acc, al) != hipSuccess) return -1;
     if (codec) {
@@ -654,7 +695,8 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
         cb.width = d->bytes;
         if (si::launch_gather_quant(stream, cb) != hipSuccess) return -1;
     }
-    const si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    if (sc.pairs && !(sc.park = park_area(stream, sc.nwg))) return -1;
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     return si::launch_gcm(1, stream, s->ctx->dev, b, sc, acc, al) == hipSuccess ? 0 : -1;
 }

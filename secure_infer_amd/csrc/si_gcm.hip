@@ -564,7 +564,9 @@ __device__ __forceinline__ RecView get_view(const uint4* src)
 // Workgroup w owns a contiguous share of the records' concatenated row
 // sequence (laid out by the host so that a share that straddles two records,
 // which pays a second set of boundary rows and placements, takes fewer
-// rows).  A share spans at most R rows: one or two segments.
+// rows).  A share spans at most R rows (one or two segments), or, when the
+// records outnumber the CUs, two whole records (a pair: two segments that
+// both end at row R).
 // Phases, separated by workgroup barriers:
 //   1. rows: every unit runs its rows of each segment; its Horner partial is
 //      multiplied by H^(d*T) (d = segment rows after the unit's last one, <
@@ -591,12 +593,13 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     // after them:
     //   [0, 768)       the units' products of the last segment
     //   [768, 783)     its wave sums, the record sums, last flags
-    //   [1024, 4864)   placement table of segment 1
+    //   [1024, 4864)   placement table of segment 1 (straddling share), or
+    //   [1024, 1792)   segment 0's products (pair)
     // throughout: [6144, 9984) the placement table of segment 0 (built in
     // the set-up; a straddling workgroup keeps segment 0's products and both
     // multipliers there until after the rows), 9984 a zero word, [9985, 9995) the two record views,
     // [9995, 9997) their tag masks E_K(J0), [9997, 10009) the wave sums of a
-    // straddling workgroup's segment 0, [10009, 10011) the expected tags.
+    // two-segment workgroup's segment 0, [10009, 10011) the expected tags.
     __shared__ uint4 s_lds[10240];
     const uint4* const g_u = s_lds;
     const uint4* const g_u2 = s_lds + 512;
@@ -615,6 +618,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     uint4* const s_ek = s_lds + 9995;
     uint4* const s_c0 = s_lds + 9997;
     uint4* const s_tag = s_lds + 10009;  // expected tags of the two records (decrypt, verify)
+    uint4* const xs0 = s_lds + 1024;     // after the rows: a pair's segment-0 products
 
     constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
     const uint32_t tid = threadIdx.x;
@@ -631,6 +635,9 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     const uint32_t qb0 = g1 - uint64_t(r0) * sch.rows < sch.rows ? uint32_t(g1 - uint64_t(r0) * sch.rows) : sch.rows;
     const uint32_t nseg = g1 > (uint64_t(r0) + 1) * sch.rows ? 2u : 1u;
     const uint32_t qb1 = uint32_t(g1 - (uint64_t(r0) + 1) * sch.rows);  // segment 1: rows [0, qb1) of r0 + 1
+    // Two whole records (the host's pair layout): both segments end at row
+    // R, so one placement table serves both.
+    const bool pair = nseg == 2 && sch.pairs;
 
     // A one-segment workgroup's placement multiplier, loaded with the tables
     // below (its placement table is built in the set-up).
@@ -638,7 +645,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     // parked products) until its tables are built after the rows.
     uint4 zp0 = make_uint4(0, 0, 0, 0), zp1 = make_uint4(0, 0, 0, 0);
     zp0 = placement_power(ctx, sch, qb0, t);
-    if (nseg == 2 && u == 0) zp1 = placement_power(ctx, sch, qb1, t);
+    if (nseg == 2 && !pair && u == 0) zp1 = placement_power(ctx, sch, qb1, t);
     if (tid < SI_T) {
         aes_fill_lds(aes, ctx->te0, tid);
     } else {
@@ -653,11 +660,11 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     }
     if (tid < nseg) put_view(s_view + 5 * tid, view_of(batch, r0 + tid));
     if (tid == 0) *s_zero = make_uint4(0, 0, 0, 0);
-    // One segment: its placement table now (thread (u, t) writes its third
-    // of the multiples of H^((R - qb)*T + T - t)).  Two segments: the region
-    // holds segment 0's products while segment 1 runs; both tables are built
-    // after the rows.
-    if (nseg == 1) {
+    // One segment or a pair: its placement table now (thread (u, t) writes
+    // its third of the multiples of H^((R - qb)*T + T - t)).  Two segments
+    // of a straddling share: the region holds segment 0's products while
+    // segment 1 runs; both tables are built after the rows.
+    if (nseg == 1 || pair) {
         const uint32_t z[4] = {zp0.x, zp0.y, zp0.z, zp0.w};
         gh_table_share(z, u, ptab0, t, SI_T);
     } else if (u == 0) {
@@ -669,20 +676,24 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     __syncthreads();
     // Tag masks E_K(J0): formed in row 0's keystream pass when that row has
     // ciphertext lanes (the segment that starts a record adds it); otherwise
-    // here, for the record whose last row ends a segment (lanes 0 and 1 of
-    // wave 0, before their rows).
-    if (!sch.ek_row0 && tid < nseg && (tid ? qb1 : qb0) == sch.rows) {
-        const RecView v = get_view(s_view + 5 * tid);
-        uint32_t ek[4];
-        aes_ctr_block(aes, aes_lane(tid), keys, bswap32(v.iv[0]) ^ ctx->rk[0], bswap32(v.iv[1]) ^ ctx->rk[1],
-                      bswap32(v.iv[2]) ^ ctx->rk[2], 1u, ek);
-        s_ek[tid] = make_uint4(ek[0], ek[1], ek[2], ek[3]);
+    // here, for the record whose last row ends segment s, by lane 0 of wave s
+    // before its rows (one lane per wave: the view is read as a scalar).
+    {
+        const uint32_t s = tid >> 6;
+        if (!sch.ek_row0 && (tid & 63u) == 0 && s < nseg && (s ? qb1 : qb0) == sch.rows) {
+            const RecView v = get_view(s_view + 5 * s);
+            uint32_t ek[4];
+            aes_ctr_block(aes, aes_lane(0), keys, bswap32(v.iv[0]) ^ ctx->rk[0], bswap32(v.iv[1]) ^ ctx->rk[1],
+                          bswap32(v.iv[2]) ^ ctx->rk[2], 1u, ek);
+            s_ek[s] = make_uint4(ek[0], ek[1], ek[2], ek[3]);
+        }
     }
 
     const AesLane lane = aes_lane(tid & 63u);
     uint4* const s_p0 = ptab0;  // two segments: segment 0's products during segment 1
     // Rows of segment s; the unit's partial, moved onto the segment's
-    // exponent grid.  A straddling workgroup parks segment 0's in s_p0.
+    // exponent grid.  A straddling workgroup parks segment 0's in s_p0, a
+    // pair (whose table holds that region) in global memory.
     auto segment = [&](const uint32_t s) __attribute__((always_inline)) -> uint4 {
         const uint32_t qa = s ? 0u : qa0, qb = s ? qb1 : qb0;
         const RecView v = get_view(s_view + 5 * s);
@@ -696,11 +707,17 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         else if (d == 2) gh_mul(g_2, y, pr);
         else { pr[0] = y[0]; pr[1] = y[1]; pr[2] = y[2]; pr[3] = y[3]; }
         const uint4 r = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        if (s == 0 && nseg == 2) s_p0[tid] = r;
+        if (s == 0 && nseg == 2) {
+            if (pair) sch.park[uint64_t(blockIdx.x) * SI_NT + tid] = r;
+            else s_p0[tid] = r;
+        }
         return r;
     };
     uint4 p = segment(0);
     if (nseg == 2) p = segment(1);
+    // A pair's segment-0 product back from global memory (this thread's own
+    // store; the load overlaps the tag read and the barrier below).
+    const uint4 p0 = pair ? sch.park[uint64_t(blockIdx.x) * SI_NT + tid] : make_uint4(0, 0, 0, 0);
     // The expected tag of each record, loaded now so that the read is off the
     // finalising workgroup's critical path (it is needed after the ticket).
     // Lanes 0 and 1 read different views, so the pointer stays per lane
@@ -723,6 +740,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     // The last segment's products to LDS; placement t is shared by the three
     // threads (u, t): one table, three nibble classes.
     xs[u * SI_T + t] = p;
+    if (pair) xs0[u * SI_T + t] = p0;
     __syncthreads();
     uint32_t w[2][4];
     {
@@ -739,20 +757,23 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         else if (u == 1) gh_mul_part<3, 1, 1>(x1, tb, s_zero, t, SI_T, o1);
         else gh_mul_part<3, 2, 1>(x1, tb, s_zero, t, SI_T, o1);
     } else {
+        const uint4* const s_w0 = pair ? xs0 : s_p0;
         {
-            const uint4 a = s_p0[t], b = s_p0[SI_T + t], c = s_p0[2 * SI_T + t];
+            const uint4 a = s_w0[t], b = s_w0[SI_T + t], c = s_w0[2 * SI_T + t];
             w[0][0] = xor3(a.x, b.x, c.x); w[0][1] = xor3(a.y, b.y, c.y);
             w[0][2] = xor3(a.z, b.z, c.z); w[0][3] = xor3(a.w, b.w, c.w);
         }
-        const uint4 z0 = s_zp[t], z1 = s_zp[SI_T + t];
-        __syncthreads();  // s_p0 and s_zp are read; the region takes segment 0's table
-        {
-            const uint32_t za[4] = {z0.x, z0.y, z0.z, z0.w}, zb[4] = {z1.x, z1.y, z1.z, z1.w};
-            gh_table_share(za, u, ptab0, t, SI_T);
-            gh_table_share(zb, u, ptab1, t, SI_T);
+        if (!pair) {  // uniform over the workgroup
+            const uint4 z0 = s_zp[t], z1 = s_zp[SI_T + t];
+            __syncthreads();  // s_p0 and s_zp are read; the region takes segment 0's table
+            {
+                const uint32_t za[4] = {z0.x, z0.y, z0.z, z0.w}, zb[4] = {z1.x, z1.y, z1.z, z1.w};
+                gh_table_share(za, u, ptab0, t, SI_T);
+                gh_table_share(zb, u, ptab1, t, SI_T);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        const uint4* const tb[2] = {ptab0, ptab1};
+        const uint4* const tb[2] = {ptab0, pair ? ptab0 : ptab1};
         if (u == 0) gh_mul_part<3, 0, 2>(w, tb, s_zero, t, SI_T, q);
         else if (u == 1) gh_mul_part<3, 1, 2>(w, tb, s_zero, t, SI_T, q);
         else gh_mul_part<3, 2, 2>(w, tb, s_zero, t, SI_T, q);

@@ -57,6 +57,9 @@ struct Sched {
     uint32_t lh[4];      // L * H, L = [len(A)]_64 || [len(C)]_64: the length block's GHASH term
     uint32_t ek_row0;    // 1: row 0 holds AAD block a-1 and a ciphertext block, and the tag
                          // mask E_K(J0) rides on row 0's keystream pass
+    uint32_t pairs;      // 1: workgroup w owns the whole records 2w and 2w+1
+    uint4* park;         // pairs: each thread's segment-0 product during segment 1
+                         // (one uint4 per thread of each workgroup)
 };
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                       const Sched& s, RecAcc* acc, bool aligned);

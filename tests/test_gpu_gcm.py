@@ -293,6 +293,75 @@ def test_writeback_layer_straddling_shares(chunk_rows):
         assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
 
 
+@pytest.mark.parametrize("bits", [0, 4])
+def test_layer_pairs_of_whole_records(bits):
+    """More records than CUs (2 * CUs - 1): the host lays out shares of two
+    whole records (one placement table for both, segment 0's products parked
+    in global memory) and a last share of one.  Reload with tampered records
+    at both positions of a pair and in the single share, then writeback
+    parity against OpenSSL."""
+    rng = np.random.default_rng(71 + bits)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    heads, dim, layer = 1, 64, 3
+    nrec = 2 * cus - 1
+    nb = (nrec + 1) // 2
+    nv = nrec - nb
+    nslots = nb + 7
+    kinds = [0] * nb + [1] * nv
+    slots_np = np.concatenate([rng.permutation(nslots)[:nb], rng.permutation(nslots)[:nv]]).astype(np.int64)
+    data = O.f32_to_bf16(rng.standard_normal((2, nslots, 128, heads, dim), dtype=np.float32))
+    blocks = [data[kinds[r]][slots_np[r]] for r in range(nrec)]
+    if bits:
+        plain = [O.codec_encode(blocks[r], bits, kinds[r], layer) for r in range(nrec)]
+    else:
+        plain = [blocks[r].view(np.uint8).reshape(-1) for r in range(nrec)]
+    n = plain[0].size
+    st, toff = W.stride(n), W.align32(n)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    staging = torch.zeros(nrec * W.align32(n), dtype=torch.uint8, device=DEV) if bits else None
+
+    # Writeback: device gather (+ quantise) + encrypt == OpenSSL.
+    ck, cv = make_caches(nslots, heads, dim)
+    ck.copy_(dev(data[0].view(np.int16)))
+    cv.copy_(dev(data[1].view(np.int16)))
+    ticket0 = 20000
+    dw = dev(W.wire_aads(KEY, SALT, n, kinds, layer, list(range(nrec)), ticket0))
+    sess.writeback_layer(dw, n, nrec, nb, ck, cv, dev(slots_np), ticket_base=ticket0, codec_bits=bits,
+                         heads=heads, head_dim=dim, layer=layer, staging=staging)
+    ww = host(dw)
+    expect = W.build_wire(KEY, SALT, plain, kinds, layer, list(range(nrec)), ticket0, direction=2)
+    for r in range(nrec):
+        o = r * st
+        assert np.array_equal(ww[o:o + n], expect[o:o + n]), f"record {r} ciphertext"
+        assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
+
+    # Reload into fresh caches, records 0, 3 (both positions of a pair) and
+    # the last (a share of its own) tampered.
+    ticket1 = 30000
+    wire = W.build_wire(KEY, SALT, plain, kinds, layer, list(range(nrec)), ticket1)
+    bad = {0, 3, nrec - 1}
+    for r in bad:
+        wire[r * st + (r * 37) % n] ^= 0x10
+    ck2, cv2 = make_caches(nslots, heads, dim)
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    dw = dev(wire)
+    sess.reload_layer(dw, n, nrec, nb, ck2, cv2, dev(slots_np), ticket_base=ticket1, codec_bits=bits,
+                      heads=heads, head_dim=dim, layer=layer, staging=staging, fail_count=fail)
+    kk, vv, ww = host(ck2), host(cv2), host(dw)
+    assert int(host(fail)[0]) == len(bad)
+    for r in range(nrec):
+        status = int(ww[r * st + toff + 16:r * st + toff + 20].view(np.uint32)[0])
+        assert status == (0 if r in bad else 1), f"record {r} status"
+        got = (kk if kinds[r] == 0 else vv)[slots_np[r]]
+        if r in bad:
+            assert not got.any(), f"record {r} not zeroed"
+        elif bits:
+            want = O.codec_decode(plain[r], heads, dim, bits, kinds[r])
+            assert np.array_equal(got.view(np.uint16), want), f"record {r} decode"
+        else:
+            assert np.array_equal(got.view(np.uint16), blocks[r]), f"record {r} payload"
+
+
 def test_native_transfer_wait_layer():
     rng = np.random.default_rng(51)
     heads, dim, nb, nslots = 2, 128, 3, 8
