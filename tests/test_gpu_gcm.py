@@ -258,6 +258,36 @@ def test_writeback_layer(bits):
         assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
 
 
+@pytest.mark.parametrize("kinds_of", ["k_only", "v_only"])
+def test_writeback_codec_one_kind(kinds_of):
+    """The quantiser grid with K workgroups only or V workgroups only."""
+    rng = np.random.default_rng(51 + len(kinds_of))
+    heads, dim, nrec, nslots, layer, bits = 4, 128, 3, 8, 5, 4
+    ck, cv = make_caches(nslots, heads, dim)
+    data = O.f32_to_bf16(rng.standard_normal((2, nslots, 128, heads, dim), dtype=np.float32))
+    ck.copy_(dev(data[0].view(np.int16)))
+    cv.copy_(dev(data[1].view(np.int16)))
+    slots_np = rng.permutation(nslots)[:nrec].astype(np.int64)
+    n_k = nrec if kinds_of == "k_only" else 0
+    kinds = [0 if r < n_k else 1 for r in range(nrec)]
+    plain = [O.codec_encode(data[kinds[r]][slots_np[r]], bits, kinds[r], layer) for r in range(nrec)]
+    n = plain[0].size
+    ticket0 = 700
+    wire = W.wire_aads(KEY, SALT, n, kinds, layer, list(range(nrec)), ticket0)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    staging = torch.zeros(nrec * W.align32(n), dtype=torch.uint8, device=DEV)
+    dw = dev(wire)
+    sess.writeback_layer(dw, n, nrec, n_k, ck, cv, dev(slots_np), ticket_base=ticket0, codec_bits=bits,
+                         heads=heads, head_dim=dim, layer=layer, staging=staging)
+    ww = host(dw)
+    expect = W.build_wire(KEY, SALT, plain, kinds, layer, list(range(nrec)), ticket0, direction=2)
+    st, toff = W.stride(n), W.align32(n)
+    for r in range(nrec):
+        o = r * st
+        assert np.array_equal(ww[o:o + n], expect[o:o + n]), f"record {r} ciphertext"
+        assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
+
+
 @pytest.mark.parametrize("chunk_rows", [3, 16, 64])
 def test_writeback_layer_straddling_shares(chunk_rows):
     """Encrypt with workgroup shares that straddle two records (straddle cost
