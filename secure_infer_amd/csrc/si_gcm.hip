@@ -446,6 +446,44 @@ __device__ __forceinline__ void rows_fast(const RecView& v, const uint4* gh, con
     }
 }
 
+// The fast rows of unit u in the segment rows [qa, qb): segment rows whose
+// blocks are all full ciphertext blocks for every thread of a unit
+// (i in [a, a + nfull) for all t), as the unit's row indices i in [i0, i1)
+// (segment row u + SI_U*i), and the segment's first block (row 0).
+struct FastRows {
+    int64_t base;
+    int64_t jf0, jf1;
+    uint32_t nu, i0, i1;
+};
+
+__device__ __forceinline__ FastRows fast_rows(const Sched& sch, uint32_t u, uint32_t qa, uint32_t qb,
+                                              bool fast_ok)
+{
+    FastRows f;
+    const int64_t m = int64_t(sch.a) + int64_t(sch.n);  // AAD || C
+    f.base = m - int64_t(sch.rows - qa) * SI_T;
+    const uint32_t J = qb - qa;
+    f.nu = u < J ? (J - u + SI_U - 1) / SI_U : 0u;
+    const int64_t nfull = int64_t(sch.bytes / 16);
+    int64_t jf0 = int64_t(sch.a) - f.base;                    // first fast row: base + j*T >= a
+    jf0 = jf0 <= 0 ? 0 : (jf0 + SI_T - 1) / SI_T;
+    int64_t jf1 = int64_t(sch.a) + nfull - f.base - SI_T;    // last fast row: base + j*T + T-1 < a + nfull
+    jf1 = jf1 < 0 ? 0 : jf1 / SI_T + 1;
+    if (jf1 > int64_t(J)) jf1 = J;
+    if (jf0 > jf1) jf0 = jf1;
+    if (!fast_ok) jf0 = jf1 = J;
+    const auto first_at = [&](int64_t j) -> uint32_t {
+        return j <= int64_t(u) ? 0u : uint32_t((j - int64_t(u) + SI_U - 1) / SI_U);
+    };
+    f.i1 = first_at(jf1);
+    f.i0 = first_at(jf0);
+    if (f.i1 > f.nu) f.i1 = f.nu;
+    if (f.i0 > f.i1) f.i0 = f.i1;
+    f.jf0 = jf0;
+    f.jf1 = jf1;
+    return f;
+}
+
 // Rows [qa, qb) of one record, shared by the workgroup's SI_U units: unit u
 // takes the segment rows j = u + SI_U*i, i = 0..nu-1, and runs Horner with
 // H^(SI_U*T) over them into y.  Row q of the record holds blocks
@@ -460,31 +498,12 @@ __device__ __forceinline__ void unit_rows(const GcmCtx* __restrict__ ctx, const 
     const uint32_t n0 = bswap32(v.iv[0]) ^ ctx->rk[0];
     const uint32_t n1 = bswap32(v.iv[1]) ^ ctx->rk[1];
     const uint32_t n2 = bswap32(v.iv[2]) ^ ctx->rk[2];
-    const int64_t m = int64_t(sch.a) + int64_t(sch.n);  // AAD || C
-    const int64_t base = m - int64_t(sch.rows - qa) * SI_T;  // first block of segment row 0
-    const uint32_t J = qb - qa;
-    const uint32_t nu = u < J ? (J - u + SI_U - 1) / SI_U : 0u;
     const uint32_t tail = uint32_t(sch.bytes - (uint64_t(sch.n) - 1) * 16u);  // bytes in last block
     const uint32_t aad_tail = sch.aad_bytes ? uint32_t(sch.aad_bytes - (uint64_t(sch.a) - 1) * 16u) : 0u;
-
-    // Segment rows whose blocks are all full ciphertext blocks for every
-    // thread of a unit take the fast path: i in [a, a + nfull) for all t.
-    const int64_t nfull = int64_t(sch.bytes / 16);
-    int64_t jf0 = int64_t(sch.a) - base;                      // first fast row: base + j*T >= a
-    jf0 = jf0 <= 0 ? 0 : (jf0 + SI_T - 1) / SI_T;
-    int64_t jf1 = int64_t(sch.a) + nfull - base - SI_T;      // last fast row: base + j*T + T-1 < a + nfull
-    jf1 = jf1 < 0 ? 0 : jf1 / SI_T + 1;
-    if (jf1 > int64_t(J)) jf1 = J;
-    if (jf0 > jf1) jf0 = jf1;
-    const bool fast_ok = kAligned && !v.skip;
-    if (!fast_ok) jf0 = jf1 = J;
-    // The unit's rows inside [jf0, jf1): i in [i0, i1).
-    const auto first_at = [&](int64_t j) -> uint32_t {
-        return j <= int64_t(u) ? 0u : uint32_t((j - int64_t(u) + SI_U - 1) / SI_U);
-    };
-    uint32_t i1 = first_at(jf1), i0 = first_at(jf0);
-    if (i1 > nu) i1 = nu;
-    if (i0 > i1) i0 = i1;
+    const FastRows f = fast_rows(sch, u, qa, qb, kAligned && !v.skip);
+    const int64_t base = f.base;
+    const int64_t jf0 = f.jf0, jf1 = f.jf1;
+    const uint32_t nu = f.nu, i0 = f.i0, i1 = f.i1;
 
     // Record row 0 (qa = 0: unit 0's first row; general, before or after the
     // fast rows) carries the tag-mask job when the batch puts it there.
