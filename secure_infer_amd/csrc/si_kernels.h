@@ -47,7 +47,8 @@ struct RecBatch {
 struct Sched {
     uint32_t nrec;       // records
     uint32_t rows;       // R: rows of T blocks per record, ceil((a + n) / T) (at least 1)
-    uint32_t nwg;        // W workgroups, W >= nrec (a share never spans more than R rows)
+    uint32_t nwg;        // W workgroups: W >= nrec (a share spans at most R rows), or
+                         // ceil(nrec / 2) with pairs (a share is two whole records)
     uint32_t use_starts; // 1: workgroup w owns rows [starts[w], starts[w+1]); 0: an equal split
     uint32_t starts[SI_MAX_WG + 1];  // share boundaries in the records' concatenated rows
     uint32_t a;          // AAD blocks
