@@ -323,17 +323,17 @@ def test_writeback_layer_straddling_shares(chunk_rows):
         assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), f"record {r} tag"
 
 
-@pytest.mark.parametrize("bits", [0, 4])
-def test_layer_pairs_of_whole_records(bits):
-    """More records than CUs (2 * CUs - 1): the host lays out shares of two
-    whole records (one placement table for both, segment 0's products parked
-    in global memory) and a last share of one.  Reload with tampered records
-    at both positions of a pair and in the single share, then writeback
-    parity against OpenSSL."""
-    rng = np.random.default_rng(71 + bits)
+@pytest.mark.parametrize("bits,extra", [(0, -1), (4, -1), (0, 0)])
+def test_layer_pairs_of_whole_records(bits, extra):
+    """More records than CUs (2 * CUs - 1 or 2 * CUs): the host lays out
+    shares of two whole records (one placement table for both, segment 0's
+    products parked in global memory), with an odd count a last share of one.
+    Reload with tampered records at both positions of a pair and in the last
+    share, then writeback parity against OpenSSL."""
+    rng = np.random.default_rng(71 + bits - extra)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     heads, dim, layer = 1, 64, 3
-    nrec = 2 * cus - 1
+    nrec = 2 * cus + extra
     nb = (nrec + 1) // 2
     nv = nrec - nb
     nslots = nb + 7
