@@ -99,6 +99,12 @@ int secure_infer_gpu_auth_gate_do(hipStream_t stream, void* data, void* status,
 
 typedef struct si_session si_session;
 
+/* Largest record (ciphertext / packet bytes) a session accepts: the kernels
+ * address a record's payload with 32-bit byte offsets.  No reference
+ * counterpart (its records are single KV blocks of at most a few MiB). */
+#define SI_MAX_RECORD_BYTES 0x7fff0000ull
+
+/* max_record_bytes: 1 .. SI_MAX_RECORD_BYTES, else -1. */
 int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt[4],
                                     uint64_t session_nonce, uint64_t max_record_bytes,
                                     si_session** out);
@@ -193,15 +199,30 @@ void secure_infer_clear_host_ranges(void);
 int secure_infer_build_gcm_aad(const void* host_ptr, size_t bytes, uint8_t direction,
                                uint64_t transfer_ticket, uint64_t transfer_offset,
                                uint64_t session_nonce, uint8_t out[64]);
-/* secure_infer.cpp:777-789: 1 if the ticket was not seen before, else 0. */
+/* secure_infer.cpp:777-789: 1 if the ticket was not seen before, else 0.
+ * The host transfer runtime reserves every ticket it seals under (H2D
+ * :6439-6445, D2H :8096-8115) and refuses a swap whose tickets were used. */
 int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket);
+
+/* secure_infer.cpp:1102-1148: retire / invalidate the speculative ticket and
+ * keystream pools.  This library keeps no speculative state, so both are
+ * no-ops; EncodedStore binds the first unconditionally (transport_codec.py:50). */
+void secure_infer_retire_transfer_prefetches(void);
+void secure_infer_invalidate_transfer_prefetches(void);
 
 /* secure_infer.cpp:5883-5903: layer-group brackets (thread-local). */
 int secure_infer_h2d_layer_group_begin(size_t expected);
 int secure_infer_h2d_layer_group_end(void);
 
 /* secure_infer.cpp:7303-7333: 0 if every record submitted for `layer` since
- * the last wait authenticated, -1 otherwise.  Waits for the layer's work. */
+ * the last wait authenticated, -1 otherwise.  Waits for the layer's work.
+ * Records sealed by secure_infer_h2d_swap inside a layer group are observed
+ * one by one (status word copied to pinned memory after their kernel); a
+ * record that failed is re-sealed once from its trusted host block under a
+ * fresh ticket and reloaded on its stream, and the layer fails only if that
+ * second attempt fails too (strict retry, :7316-7330).  Device-resident
+ * records registered with secure_infer_recovery_track_layer have no host
+ * copy: any failure among them is -1. */
 int secure_infer_recovery_wait_layer_authentication(uint32_t layer);
 /* Registers a reload of `layer` whose per-record statuses land in the device
  * u32 `fail_count` once `event` completes (library-internal bookkeeping used
@@ -221,21 +242,37 @@ int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event,
 /* bf16 KV blocks [128, heads, head_dim], or codec packets (rows of a     */
 /* packet array, at least secure_infer_codec_width bytes).  AADs are      */
 /* built from the registered host ranges (secure_infer_build_gcm_aad).    */
+/* Like swap_blocks, which sees both tensors' shapes, the calls know the  */
+/* pool sizes: a mapping entry outside [0, host_nblocks) or [0, nslots)   */
+/* refuses the whole call (-1) before any work is queued.                 */
 
 /* H2D reload of n blocks of one (layer, kind): host OpenSSL AES-128-GCM on
  * the library's worker pool into a pinned ring slot (inline_h2d_encrypt_commit,
  * secure_infer.cpp:6486-6550; slot ring :5174-5229, :5905-6059), DMA on the
- * library's copy stream, then the fused verify + decrypt (+ dequantise) +
- * paged scatter on `stream` once the copy has landed.  Returns when the work
- * is queued; a ring slot is reused only after its kernel completed.  Inside
- * secure_infer_h2d_layer_group_begin/end, the layer is registered for
- * secure_infer_recovery_wait_layer_authentication (needs fail_count, a device
- * u32 the caller zeroes per layer). */
+ * ring's copy stream, then the fused verify + decrypt (+ dequantise) + paged
+ * scatter on `stream` once the copy has landed.  Returns when the work is
+ * queued; a ring slot is reused only after its kernel (and status copy)
+ * completed.  Rings, copy streams and locks are per (device, stream), as the
+ * reference keeps them per stream (:5389-5399).  Inside
+ * secure_infer_h2d_layer_group_begin/end every record is observed for
+ * secure_infer_recovery_wait_layer_authentication.  mapping pairs are (host
+ * block, device slot).  fail_count (device u32, may be NULL): += records
+ * that failed in this launch. */
 int secure_infer_h2d_swap(hipStream_t stream, si_session* session, const void* host_base,
-                          uint64_t host_block_bytes, void* dev_cache, uint64_t slot_bytes,
-                          uint64_t nslots, const int64_t* mapping, uint32_t n, uint32_t kind,
-                          uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim,
-                          uint32_t* fail_count);
+                          uint64_t host_block_bytes, uint64_t host_nblocks, void* dev_cache,
+                          uint64_t slot_bytes, uint64_t nslots, const int64_t* mapping, uint32_t n,
+                          uint32_t kind, uint32_t layer, uint32_t codec_bits, uint32_t heads,
+                          uint32_t head_dim, uint32_t* fail_count);
+
+/* Test-only fault injection of the reference's trust-boundary tests
+ * (PIPE_GCM_TAMPER_H2D / _LAYER / _TENSOR, secure_infer.cpp:6139-6250, and
+ * PIPE_GCM_TAMPER_D2H, :2451-2467): the next `shots` H2D records sealed from
+ * host block `host_block` of (layer, kind) -- -1 matches any -- get their
+ * first ciphertext byte flipped after sealing and before the DMA; the next
+ * `shots` D2H records get theirs flipped in host memory before host
+ * authentication.  0 shots disarms.  Production code never calls them. */
+int secure_infer_test_tamper_h2d(int32_t layer, int32_t kind, int64_t host_block, uint32_t shots);
+int secure_infer_test_tamper_d2h(uint32_t shots);
 
 /* Threads of the host crypto pool (the calling thread included): the CPUs of
  * the process affinity mask, or SECURE_INFER_HOST_THREADS.  No reference
@@ -259,12 +296,13 @@ int secure_infer_d2h_batch_end(void);
  * pinned memory on the library's D2H stream; at group end the worker pool
  * authenticates and decrypts each into host_base + block*host_block_bytes
  * (d2h_host_decrypt_one, secure_infer.cpp:2470-2547).  mapping pairs are
- * (device slot, host block). */
+ * (device slot, host block).  A failed record is zeroed in the host pool
+ * and makes batch_end return -1 (the reference zeroes and aborts). */
 int secure_infer_d2h_swap(hipStream_t stream, si_session* session, const void* dev_cache,
                           uint64_t slot_bytes, uint64_t nslots, void* host_base,
-                          uint64_t host_block_bytes, const int64_t* mapping, uint32_t n,
-                          uint32_t kind, uint32_t layer, uint32_t codec_bits, uint32_t heads,
-                          uint32_t head_dim);
+                          uint64_t host_block_bytes, uint64_t host_nblocks, const int64_t* mapping,
+                          uint32_t n, uint32_t kind, uint32_t layer, uint32_t codec_bits,
+                          uint32_t heads, uint32_t head_dim);
 
 /* Library build / device information. */
 const char* secure_infer_gpu_version(void);

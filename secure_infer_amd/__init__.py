@@ -5,8 +5,9 @@ C-ABI, include/secure_infer_gpu.h); this package binds it for PyTorch-ROCm
 tensors.  See ``secure_infer_amd.gcm``.
 """
 from .gcm import (  # noqa: F401
-    AAD_BYTES, SI_CODEC_INT4, SI_CODEC_INT8, SI_CODEC_NONE, GcmSession, LayerShape,
-    D2HTransfer, NativeTransfer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
+    AAD_BYTES, CODEC_MODES, SI_CODEC_INT4, SI_CODEC_INT8, SI_CODEC_NONE, D2HTransfer, GcmSession,
+    LayerShape, NativeTransfer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
     derive_transfer_iv, gcm_decrypt_verify, gcm_encrypt_tag, gcm_verify_only, gcm_verify_xor,
-    iv_words, keystream, new_transfer_ticket, register_host_range, replay_reserve,
+    inject_d2h_tamper, inject_h2d_tamper, iv_words, keystream, layer_bits, new_transfer_ticket,
+    reference_ticket_order, register_host_range, replay_reserve, retire_transfer_prefetches,
     set_chunk_rows, set_straddle_rows, wire_stride, wire_tag_offset)

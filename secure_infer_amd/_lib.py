@@ -64,15 +64,19 @@ SIGNATURES = {
     "secure_infer_recovery_wait_layer_authentication": ([_u32], _i),
     "secure_infer_recovery_track_layer": ([_u32, _v, _v], _i),
     "secure_infer_host_threads": ([], _i),
-    "secure_infer_h2d_swap": ([_v, _v, _v, _u64, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32, _u32,
-                               _u32, _v], _i),
+    "secure_infer_h2d_swap": ([_v, _v, _v, _u64, _u64, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32,
+                               _u32, _u32, _v], _i),
+    "secure_infer_test_tamper_h2d": ([ct.c_int32, ct.c_int32, ct.c_int64, _u32], _i),
+    "secure_infer_test_tamper_d2h": ([_u32], _i),
+    "secure_infer_retire_transfer_prefetches": ([], None),
+    "secure_infer_invalidate_transfer_prefetches": ([], None),
     "secure_infer_d2h_batch_begin": ([_sz], _i),
     "secure_infer_d2h_group_begin": ([_sz], _i),
     "secure_infer_d2h_group_end": ([], _i),
     "secure_infer_d2h_batch_device_barrier": ([], _i),
     "secure_infer_d2h_batch_end": ([], _i),
-    "secure_infer_d2h_swap": ([_v, _v, _v, _u64, _u64, _v, _u64, _v, _u32, _u32, _u32, _u32, _u32,
-                               _u32], _i),
+    "secure_infer_d2h_swap": ([_v, _v, _v, _u64, _u64, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32,
+                               _u32, _u32], _i),
     "secure_infer_gpu_version": ([], ct.c_char_p),
     "secure_infer_gpu_set_chunk_rows": ([_i], _i),
     "secure_infer_gpu_set_straddle_rows": ([_i], _i),

@@ -1,4 +1,6 @@
-"""Builds libsecure_infer.so (HIP for gfx950) in-tree with hipcc."""
+"""Builds libsecure_infer.so (HIP for gfx950) in-tree with hipcc, and the
+GPU self-test library the tests load (tests/_build/libsi_selftest.so: the
+sweep of the codec's packed conversions over every float pattern)."""
 from __future__ import annotations
 
 import os
@@ -10,6 +12,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "_lib" / "libsecure_infer.so"
+SELFTEST_SRC = ROOT / "tests" / "csrc" / "codec_cvt_sweep.hip"
+SELFTEST_OUT = ROOT / "tests" / "_build" / "libsi_selftest.so"
 
 SOURCES = ["si_gcm.hip", "si_codec.hip", "si_api.cpp", "si_host.cpp"]
 LIBS = ["-lcrypto", "-lpthread"]
@@ -44,6 +48,14 @@ def build(verbose: bool = False) -> Path:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, OUT)
+    if SELFTEST_SRC.exists():
+        SELFTEST_OUT.parent.mkdir(parents=True, exist_ok=True)
+        tmp = SELFTEST_OUT.with_suffix(".so.tmp")
+        cmd = [hipcc(), *FLAGS, "-I", str(CSRC), "-o", str(tmp), str(SELFTEST_SRC)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(tmp, SELFTEST_OUT)
     return OUT
 
 

@@ -367,22 +367,36 @@ uint32_t npow_for(uint64_t bytes, uint64_t aad_bytes)
     return uint32_t((aad_bytes + 15) / 16 + (bytes + 15) / 16 + 1 + SI_T + 16);
 }
 
-std::mutex g_lock;
-std::vector<std::unique_ptr<DevCtx>> g_ctx_cache;  // compat entry points, keyed by (key, H)
+// Per-key contexts of the kernel-level entry points (keyed by key and H);
+// those calls hold this lock for their whole duration.
+std::mutex g_ctx_lock;
+std::vector<std::unique_ptr<DevCtx>> g_ctx_cache;
 
 // Per-stream accumulator workspaces (and the parking area of two-record
-// shares).
+// shares).  A launch holds its stream's workspace lock from the workspace
+// lookup to the launch; launches on different streams do not contend.
 struct Workspace {
+    std::mutex m;
     si::RecAcc* acc = nullptr;
     size_t cap = 0;
     uint4* park = nullptr;
     size_t park_cap = 0;
 };
-std::unordered_map<hipStream_t, Workspace> g_ws;
+std::mutex g_ws_lock;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>> g_ws;
 
-si::RecAcc* workspace(hipStream_t stream, size_t nrec)
+Workspace* workspace_of(hipStream_t stream)
 {
-    Workspace& w = g_ws[stream];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> g(g_ws_lock);
+    auto& w = g_ws[std::make_pair(dev, stream)];
+    if (!w) w = std::make_unique<Workspace>();
+    return w.get();
+}
+
+si::RecAcc* workspace(Workspace& w, hipStream_t stream, size_t nrec)
+{
     if (w.cap >= nrec) return w.acc;
     if (w.acc) {
         if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
@@ -399,9 +413,8 @@ si::RecAcc* workspace(hipStream_t stream, size_t nrec)
 }
 
 // Parking area for nwg two-record workgroups (one uint4 per thread).
-uint4* park_area(hipStream_t stream, size_t nwg)
+uint4* park_area(Workspace& w, hipStream_t stream, size_t nwg)
 {
-    Workspace& w = g_ws[stream];
     const size_t need = nwg * SI_NT;
     if (w.park_cap >= need) return w.park;
     if (w.park) {
@@ -439,10 +452,14 @@ int run_single(int mode, hipStream_t stream, void* src, void* key, void* h, void
                void* status, const void* ks, uint64_t bytes, const uint32_t iv[4], void* aad,
                uint64_t aad_bytes)
 {
-    std::lock_guard<std::mutex> g(g_lock);
+    if (bytes > SI_MAX_RECORD_BYTES) return -1;
+    std::lock_guard<std::mutex> g(g_ctx_lock);
     DevCtx* c = ctx_for_device_key(stream, key, h, npow_for(bytes, aad_bytes));
     if (!c) return -1;
-    si::RecAcc* acc = workspace(stream, 1);
+    Workspace* ws = workspace_of(stream);
+    if (!ws) return -1;
+    std::lock_guard<std::mutex> gw(ws->m);
+    si::RecAcc* acc = workspace(*ws, stream, 1);
     if (!acc) return -1;
     si::RecBatch b{};
     b.single = 1;
@@ -470,19 +487,40 @@ struct HostRange {
 std::mutex g_ranges_lock;
 std::vector<HostRange> g_ranges;
 
+// Tickets used so far, as disjoint half-open intervals [first, last)
+// (tickets are reserved in runs, so the set stays small).
 std::mutex g_replay_lock;
-std::unordered_set<uint64_t> g_replay;
+std::map<uint64_t, uint64_t> g_replay;
+
+bool replay_insert(uint64_t a, uint64_t b)
+{
+    if (a >= b) return true;
+    std::lock_guard<std::mutex> g(g_replay_lock);
+    auto next = g_replay.lower_bound(a);
+    if (next != g_replay.end() && next->first < b) return false;
+    if (next != g_replay.begin()) {
+        auto prev = std::prev(next);
+        if (prev->second > a) return false;
+        if (prev->second == a) {  // extend the run that ends at a
+            prev->second = b;
+            if (next != g_replay.end() && next->first == b) {
+                prev->second = next->second;
+                g_replay.erase(next);
+            }
+            return true;
+        }
+    }
+    if (next != g_replay.end() && next->first == b) {
+        const uint64_t e = next->second;
+        g_replay.erase(next);
+        g_replay.emplace(a, e);
+    } else {
+        g_replay.emplace(a, b);
+    }
+    return true;
+}
 
 thread_local int64_t t_group_expected = -1;
-
-// Layer reloads issued through the host pipeline inside the calling thread's
-// open layer group; the group's end publishes one completion event per entry.
-struct GroupNote {
-    hipStream_t stream;
-    uint32_t layer;
-    uint32_t* fail_count;
-};
-thread_local std::vector<GroupNote> t_group_notes;
 
 struct TrackedLayer {
     hipEvent_t event;
@@ -514,7 +552,8 @@ int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt
                                     uint64_t session_nonce, uint64_t max_record_bytes,
                                     si_session** out)
 {
-    if (!key || !iv_salt || !out || max_record_bytes == 0) return -1;
+    if (!key || !iv_salt || !out || max_record_bytes == 0 || max_record_bytes > SI_MAX_RECORD_BYTES)
+        return -1;
     uint8_t rk[176], h[16], zero[16] = {0};
     aes_expand(key, rk);
     aes_encrypt(rk, zero, h);
@@ -561,7 +600,7 @@ static int layer_common(const si_session* s, uint64_t bytes, uint32_t nrec, uint
                         uint64_t slot_bytes)
 {
     if (!s || !wire || !slots || nrec == 0 || n_k > nrec || bytes == 0) return -1;
-    if (nslots == 0) return -1;
+    if (nslots == 0 || bytes > SI_MAX_RECORD_BYTES) return -1;
     if (bytes > s->max_record_bytes) return -1;
     if (wire_stride < secure_infer_wire_stride(bytes) || (wire_stride & 15)) return -1;
     if (!aligned16(wire)) return -1;
@@ -593,8 +632,10 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
     if (!d->cache_k && d->n_k) return -1;
     if (!d->cache_v && d->n_k < d->nrec) return -1;
     if (!d->iv_words && d->ticket_base == 0) return -1;
-    std::lock_guard<std::mutex> g(g_lock);
-    si::RecAcc* acc = workspace(stream, d->nrec);
+    Workspace* ws = workspace_of(stream);
+    if (!ws) return -1;
+    std::lock_guard<std::mutex> g(ws->m);
+    si::RecAcc* acc = workspace(*ws, stream, d->nrec);
     if (!acc) return -1;
     si::RecBatch b{};
     b.single = 0;
@@ -618,7 +659,7 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
         b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
     }
     si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
-    if (sc.pairs && !(sc.park = park_area(stream, sc.nwg))) return -1;
+    if (sc.pairs && !(sc.park = park_area(*ws, stream, sc.nwg))) return -1;
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     if (si::launch_gcm(0, stream, s->ctx->dev, b, sc, acc, al) != hipSuccess) return -1;
     if (codec) {
@@ -653,8 +694,10 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
     if (!d->cache_k && d->n_k) return -1;
     if (!d->cache_v && d->n_k < d->nrec) return -1;
     if (!d->iv_words && d->ticket_base == 0) return -1;
-    std::lock_guard<std::mutex> g(g_lock);
-    si::RecAcc* acc = workspace(stream, d->nrec);
+    Workspace* ws = workspace_of(stream);
+    if (!ws) return -1;
+    std::lock_guard<std::mutex> g(ws->m);
+    si::RecAcc* acc = workspace(*ws, stream, d->nrec);
     if (!acc) return -1;
     const bool codec = d->codec_bits != SI_CODEC_NONE;
     si::RecBatch b{};
@@ -696,7 +739,7 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
         if (si::launch_gather_quant(stream, cb) != hipSuccess) return -1;
     }
     si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
-    if (sc.pairs && !(sc.park = park_area(stream, sc.nwg))) return -1;
+    if (sc.pairs && !(sc.park = park_area(*ws, stream, sc.nwg))) return -1;
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     return si::launch_gcm(1, stream, s->ctx->dev, b, sc, acc, al) == hipSuccess ? 0 : -1;
 }
@@ -776,7 +819,7 @@ int secure_infer_gpu_gcm_verify_xor_aad_do(hipStream_t stream, void* ciphertext,
 static int run_ctr(hipStream_t stream, const void* in, void* key, void* out, uint64_t bytes,
                    const uint32_t iv[4])
 {
-    std::lock_guard<std::mutex> g(g_lock);
+    std::lock_guard<std::mutex> g(g_ctx_lock);
     DevCtx* c = ctx_for_device_key(stream, key, nullptr, 1);
     if (!c) return -1;
     return si::launch_ctr(stream, c->dev, static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out),
@@ -884,15 +927,24 @@ int secure_infer_build_gcm_aad(const void* host_ptr, size_t bytes, uint8_t direc
 int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket)
 {
     if (transfer_ticket == 0) return 1;
-    std::lock_guard<std::mutex> g(g_replay_lock);
-    return g_replay.insert(transfer_ticket).second ? 1 : 0;
+    if (replay_insert(transfer_ticket, transfer_ticket + 1)) return 1;
+    fprintf(stderr, "[secure_infer] replayed transfer ticket rejected: %llu\n",
+            static_cast<unsigned long long>(transfer_ticket));
+    return 0;
 }
+
+// The reference retires or invalidates its speculative keystream / ticket
+// pools here (secure_infer.cpp:1102-1148).  This library keeps no speculative
+// state (tickets are reserved when a swap is issued), so both are no-ops; they
+// are exported because EncodedStore binds the first unconditionally
+// (transport_codec.py:50).
+void secure_infer_retire_transfer_prefetches(void) {}
+void secure_infer_invalidate_transfer_prefetches(void) {}
 
 int secure_infer_h2d_layer_group_begin(size_t expected)
 {
     if (t_group_expected >= 0) return -1;
     t_group_expected = int64_t(expected);
-    t_group_notes.clear();
     return 0;
 }
 
@@ -900,25 +952,7 @@ int secure_infer_h2d_layer_group_end(void)
 {
     if (t_group_expected < 0) return -1;
     t_group_expected = -1;
-    int rc = 0;
-    std::vector<GroupNote> notes;
-    notes.swap(t_group_notes);
-    for (size_t i = 0; i < notes.size(); ++i) {
-        bool seen = false;
-        for (size_t j = 0; j < i; ++j)
-            seen |= notes[j].stream == notes[i].stream && notes[j].layer == notes[i].layer &&
-                    notes[j].fail_count == notes[i].fail_count;
-        if (seen) continue;
-        hipEvent_t ev = nullptr;
-        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess ||
-            hipEventRecord(ev, notes[i].stream) != hipSuccess) {
-            rc = -1;
-            continue;
-        }
-        std::lock_guard<std::mutex> g(g_track_lock);
-        g_tracked.emplace(notes[i].layer, TrackedLayer{ev, notes[i].fail_count, true});
-    }
-    return rc;
+    return 0;
 }
 
 int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event, const uint32_t* fail_count)
@@ -931,6 +965,11 @@ int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event, const ui
 
 int secure_infer_recovery_wait_layer_authentication(uint32_t layer)
 {
+    // Host-sealed records of the layer: statuses, one strict retry.
+    bool found = false;
+    const int rc_host = si_internal::wait_observed_layer(layer, &found);
+    // Device-resident records of the layer: a fail count (no host copy to
+    // retry from).
     std::vector<TrackedLayer> recs;
     {
         std::lock_guard<std::mutex> g(g_track_lock);
@@ -948,7 +987,7 @@ int secure_infer_recovery_wait_layer_authentication(uint32_t layer)
             rc = -1;
         if (t.owned) (void)hipEventDestroy(t.event);
     }
-    return rc;
+    return (rc != 0 || rc_host != 0) ? -1 : 0;
 }
 
 int secure_infer_gpu_set_chunk_rows(int jmax)
@@ -989,11 +1028,8 @@ uint64_t reserve_tickets(uint32_t n)
     return t;
 }
 
-bool group_note(hipStream_t stream, uint32_t layer, uint32_t* fail_count)
-{
-    if (t_group_expected < 0 || !fail_count) return false;
-    t_group_notes.push_back(GroupNote{stream, layer, fail_count});
-    return true;
-}
+bool replay_reserve_range(uint64_t t0, uint64_t n) { return replay_insert(t0, t0 + n); }
+
+bool group_open() { return t_group_expected >= 0; }
 
 }  // namespace si_internal

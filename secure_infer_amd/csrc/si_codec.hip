@@ -15,17 +15,10 @@
 // Non-finite KV follows torch: x.amin / x.amax propagate NaN, so a group with
 // a NaN gets NaN scale and low and quantises to 0; decoding a NaN gives the
 // bf16 NaN 0x7fc0.  The bit patterns of NaN parameters are not specified.
+#include "si_codec_math.h"
 #include "si_kernels.h"
 
 namespace si {
-
-__device__ __forceinline__ uint32_t f32_to_bf16(float f)
-{
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h)
 {
@@ -41,9 +34,6 @@ __device__ __forceinline__ uint32_t udiv_small(uint32_t n, uint32_t d)
     return q;
 }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
 // Two decoded elements fl(fl(q*s) + o) as packed bf16.  With finite s and o
 // no result is NaN (q is a small integer), and v_cvt_pk_bf16_f32 rounds every
 // non-NaN float to nearest even exactly like f32_to_bf16 (checked on every
@@ -55,10 +45,7 @@ __device__ __forceinline__ uint32_t dq2(float q0, float s0, float o0, float q1, 
     const float v0 = __fadd_rn(__fmul_rn(q0, s0), o0);
     const float v1 = __fadd_rn(__fmul_rn(q1, s1), o1);
     if constexpr (kFinite) {
-        f32x2 v;
-        v.x = v0;
-        v.y = v1;
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+        return pack_bf16x2(v0, v1);
     } else {
         return f32_to_bf16(v0) | (f32_to_bf16(v1) << 16);
     }
@@ -192,43 +179,13 @@ __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
     return s < 1e-12f ? 1e-12f : s;
 }
 
-// RN(1/s) for a normal s: hardware estimate, two Newton steps, then the
-// neighbour with the smallest exact residual |1 - s*y| (one FMA each).
-__device__ __forceinline__ float recip_rn(float s)
-{
-    float y = __builtin_amdgcn_rcpf(s);
-    y = fmaf(fmaf(-s, y, 1.0f), y, y);
-    y = fmaf(fmaf(-s, y, 1.0f), y, y);
-    const float ylo = __uint_as_float(__float_as_uint(y) - 1u);
-    const float yhi = __uint_as_float(__float_as_uint(y) + 1u);
-    const float e = fabsf(fmaf(-s, y, 1.0f));
-    const float elo = fabsf(fmaf(-s, ylo, 1.0f));
-    const float ehi = fabsf(fmaf(-s, yhi, 1.0f));
-    if (elo < e) return ylo;
-    if (ehi < e) return yhi;
-    return y;
-}
-
-// RN(a/s) given y = RN(1/s) (Markstein: q within 1 ulp of a/s, exact FMA
-// residual r = a - q*s, q + r*y rounds correctly); a >= 0, a/s < 2^23.
-__device__ __forceinline__ float div_rn(float a, float s, float y)
-{
-    const float q = __fmul_rn(a, y);
-    return fmaf(fmaf(-q, s, a), y, q);
-}
-
 // RN((x - lo) / s) rounded half-to-even, clamped to [0, qmax] and inserted
-// as byte K of acc: v_cvt_pk_u8_f32 rounds to nearest even, saturates to
-// [0, 255] and sends NaN to 0 (checked on every float bit pattern against
-// clamp(rne(f), 0, 255)), so int8 needs no clamp of its own; int4 clamps to
-// [0, 15] first (the clamp commutes with rounding: integer bounds).
+// as byte K of acc.
 template <int K>
 __device__ __forceinline__ uint32_t quant_byte(float x, float lo, float s, float y, uint32_t bits,
                                                uint32_t acc)
 {
-    float v = div_rn(__fsub_rn(x, lo), s, y);
-    if (bits != 8) v = __builtin_amdgcn_fmed3f(v, 0.0f, 15.0f);
-    return __builtin_amdgcn_cvt_pk_u8_f32(v, K, acc);
+    return insert_q<K>(div_rn(__fsub_rn(x, lo), s, y), bits, acc);
 }
 
 __device__ __forceinline__ void unpack8(uint4 w, float x[8])
@@ -291,13 +248,15 @@ __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, u
     const uint32_t idx = bx * 256u + threadIdx.x;
     // Whole 8-lane groups take the same branch (shuffle partners stay active).
     if (idx >= 2u * nch * 8u) return;
+    // A slot id out of range reads nothing from the cache: the record's
+    // packet encodes zeros (its tag is poisoned by the encrypt kernel).
     const int64_t sid = b.slots[r];
-    if (sid < 0 || sid >= b.nslots) return;
+    const bool bad = sid < 0 || sid >= b.nslots;
     const uint32_t l8 = idx & 7u, cg = idx >> 3;
     const uint32_t g = cg >= nch ? 1u : 0u;
     const uint32_t col = (cg - g * nch) * 8u;
     const float qmax = float((1u << b.bits) - 1u);
-    const uint8_t* slot = b.cache[0] + uint64_t(sid) * b.slot_bytes;
+    const uint8_t* slot = b.cache[0] + uint64_t(bad ? 0 : sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
     if (idx == 0) store_header(b, pkt, 0u);
 
@@ -305,7 +264,8 @@ __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, u
     uint4 raw[8];
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt)
-        raw[tt] = *reinterpret_cast<const uint4*>(slot + (uint64_t(t0 + tt) * hd + col) * 2u);
+        raw[tt] = bad ? make_uint4(0, 0, 0, 0)
+                      : *reinterpret_cast<const uint4*>(slot + (uint64_t(t0 + tt) * hd + col) * 2u);
     float lo[8], hi[8];
     {
         float x[8];
@@ -371,16 +331,17 @@ __device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, u
     // meets an active partner.
     if (idx >= ngroups * 2u) return;
     const int64_t sid = b.slots[r];
-    if (sid < 0 || sid >= b.nslots) return;
+    const bool bad = sid < 0 || sid >= b.nslots;  // encode zeros, as in quant_k_block
     const uint32_t gi = idx >> 1, half = idx & 1u;
     const float qmax = float((1u << b.bits) - 1u);
-    const uint8_t* slot = b.cache[1] + uint64_t(sid) * b.slot_bytes;
+    const uint8_t* slot = b.cache[1] + uint64_t(bad ? 0 : sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
     if (idx == 0) store_header(b, pkt, 1u);
     const uint32_t e = gi * 64u + half * 32u;
     uint4 raw[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) raw[k] = *reinterpret_cast<const uint4*>(slot + uint64_t(e + 8u * k) * 2u);
+    for (int k = 0; k < 4; ++k)
+        raw[k] = bad ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(slot + uint64_t(e + 8u * k) * 2u);
     float x[32];
 #pragma unroll
     for (int k = 0; k < 4; ++k) unpack8(raw[k], x + 8 * k);

@@ -859,9 +859,12 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         if (!s_last[s]) continue;
         const RecView v = get_view(s_view + 5 * s);
         if (kMode == MODE_ENCRYPT) {
+            // A record whose block-table entry is out of range gets the
+            // complement of its tag, which never verifies: the host rejects
+            // it whether or not the caller reads the fail counter.
             if (tid == 0 && v.bad && v.fail_count) atomicAdd(v.fail_count, 1u);
             if (tid < 4) {
-                const uint32_t w = s_fin[s][tid];
+                const uint32_t w = s_fin[s][tid] ^ (v.bad ? 0xffffffffu : 0u);
                 for (int b = 0; b < 4; ++b) gmem(v.tag)[4 * tid + b] = uint8_t(w >> (8 * b));
             }
             continue;

@@ -4,11 +4,19 @@
 //    the reference's host crypto (inline_h2d_encrypt_commit,
 //    secure_infer.cpp:6486-6550; d2h_host_decrypt_one, :2470-2547).
 //  * H2D: secure_infer_h2d_swap seals host KV blocks into wire records in a
-//    pinned ring slot, copies the slot to the device on the library's copy
-//    stream and makes the caller's stream wait for that copy before the fused
-//    verify + decrypt (+ dequant) + paged-scatter kernel.  The caller returns
-//    as soon as the work is queued, so the copy of layer l+1 overlaps the
-//    kernel of layer l.  A slot is reused only after its kernel completed.
+//    pinned ring slot of the caller's stream, copies the slot to the device
+//    on that ring's copy stream and makes the caller's stream wait for the
+//    copy before the fused verify + decrypt (+ dequant) + paged-scatter
+//    kernel.  The caller returns as soon as the work is queued, so the copy
+//    of layer l+1 overlaps the kernel of layer l.  Rings, their copy streams
+//    and their locks are per (device, caller stream), like the reference's
+//    per-stream pipelines (secure_infer.cpp:5389-5399).
+//  * Observation and strict retry: inside a layer group every record's
+//    status word is copied to pinned host memory once its kernel is done
+//    (observe_recovery_authentication, secure_infer.cpp:5316-5387);
+//    secure_infer_recovery_wait_layer_authentication re-seals a record that
+//    failed once from the trusted host copy under a fresh ticket and
+//    returns -1 only when that second attempt fails too (:7303-7333).
 //  * D2H: the reference's batch / group API with the same names and
 //    thread-local contexts (secure_infer.cpp:2707-2970).  Inside a group,
 //    secure_infer_d2h_swap gathers (+ quantises) and seals device KV blocks
@@ -16,6 +24,8 @@
 //    second copy stream; the group's end hands them to the worker pool, which
 //    authenticates and decrypts each record into its host destination (a
 //    record that fails is zeroed).  batch_end waits for that verification.
+//  * Every block id is range-checked on the host before any work: a swap
+//    with a host block or device slot outside its pool is refused (-1).
 #include "si_host.h"
 
 #include <openssl/evp.h>
@@ -33,6 +43,7 @@
 #include <memory>
 #include <mutex>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 namespace {
@@ -88,6 +99,8 @@ public:
         sh->cv.wait(g, [&] { return sh->done.load() == n; });
     }
 
+    size_t threads() const { return threads_.size() + 1; }
+
 private:
     Pool()
     {
@@ -98,7 +111,7 @@ private:
         if (sched_getaffinity(0, sizeof(set), &set) == 0) n = unsigned(CPU_COUNT(&set));
         if (const char* e = std::getenv("SECURE_INFER_HOST_THREADS")) n = unsigned(std::atoi(e));
         if (n == 0) n = 1;
-        if (n > 64) n = 64;
+        if (n > 256) n = 256;
         for (unsigned i = 0; i + 1 < n; ++i) threads_.emplace_back([this] { run(); });
     }
 
@@ -116,10 +129,6 @@ private:
         }
     }
 
-public:
-    size_t threads() const { return threads_.size() + 1; }
-
-private:
     std::vector<std::thread> threads_;
     std::deque<std::function<void()>> q_;
     std::mutex m_;
@@ -182,6 +191,38 @@ void record_iv(const si_internal::SessionKeys& k, uint64_t ticket, uint8_t iv[12
 
 uint64_t tag_offset(uint64_t bytes) { return (bytes + 31) & ~uint64_t(31); }
 
+// ---------------------------------------------------------------- test fault injection
+//
+// The reference's opt-in, test-only bit flips at the two trust boundaries:
+// after the host sealed an H2D record and before its DMA
+// (PIPE_GCM_TAMPER_H2D*, secure_infer.cpp:6139-6250), and after a D2H record
+// reached host memory and before host authentication (PIPE_GCM_TAMPER_D2H,
+// :2451-2467).  Disarmed unless a test arms them.
+
+struct H2DTamper {
+    std::atomic<int64_t> layer{-1}, kind{-1}, block{-1};
+    std::atomic<int64_t> shots{0};
+};
+H2DTamper g_tamper_h2d;
+std::atomic<int64_t> g_tamper_d2h{0};
+
+bool take_shot(std::atomic<int64_t>& shots)
+{
+    int64_t s = shots.load();
+    while (s > 0)
+        if (shots.compare_exchange_weak(s, s - 1)) return true;
+    return false;
+}
+
+bool tamper_h2d(uint32_t layer, uint32_t kind, int64_t host_block)
+{
+    if (g_tamper_h2d.shots.load() <= 0) return false;
+    const int64_t l = g_tamper_h2d.layer.load(), k = g_tamper_h2d.kind.load(), b = g_tamper_h2d.block.load();
+    if ((l >= 0 && l != int64_t(layer)) || (k >= 0 && k != int64_t(kind)) || (b >= 0 && b != host_block))
+        return false;
+    return take_shot(g_tamper_h2d.shots);
+}
+
 // ---------------------------------------------------------------- device buffers
 
 // A pinned host buffer mirrored by a device buffer of the same size, plus
@@ -192,7 +233,9 @@ struct Mirror {
     size_t cap = 0;
     uint8_t* stage = nullptr;
     size_t stage_cap = 0;
-    hipEvent_t ev_a = nullptr, ev_b = nullptr;
+    hipEvent_t ev_a = nullptr;  // H2D: wire records landed; D2H: records sealed
+    hipEvent_t ev_b = nullptr;  // H2D: slot free again; D2H: records in host memory
+    hipEvent_t ev_c = nullptr;  // H2D: the slot's kernel is done
 
     Mirror() = default;
     Mirror(const Mirror&) = delete;
@@ -205,12 +248,14 @@ struct Mirror {
         if (stage) (void)hipFree(stage);
         if (ev_a) (void)hipEventDestroy(ev_a);
         if (ev_b) (void)hipEventDestroy(ev_b);
+        if (ev_c) (void)hipEventDestroy(ev_c);
     }
 
     bool init()
     {
         return hipEventCreateWithFlags(&ev_a, hipEventDisableTiming) == hipSuccess &&
-               hipEventCreateWithFlags(&ev_b, hipEventDisableTiming) == hipSuccess;
+               hipEventCreateWithFlags(&ev_b, hipEventDisableTiming) == hipSuccess &&
+               hipEventCreateWithFlags(&ev_c, hipEventDisableTiming) == hipSuccess;
     }
     // Callers guarantee no queued work still uses the buffers.
     bool reserve(size_t need, size_t stage_need)
@@ -237,15 +282,38 @@ struct Mirror {
     }
 };
 
-struct DeviceState {
-    hipStream_t h2d = nullptr;  // H2D copies of the reload ring
-    hipStream_t d2h = nullptr;  // D2H copies of sealed records
-    std::mutex ring_lock;
-    std::vector<std::unique_ptr<Mirror>> ring;
-    std::vector<bool> ring_used;
+// Pinned status words of one observed swap and the event after their copy.
+struct StatusBuf {
+    uint32_t* host = nullptr;
+    size_t cap = 0;  // words
+    hipEvent_t ready = nullptr;
+    ~StatusBuf()
+    {
+        if (host) (void)hipHostFree(host);
+        if (ready) (void)hipEventDestroy(ready);
+    }
+};
+
+// The reload ring of one caller stream: slots, their cursor and lock, the
+// copy stream of its H2D records and the stream of its status copies.
+struct StreamRing {
+    std::mutex lock;
+    hipStream_t copy = nullptr;
+    hipStream_t observe = nullptr;
+    std::vector<std::unique_ptr<Mirror>> slots;
+    std::vector<bool> used;
     size_t next = 0;
+};
+
+struct DeviceState {
+    int device = 0;
+    hipStream_t d2h = nullptr;  // D2H copies of sealed records
+    std::mutex rings_lock;
+    std::unordered_map<hipStream_t, std::unique_ptr<StreamRing>> rings;
     std::mutex pool_lock;
     std::vector<std::unique_ptr<Mirror>> free_bufs;  // D2H buffers between batches
+    std::mutex status_lock;
+    std::vector<std::unique_ptr<StatusBuf>> free_status;
 };
 
 DeviceState* device_state()
@@ -258,21 +326,61 @@ DeviceState* device_state()
     auto& st = states[dev];
     if (!st) {
         auto s = std::make_unique<DeviceState>();
+        s->device = dev;
         // default priority on purpose: every stream of the library shares it
-        if (hipStreamCreateWithFlags(&s->h2d, hipStreamNonBlocking) != hipSuccess ||
-            hipStreamCreateWithFlags(&s->d2h, hipStreamNonBlocking) != hipSuccess)
+        if (hipStreamCreateWithFlags(&s->d2h, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        st = std::move(s);
+    }
+    return st.get();
+}
+
+StreamRing* ring_of(DeviceState* ds, hipStream_t stream)
+{
+    std::lock_guard<std::mutex> g(ds->rings_lock);
+    auto& r = ds->rings[stream];
+    if (!r) {
+        auto nr = std::make_unique<StreamRing>();
+        if (hipStreamCreateWithFlags(&nr->copy, hipStreamNonBlocking) != hipSuccess ||
+            hipStreamCreateWithFlags(&nr->observe, hipStreamNonBlocking) != hipSuccess)
             return nullptr;
         size_t slots = 4;
         if (const char* e = std::getenv("SECURE_INFER_H2D_SLOTS")) slots = size_t(std::max(2, std::atoi(e)));
         for (size_t i = 0; i < slots; ++i) {
             auto mbuf = std::make_unique<Mirror>();
             if (!mbuf->init()) return nullptr;
-            s->ring.push_back(std::move(mbuf));
-            s->ring_used.push_back(false);
+            nr->slots.push_back(std::move(mbuf));
+            nr->used.push_back(false);
         }
-        st = std::move(s);
+        r = std::move(nr);
     }
-    return st.get();
+    return r.get();
+}
+
+std::unique_ptr<StatusBuf> take_status(DeviceState* ds, size_t words)
+{
+    {
+        std::lock_guard<std::mutex> g(ds->status_lock);
+        for (size_t i = 0; i < ds->free_status.size(); ++i)
+            if (ds->free_status[i]->cap >= words) {
+                auto b = std::move(ds->free_status[i]);
+                ds->free_status.erase(ds->free_status.begin() + long(i));
+                return b;
+            }
+    }
+    auto b = std::make_unique<StatusBuf>();
+    const size_t cap = std::max<size_t>(1024, (words + 1023) / 1024 * 1024);
+    if (hipHostMalloc(reinterpret_cast<void**>(&b->host), cap * 4, hipHostMallocDefault) != hipSuccess ||
+        hipEventCreateWithFlags(&b->ready, hipEventDisableTiming) != hipSuccess)
+        return nullptr;
+    b->cap = cap;
+    return b;
+}
+
+void give_status(DeviceState* ds, std::unique_ptr<StatusBuf> b)
+{
+    if (!b) return;
+    std::lock_guard<std::mutex> g(ds->status_lock);
+    ds->free_status.push_back(std::move(b));
 }
 
 bool valid_geometry(uint32_t codec, uint32_t heads, uint32_t dim, uint64_t host_block_bytes,
@@ -288,12 +396,162 @@ bool valid_geometry(uint32_t codec, uint32_t heads, uint32_t dim, uint64_t host_
     return host_block_bytes >= bytes;
 }
 
+// Every (host block, device slot) of a swap inside its pool.
+bool valid_mapping(const int64_t* mapping, uint32_t n, bool host_first, uint64_t host_nblocks,
+                   uint64_t nslots)
+{
+    for (uint32_t r = 0; r < n; ++r) {
+        const int64_t hb = mapping[2 * r + (host_first ? 0 : 1)];
+        const int64_t ds = mapping[2 * r + (host_first ? 1 : 0)];
+        if (hb < 0 || uint64_t(hb) >= host_nblocks || ds < 0 || uint64_t(ds) >= nslots) return false;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------- observed reloads
+
+// One observed swap: where each record came from and went to (for a strict
+// retry from the trusted host copy) and its status words.
+struct Observed {
+    DeviceState* ds = nullptr;
+    si_session* session = nullptr;
+    const uint8_t* host_base = nullptr;
+    uint64_t host_block_bytes = 0, host_nblocks = 0;
+    void* dev_cache = nullptr;
+    uint64_t slot_bytes = 0, nslots = 0;
+    uint32_t kind = 0, layer = 0, codec = 0, heads = 0, dim = 0;
+    hipStream_t stream = nullptr;
+    std::vector<int64_t> mapping;  // n (host block, device slot) pairs
+    std::unique_ptr<StatusBuf> status;
+};
+
+std::mutex g_obs_lock;
+std::multimap<uint32_t, std::shared_ptr<Observed>> g_observed;
+
+// ---------------------------------------------------------------- H2D
+
+int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint64_t host_block_bytes,
+                  uint64_t host_nblocks, void* dev_cache, uint64_t slot_bytes, uint64_t nslots,
+                  const int64_t* mapping, uint32_t n, uint32_t kind, uint32_t layer, uint32_t codec_bits,
+                  uint32_t heads, uint32_t head_dim, uint32_t* fail_count, bool observe)
+{
+    if (!s || !host_base || !dev_cache || !mapping || n == 0 || kind > 1 || nslots == 0 || host_nblocks == 0)
+        return -1;
+    uint64_t bytes = 0;
+    if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
+    if (!valid_mapping(mapping, n, true, host_nblocks, nslots)) return -1;
+    const si_internal::SessionKeys keys = si_internal::session_keys(s);
+    if (bytes > keys.max_record_bytes) return -1;
+    DeviceState* ds = device_state();
+    if (!ds) return -1;
+    StreamRing* ring = ring_of(ds, stream);
+    if (!ring) return -1;
+    const uint64_t stride = secure_infer_wire_stride(bytes);
+    const uint64_t tag_off = tag_offset(bytes);
+    const size_t wire = size_t(n) * stride;
+    const size_t need = wire + size_t(n) * 8;
+
+    std::unique_ptr<StatusBuf> status;
+    if (observe && !(status = take_status(ds, n))) return -1;
+
+    std::lock_guard<std::mutex> g(ring->lock);
+    const size_t si = ring->next;
+    ring->next = (ring->next + 1) % ring->slots.size();
+    Mirror& sl = *ring->slots[si];
+    if (ring->used[si] && hipEventSynchronize(sl.ev_b) != hipSuccess) return -1;
+    if (!sl.reserve(need, codec_bits ? size_t(n) * tag_off : 0)) return -1;
+
+    const uint64_t t0 = si_internal::reserve_tickets(n);
+    if (!si_internal::replay_reserve_range(t0, n)) {
+        fprintf(stderr, "[secure_infer] duplicate H2D transfer tickets rejected at %llu\n",
+                static_cast<unsigned long long>(t0));
+        return -1;
+    }
+    int64_t* slot_ids = reinterpret_cast<int64_t*>(sl.host + wire);
+    std::atomic<int> bad{0};
+    Pool::get().parallel_for(n, [&](size_t r) {
+        const int64_t hb = mapping[2 * r];
+        slot_ids[r] = mapping[2 * r + 1];
+        uint8_t* rec = sl.host + r * stride;
+        const uint8_t* src = static_cast<const uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes;
+        uint8_t* aad = rec + tag_off + 32;
+        uint8_t iv[12];
+        record_iv(keys, t0 + r, iv);
+        if (secure_infer_build_gcm_aad(src, bytes, 1, t0 + r, 0, keys.nonce, aad) != 1 ||
+            !gcm_seal(keys.key, iv, aad, 64, src, bytes, rec, rec + tag_off)) {
+            bad.store(1);
+            return;
+        }
+        memset(rec + bytes, 0, tag_off - bytes);
+        memset(rec + tag_off + 16, 0, 16);  // status slot
+        if (tamper_h2d(layer, kind, hb)) rec[0] ^= 0x01;
+    });
+    if (bad.load()) return -1;
+    if (hipMemcpyAsync(sl.dev, sl.host, need, hipMemcpyHostToDevice, ring->copy) != hipSuccess ||
+        hipEventRecord(sl.ev_a, ring->copy) != hipSuccess || hipStreamWaitEvent(stream, sl.ev_a, 0) != hipSuccess)
+        return -1;
+    si_reload_desc d{};
+    d.wire = sl.dev;
+    d.wire_stride = stride;
+    d.bytes = bytes;
+    d.nrec = n;
+    d.n_k = kind == 0 ? n : 0;
+    d.iv_words = nullptr;
+    d.ticket_base = t0;
+    d.cache_k = dev_cache;
+    d.cache_v = dev_cache;
+    d.slot_bytes = slot_bytes;
+    d.nslots = nslots;
+    d.slots = reinterpret_cast<const int64_t*>(sl.dev + wire);
+    d.codec_bits = codec_bits;
+    d.heads = heads;
+    d.head_dim = head_dim;
+    d.layer = layer;
+    d.staging = sl.stage;
+    d.fail_count = fail_count;
+    if (secure_infer_gpu_reload_layer(stream, s, &d) != 0) return -1;
+    ring->used[si] = true;
+    if (hipEventRecord(sl.ev_b, stream) != hipSuccess) return -1;
+    if (!observe) return 0;
+
+    // Status words to pinned memory once the kernel is done; the slot is free
+    // again after that copy.
+    if (hipEventRecord(sl.ev_c, stream) != hipSuccess ||
+        hipStreamWaitEvent(ring->observe, sl.ev_c, 0) != hipSuccess ||
+        hipMemcpy2DAsync(status->host, 4, sl.dev + tag_off + 16, stride, 4, n, hipMemcpyDeviceToHost,
+                         ring->observe) != hipSuccess ||
+        hipEventRecord(status->ready, ring->observe) != hipSuccess ||
+        hipEventRecord(sl.ev_b, ring->observe) != hipSuccess)
+        return -1;
+    auto ob = std::make_shared<Observed>();
+    ob->ds = ds;
+    ob->session = s;
+    ob->host_base = static_cast<const uint8_t*>(host_base);
+    ob->host_block_bytes = host_block_bytes;
+    ob->host_nblocks = host_nblocks;
+    ob->dev_cache = dev_cache;
+    ob->slot_bytes = slot_bytes;
+    ob->nslots = nslots;
+    ob->kind = kind;
+    ob->layer = layer;
+    ob->codec = codec_bits;
+    ob->heads = heads;
+    ob->dim = head_dim;
+    ob->stream = stream;
+    ob->mapping.assign(mapping, mapping + 2 * size_t(n));
+    ob->status = std::move(status);
+    std::lock_guard<std::mutex> go(g_obs_lock);
+    g_observed.emplace(layer, std::move(ob));
+    return 0;
+}
+
 // ---------------------------------------------------------------- D2H batches
 
 struct D2HJob {
     std::unique_ptr<Mirror> buf;
     uint32_t n = 0;
     uint64_t bytes = 0, stride = 0, tag_off = 0, t0 = 0;
+    uint64_t fail_off = 0;  // device u32 counting records with a bad slot id
     uint8_t* host_base = nullptr;
     uint64_t host_block_bytes = 0;
     std::vector<int64_t> host_blocks;
@@ -307,10 +565,10 @@ struct D2HBatch {
     size_t group_first = 0;  // first job of the open group
     std::vector<hipStream_t> streams;
     std::vector<hipEvent_t> joins;
-    std::atomic<size_t> pending{0};
-    std::atomic<uint64_t> failures{0};
     std::mutex m;
     std::condition_variable cv;
+    size_t pending = 0;  // verification tasks in flight (guarded by m)
+    std::atomic<uint64_t> failures{0};
 };
 
 thread_local std::unique_ptr<D2HBatch> t_batch;
@@ -336,9 +594,18 @@ void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
     if (hipEventSynchronize(job->buf->ev_b) != hipSuccess) {
         bad = r1 - r0;
     } else {
+        // The device's count of records sealed over a bad slot id (checked by
+        // the first task of the job; such a record also carries a tag that
+        // cannot verify).
+        if (r0 == 0) {
+            uint32_t dev_fail = 0;
+            memcpy(&dev_fail, job->buf->host + job->fail_off, 4);
+            bad += dev_fail;
+        }
         for (uint32_t r = r0; r < r1; ++r) {
-            const uint8_t* rec = job->buf->host + uint64_t(r) * job->stride;
+            uint8_t* rec = job->buf->host + uint64_t(r) * job->stride;
             uint8_t* dst = job->host_base + uint64_t(job->host_blocks[r]) * job->host_block_bytes;
+            if (take_shot(g_tamper_d2h)) rec[0] ^= 0x01;
             uint8_t iv[12];
             record_iv(job->keys, job->t0 + r, iv);
             if (!gcm_open(job->keys.key, iv, rec + job->tag_off + 32, 64, rec, job->bytes,
@@ -349,93 +616,119 @@ void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
         }
     }
     if (bad) b->failures.fetch_add(bad);
-    if (b->pending.fetch_sub(1) == 1) {
-        std::lock_guard<std::mutex> g(b->m);
-        b->cv.notify_all();
-    }
+    // The decrement and the notification happen under the batch's lock:
+    // batch_end may destroy the batch as soon as it sees pending == 0.
+    std::lock_guard<std::mutex> g(b->m);
+    if (--b->pending == 0) b->cv.notify_all();
 }
 
 }  // namespace
+
+namespace si_internal {
+
+int wait_observed_layer(uint32_t layer, bool* found)
+{
+    *found = false;
+    for (unsigned round = 0;; ++round) {
+        std::vector<std::shared_ptr<Observed>> recs;
+        {
+            std::lock_guard<std::mutex> g(g_obs_lock);
+            auto range = g_observed.equal_range(layer);
+            for (auto it = range.first; it != range.second; ++it) recs.push_back(it->second);
+            g_observed.erase(range.first, range.second);
+        }
+        if (recs.empty()) return 0;
+        *found = true;
+        int rc = 0;
+        // Records that failed once: (swap, index).
+        std::vector<std::pair<Observed*, uint32_t>> retry;
+        for (const auto& ob : recs) {
+            const uint32_t n = uint32_t(ob->mapping.size() / 2);
+            if (hipEventSynchronize(ob->status->ready) != hipSuccess) {
+                rc = -1;
+                continue;
+            }
+            for (uint32_t r = 0; r < n; ++r) {
+                const uint32_t st = ob->status->host[r];
+                if (st == 1u) continue;
+                if (st != 0u || round != 0) rc = -1;
+                else retry.emplace_back(ob.get(), r);
+            }
+        }
+        if (rc == 0) {
+            // A record that failed is re-sealed from the trusted host copy
+            // under a fresh ticket; its verifier result is checked in the next
+            // round, before the layer is used (secure_infer.cpp:7316-7330).
+            for (size_t i = 0; i < retry.size() && rc == 0;) {
+                Observed* ob = retry[i].first;
+                std::vector<int64_t> part;
+                for (; i < retry.size() && retry[i].first == ob; ++i) {
+                    part.push_back(ob->mapping[2 * retry[i].second]);
+                    part.push_back(ob->mapping[2 * retry[i].second + 1]);
+                }
+                const uint32_t m = uint32_t(part.size() / 2);
+                // The retry runs on the device (and ring) the swap used.
+                int cur = 0;
+                if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(ob->ds->device) != hipSuccess) {
+                    rc = -1;
+                    break;
+                }
+                if (h2d_swap_impl(ob->stream, ob->session, ob->host_base, ob->host_block_bytes,
+                                  ob->host_nblocks, ob->dev_cache, ob->slot_bytes, ob->nslots, part.data(), m,
+                                  ob->kind, ob->layer, ob->codec, ob->heads, ob->dim, nullptr, true) != 0 ||
+                    hipStreamSynchronize(ob->stream) != hipSuccess)
+                    rc = -1;
+                (void)hipSetDevice(cur);
+            }
+        }
+        for (auto& ob : recs) give_status(ob->ds, std::move(ob->status));
+        if (rc != 0) {
+            // Drop the retries' own observations too: the layer has failed.
+            std::lock_guard<std::mutex> g(g_obs_lock);
+            auto range = g_observed.equal_range(layer);
+            std::vector<std::shared_ptr<Observed>> rest;
+            for (auto it = range.first; it != range.second; ++it) rest.push_back(it->second);
+            g_observed.erase(range.first, range.second);
+            for (auto& ob : rest) {
+                (void)hipEventSynchronize(ob->status->ready);
+                give_status(ob->ds, std::move(ob->status));
+            }
+            return -1;
+        }
+        if (retry.empty()) return 0;
+    }
+}
+
+}  // namespace si_internal
 
 extern "C" {
 
 int secure_infer_host_threads(void) { return int(Pool::get().threads()); }
 
 int secure_infer_h2d_swap(hipStream_t stream, si_session* s, const void* host_base,
-                          uint64_t host_block_bytes, void* dev_cache, uint64_t slot_bytes,
-                          uint64_t nslots, const int64_t* mapping, uint32_t n, uint32_t kind,
-                          uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim,
-                          uint32_t* fail_count)
+                          uint64_t host_block_bytes, uint64_t host_nblocks, void* dev_cache,
+                          uint64_t slot_bytes, uint64_t nslots, const int64_t* mapping, uint32_t n,
+                          uint32_t kind, uint32_t layer, uint32_t codec_bits, uint32_t heads,
+                          uint32_t head_dim, uint32_t* fail_count)
 {
-    if (!s || !host_base || !dev_cache || !mapping || n == 0 || kind > 1 || nslots == 0) return -1;
-    uint64_t bytes = 0;
-    if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
-    const si_internal::SessionKeys keys = si_internal::session_keys(s);
-    if (bytes > keys.max_record_bytes) return -1;
-    DeviceState* ds = device_state();
-    if (!ds) return -1;
-    const uint64_t stride = secure_infer_wire_stride(bytes);
-    const uint64_t tag_off = tag_offset(bytes);
-    const size_t wire = size_t(n) * stride;
-    const size_t need = wire + size_t(n) * 8;
+    return h2d_swap_impl(stream, s, host_base, host_block_bytes, host_nblocks, dev_cache, slot_bytes, nslots,
+                         mapping, n, kind, layer, codec_bits, heads, head_dim, fail_count,
+                         si_internal::group_open());
+}
 
-    std::lock_guard<std::mutex> g(ds->ring_lock);
-    const size_t si = ds->next;
-    ds->next = (ds->next + 1) % ds->ring.size();
-    Mirror& sl = *ds->ring[si];
-    if (ds->ring_used[si] && hipEventSynchronize(sl.ev_b) != hipSuccess) return -1;
-    if (!sl.reserve(need, codec_bits ? size_t(n) * tag_off : 0)) return -1;
+int secure_infer_test_tamper_h2d(int32_t layer, int32_t kind, int64_t host_block, uint32_t shots)
+{
+    g_tamper_h2d.shots.store(0);
+    g_tamper_h2d.layer.store(layer);
+    g_tamper_h2d.kind.store(kind);
+    g_tamper_h2d.block.store(host_block);
+    g_tamper_h2d.shots.store(int64_t(shots));
+    return 0;
+}
 
-    const uint64_t t0 = si_internal::reserve_tickets(n);
-    int64_t* slot_ids = reinterpret_cast<int64_t*>(sl.host + wire);
-    std::atomic<int> bad{0};
-    Pool::get().parallel_for(n, [&](size_t r) {
-        const int64_t hb = mapping[2 * r];
-        slot_ids[r] = mapping[2 * r + 1];
-        uint8_t* rec = sl.host + r * stride;
-        if (hb < 0) {
-            bad.store(1);
-            return;
-        }
-        const uint8_t* src = static_cast<const uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes;
-        uint8_t* aad = rec + tag_off + 32;
-        uint8_t iv[12];
-        record_iv(keys, t0 + r, iv);
-        if (secure_infer_build_gcm_aad(src, bytes, 1, t0 + r, 0, keys.nonce, aad) != 1 ||
-            !gcm_seal(keys.key, iv, aad, 64, src, bytes, rec, rec + tag_off)) {
-            bad.store(1);
-            return;
-        }
-        memset(rec + bytes, 0, tag_off - bytes);
-        memset(rec + tag_off + 16, 0, 16);  // status slot
-    });
-    if (bad.load()) return -1;
-    if (hipMemcpyAsync(sl.dev, sl.host, need, hipMemcpyHostToDevice, ds->h2d) != hipSuccess ||
-        hipEventRecord(sl.ev_a, ds->h2d) != hipSuccess || hipStreamWaitEvent(stream, sl.ev_a, 0) != hipSuccess)
-        return -1;
-    si_reload_desc d{};
-    d.wire = sl.dev;
-    d.wire_stride = stride;
-    d.bytes = bytes;
-    d.nrec = n;
-    d.n_k = kind == 0 ? n : 0;
-    d.iv_words = nullptr;
-    d.ticket_base = t0;
-    d.cache_k = dev_cache;
-    d.cache_v = dev_cache;
-    d.slot_bytes = slot_bytes;
-    d.nslots = nslots;
-    d.slots = reinterpret_cast<const int64_t*>(sl.dev + wire);
-    d.codec_bits = codec_bits;
-    d.heads = heads;
-    d.head_dim = head_dim;
-    d.layer = layer;
-    d.staging = sl.stage;
-    d.fail_count = fail_count;
-    if (secure_infer_gpu_reload_layer(stream, s, &d) != 0) return -1;
-    if (hipEventRecord(sl.ev_b, stream) != hipSuccess) return -1;
-    ds->ring_used[si] = true;
-    si_internal::group_note(stream, layer, fail_count);
+int secure_infer_test_tamper_d2h(uint32_t shots)
+{
+    g_tamper_d2h.store(int64_t(shots));
     return 0;
 }
 
@@ -460,15 +753,17 @@ int secure_infer_d2h_group_begin(size_t expected_tasks)
 }
 
 int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cache, uint64_t slot_bytes,
-                          uint64_t nslots, void* host_base, uint64_t host_block_bytes,
+                          uint64_t nslots, void* host_base, uint64_t host_block_bytes, uint64_t host_nblocks,
                           const int64_t* mapping, uint32_t n, uint32_t kind, uint32_t layer,
                           uint32_t codec_bits, uint32_t heads, uint32_t head_dim)
 {
     D2HBatch* b = t_batch.get();
     if (!b || !b->group_open) return -1;
-    if (!s || !dev_cache || !host_base || !mapping || n == 0 || kind > 1 || nslots == 0) return -1;
+    if (!s || !dev_cache || !host_base || !mapping || n == 0 || kind > 1 || nslots == 0 || host_nblocks == 0)
+        return -1;
     uint64_t bytes = 0;
     if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
+    if (!valid_mapping(mapping, n, false, host_nblocks, nslots)) return -1;
     auto job = std::make_unique<D2HJob>();
     job->keys = si_internal::session_keys(s);
     if (bytes > job->keys.max_record_bytes) return -1;
@@ -481,16 +776,25 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cac
     job->host_base = static_cast<uint8_t*>(host_base);
     job->host_block_bytes = host_block_bytes;
     job->host_blocks.resize(n);
+    // [wire records][slot ids, n x 8][fail word, 16]
     const size_t wire = size_t(n) * job->stride;
-    if (!job->buf->reserve(wire + size_t(n) * 8, codec_bits ? size_t(n) * job->tag_off : 0)) return -1;
+    job->fail_off = wire + size_t(n) * 8;
+    const size_t need = job->fail_off + 16;
+    if (!job->buf->reserve(need, codec_bits ? size_t(n) * job->tag_off : 0)) return -1;
     job->t0 = si_internal::reserve_tickets(n);
+    if (!si_internal::replay_reserve_range(job->t0, n)) {
+        fprintf(stderr, "[secure_infer] duplicate D2H transfer tickets rejected at %llu\n",
+                static_cast<unsigned long long>(job->t0));
+        return -1;
+    }
 
-    // AADs (direction 2) and device slot ids go up first, on the caller's stream.
+    // AADs (direction 2), device slot ids and the zeroed fail word go up
+    // first, on the caller's stream.
     uint8_t* h = job->buf->host;
     int64_t* slot_ids = reinterpret_cast<int64_t*>(h + wire);
+    memset(h + job->fail_off, 0, 16);
     for (uint32_t r = 0; r < n; ++r) {
         const int64_t ds_id = mapping[2 * r], hb = mapping[2 * r + 1];
-        if (hb < 0) return -1;
         slot_ids[r] = ds_id;
         job->host_blocks[r] = hb;
         const uint8_t* dst = job->host_base + uint64_t(hb) * host_block_bytes;
@@ -501,7 +805,7 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cac
     uint8_t* d = job->buf->dev;
     if (hipMemcpy2DAsync(d + job->tag_off + 32, job->stride, h + job->tag_off + 32, job->stride, 64, n,
                          hipMemcpyHostToDevice, stream) != hipSuccess ||
-        hipMemcpyAsync(d + wire, h + wire, size_t(n) * 8, hipMemcpyHostToDevice, stream) != hipSuccess)
+        hipMemcpyAsync(d + wire, h + wire, size_t(n) * 8 + 16, hipMemcpyHostToDevice, stream) != hipSuccess)
         return -1;
     si_writeback_desc w{};
     w.wire = d;
@@ -521,12 +825,13 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cac
     w.head_dim = head_dim;
     w.layer = layer;
     w.staging = job->buf->stage;
-    w.fail_count = nullptr;
+    w.fail_count = reinterpret_cast<uint32_t*>(d + job->fail_off);
     if (secure_infer_gpu_writeback_layer(stream, s, &w) != 0) return -1;
     DeviceState* ds = b->ds;
     if (hipEventRecord(job->buf->ev_a, stream) != hipSuccess ||
         hipStreamWaitEvent(ds->d2h, job->buf->ev_a, 0) != hipSuccess ||
         hipMemcpyAsync(h, d, wire, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
+        hipMemcpyAsync(h + job->fail_off, d + job->fail_off, 16, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
         hipEventRecord(job->buf->ev_b, ds->d2h) != hipSuccess)
         return -1;
     if (std::find(b->streams.begin(), b->streams.end(), stream) == b->streams.end())
@@ -545,7 +850,10 @@ int secure_infer_d2h_group_end(void)
         D2HJob* job = b->jobs[j].get();
         for (uint32_t r0 = 0; r0 < job->n; r0 += per_task) {
             const uint32_t r1 = std::min(job->n, r0 + per_task);
-            b->pending.fetch_add(1);
+            {
+                std::lock_guard<std::mutex> g(b->m);
+                ++b->pending;
+            }
             Pool::get().submit([b, job, r0, r1] { verify_records(b, job, r0, r1); });
         }
     }
@@ -572,7 +880,7 @@ int secure_infer_d2h_batch_end(void)
     std::unique_ptr<D2HBatch> b = std::move(t_batch);
     {
         std::unique_lock<std::mutex> g(b->m);
-        b->cv.wait(g, [&] { return b->pending.load() == 0; });
+        b->cv.wait(g, [&] { return b->pending == 0; });
     }
     for (hipEvent_t e : b->joins) {
         (void)hipEventSynchronize(e);

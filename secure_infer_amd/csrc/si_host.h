@@ -21,8 +21,17 @@ SessionKeys session_keys(const si_session* s);
 // n consecutive fresh transfer tickets (process-monotonic, never 0).
 uint64_t reserve_tickets(uint32_t n);
 
-// Registers a reload issued on `stream` with the calling thread's open layer
-// group; false when no group is open.
-bool group_note(hipStream_t stream, uint32_t layer, uint32_t* fail_count);
+// Marks tickets [t0, t0 + n) as used; false if any of them was used before
+// (the replay set of secure_infer_gcm_replay_reserve).
+bool replay_reserve_range(uint64_t t0, uint64_t n);
+
+// True while the calling thread is inside secure_infer_h2d_layer_group_begin/end.
+bool group_open();
+
+// Observed H2D swaps of `layer` (host-sealed records): waits for their
+// status words, re-seals every record that failed once under a fresh ticket
+// and checks it again.  0 if every record authenticated, -1 otherwise;
+// *found tells whether the layer had observed swaps.
+int wait_observed_layer(uint32_t layer, bool* found);
 
 }  // namespace si_internal

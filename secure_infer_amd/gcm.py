@@ -15,6 +15,7 @@ asynchronous on the given (default: current) stream.
 from __future__ import annotations
 
 import ctypes as ct
+import math
 import struct
 from dataclasses import dataclass
 
@@ -175,22 +176,59 @@ def auth_gate(data, status, stream=None) -> None:
 
 # ------------------------------------------------------------------ sessions
 
+CODEC_MODES = ("none", "int8", "int4", "mixed")
+
+
+def layer_bits(mode: str, layer: int, layers: int) -> int:
+    """Codec bits of one layer (transport_codec.layer_bits, transport_codec.py:18-19):
+    ``mixed`` keeps int8 for the first ceil(L/3) layers and int4 after them."""
+    if mode not in CODEC_MODES:
+        raise ValueError(f"codec mode {mode!r} not in {CODEC_MODES}")
+    if mode == "none":
+        return SI_CODEC_NONE
+    return SI_CODEC_INT8 if mode == "int8" or (mode == "mixed" and layer < math.ceil(layers / 3)) \
+        else SI_CODEC_INT4
+
+
 @dataclass
 class LayerShape:
-    """Geometry of one layer's records: `nblocks` 128-token blocks per kind."""
+    """Geometry of one layer's records: kv heads x head_dim per token, and the
+    transport codec -- either fixed bits for every layer (``codec_bits``) or a
+    reference codec mode (``codec`` in none / int8 / int4 / mixed) over
+    ``layers`` layers."""
     heads: int
     head_dim: int
     codec_bits: int = SI_CODEC_NONE
+    codec: str | None = None
+    layers: int | None = None
+
+    def __post_init__(self):
+        if self.codec is not None:
+            if self.codec not in CODEC_MODES:
+                raise ValueError(f"codec mode {self.codec!r} not in {CODEC_MODES}")
+            if self.codec == "mixed" and not self.layers:
+                raise ValueError("the mixed codec needs the layer count")
+
+    def bits_for(self, layer: int) -> int:
+        if self.codec is None:
+            return self.codec_bits
+        return layer_bits(self.codec, layer, self.layers or 1)
 
     @property
     def block_bytes(self) -> int:
         return 128 * self.heads * self.head_dim * 2
 
+    def record_bytes_for(self, layer: int) -> int:
+        bits = self.bits_for(layer)
+        if bits == SI_CODEC_NONE:
+            return self.block_bytes
+        return codec_width(bits, self.heads, self.head_dim)
+
     @property
     def record_bytes(self) -> int:
-        if self.codec_bits == SI_CODEC_NONE:
-            return self.block_bytes
-        return codec_width(self.codec_bits, self.heads, self.head_dim)
+        if self.codec == "mixed":
+            raise ValueError("record size depends on the layer under the mixed codec: use record_bytes_for")
+        return self.record_bytes_for(0)
 
 
 class GcmSession:
@@ -306,6 +344,26 @@ def set_straddle_rows(rows: int) -> None:
     _check(lib().secure_infer_gpu_set_straddle_rows(rows), "set_straddle_rows")
 
 
+def reference_ticket_order(nblocks: int, group_blocks: int) -> list[tuple[int, int]]:
+    """(kind, block) of a layer's records in the order NativeTransfer submits
+    them, i.e. the order their tickets follow: groups of ``group_blocks``
+    (0: one group) from the tail, K then V within a group, blocks ascending
+    (native_layerwise.py:96-129 with one slice stream)."""
+    order = []
+    end = nblocks
+    g = group_blocks if group_blocks and nblocks > group_blocks else nblocks
+    while end > 0:
+        start = max(0, end - g)
+        for kind in (0, 1):
+            order.extend((kind, b) for b in range(start, end))
+        end = start
+    return order
+
+
+def _torch_stream(stream):
+    return stream if stream is not None else torch.cuda.current_stream()
+
+
 class NativeTransfer:
     """Per-layer authenticated reload driver (native_layerwise.py:85-130).
 
@@ -314,83 +372,127 @@ class NativeTransfer:
     ([num_cpu_blocks, 128, h, d] bf16, or packet arrays [num_cpu_blocks,
     width] uint8 with a codec), ``mapping`` = the [N, 2] int64 (cpu_block,
     gpu_slot) table of swap_blocks, ``destination`` = (cache_k, cache_v) device
-    paged caches [num_slots, 128, h, d].  Each kind is sealed on the host
-    (OpenSSL, worker pool), copied through the library's pinned ring on its
-    copy stream and verified / decrypted / scattered on the device; the call
-    returns once the work is queued.  The layer's authentication result is
-    available through ``wait_layer`` (wait_for_layer_load, connector.py:378-410).
+    paged caches [num_slots, 128, h, d].
+
+    * With ``causal_group_blocks`` = G (the reference sets RUNTIME_LOAD_CHUNK /
+      128, connector.py:288) a layer's mapping is cut into groups of G blocks
+      submitted tail first, each inside its own layer-group brackets
+      (native_layerwise.py:96-112); records therefore take tickets in
+      (layer, group, kind, slice, block) order.
+    * Each group stripes its rows over the slice ``streams``
+      (native_layerwise.py:113-129): every slice stream first waits for the
+      caller's stream, and the caller's stream waits for all of them after
+      the submission, so attention on the caller's stream is ordered after
+      the reload.
+    * Each (kind, slice) is sealed on the host (OpenSSL, worker pool), copied
+      through the slice stream's pinned ring and verified / decrypted /
+      scattered on the device; the call returns once the work is queued.
+      ``wait_layer`` returns the layer's authentication result after at most
+      one strict retry per failed record (wait_for_layer_load,
+      connector.py:378-410; secure_infer.cpp:7303-7333).
 
     ``single_layer_wire_transfer((wire, mapping), destination, ticket_base)``
     reloads records already resident on the device (K blocks then V blocks,
-    tickets ticket_base .. ticket_base+2N-1).
+    tickets ticket_base .. ticket_base+2N-1, or explicit per-record IV words);
+    a failure among them is final (there is no host copy to retry from).
     """
 
-    def __init__(self, session: GcmSession, shape: LayerShape, stream=None):
+    def __init__(self, session: GcmSession, shape: LayerShape, stream=None, streams=None,
+                 causal_group_blocks: int = 0):
         self.session = session
         self.shape = shape
         self.stream = stream
+        self.streams = list(streams) if streams else [stream]
+        self.causal_group_blocks = int(causal_group_blocks)
         self.layer = 0
-        self._fail = {}
-        self._events = {}
+        self._keep = {}
         self._staging = None
 
-    def _fail_counter(self, device) -> torch.Tensor:
-        fail = torch.zeros(1, dtype=torch.int32, device=device)
-        self._fail[self.layer] = fail
-        return fail
-
-    def single_layer_kv_transfer(self, payload, destination) -> None:
+    def single_layer_kv_transfer(self, payload, destination, *unused) -> None:
         host, mapping = payload
         mapping = mapping.to(device="cpu", dtype=torch.int64).contiguous()
+        group = self.causal_group_blocks
+        if group and mapping.shape[0] > group:
+            layer = self.layer
+            self.causal_group_blocks = 0
+            try:
+                end = int(mapping.shape[0])
+                while end > 0:
+                    start = max(0, end - group)
+                    self.layer = layer
+                    self.single_layer_kv_transfer((host, mapping[start:end]), destination)
+                    end = start
+            finally:
+                self.causal_group_blocks = group
+                self.layer = layer + 1
+            return
         n = int(mapping.shape[0])
         if n == 0:
             self.layer += 1
             return
-        fail = self._fail_counter(destination[0].device)
-        stream = _stream(self.stream)
+        bits = self.shape.bits_for(self.layer)
+        parent = torch.cuda.current_stream()
+        streams = [_torch_stream(s) for s in self.streams]
+        for st in streams:
+            if st != parent:
+                st.wait_stream(parent)
         _check(lib().secure_infer_h2d_layer_group_begin(2 * n), "h2d_layer_group_begin")
         try:
             for kind, (src, dst) in enumerate(zip(host, destination)):
                 if src.is_cuda or not src.is_contiguous():
                     raise ValueError("host pools must be contiguous CPU tensors")
                 _dev(dst, "destination cache")
-                _check(lib().secure_infer_h2d_swap(
-                    stream, self.session._h, ct.c_void_p(src.data_ptr()),
-                    src[0].numel() * src.element_size(), ct.c_void_p(dst.data_ptr()),
-                    dst[0].numel() * dst.element_size(), dst.shape[0],
-                    ct.c_void_p(mapping.data_ptr()), n, kind, self.layer, self.shape.codec_bits,
-                    self.shape.heads, self.shape.head_dim, ct.c_void_p(fail.data_ptr())),
-                    "h2d_swap")
+                for j, st in enumerate(streams):
+                    part = mapping[n * j // len(streams):n * (j + 1) // len(streams)].contiguous()
+                    if part.shape[0] == 0:
+                        continue
+                    _check(lib().secure_infer_h2d_swap(
+                        _stream(st), self.session._h, ct.c_void_p(src.data_ptr()),
+                        src[0].numel() * src.element_size(), src.shape[0], ct.c_void_p(dst.data_ptr()),
+                        dst[0].numel() * dst.element_size(), dst.shape[0],
+                        ct.c_void_p(part.data_ptr()), part.shape[0], kind, self.layer, bits,
+                        self.shape.heads, self.shape.head_dim, None), "h2d_swap")
         finally:
             _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
+        for st in streams:
+            if st != parent:
+                parent.wait_stream(st)
         self.layer += 1
 
-    def single_layer_wire_transfer(self, payload, destination, ticket_base: int) -> None:
+    def single_layer_wire_transfer(self, payload, destination, ticket_base: int = 0,
+                                   iv_words_dev: torch.Tensor | None = None) -> None:
         wire, mapping = payload
         cache_k, cache_v = destination
         n = int(mapping.shape[0])
-        slots = mapping[:, 1].to(device=cache_k.device, dtype=torch.int64)
-        slots = torch.cat([slots, slots]).contiguous()
-        nbytes = self.shape.record_bytes
-        staging = None
-        if self.shape.codec_bits:
-            need = 2 * n * wire_tag_offset(nbytes)
-            if self._staging is None or self._staging.numel() < need:
-                self._staging = torch.empty(need, dtype=torch.uint8, device=cache_k.device)
-            staging = self._staging
-        fail = self._fail_counter(cache_k.device)
-        _check(lib().secure_infer_h2d_layer_group_begin(2 * n), "h2d_layer_group_begin")
-        try:
-            self.session.reload_layer(wire, nbytes, 2 * n, n, cache_k, cache_v, slots,
-                                      ticket_base=ticket_base,
-                                      codec_bits=self.shape.codec_bits, heads=self.shape.heads,
-                                      head_dim=self.shape.head_dim, layer=self.layer,
-                                      staging=staging, fail_count=fail, stream=self.stream)
-        finally:
-            _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
+        bits = self.shape.bits_for(self.layer)
+        nbytes = self.shape.record_bytes_for(self.layer)
+        parent = torch.cuda.current_stream()
+        launch = _torch_stream(self.stream)
+        if launch != parent:
+            launch.wait_stream(parent)
+        # Everything the kernel reads or counts into is made on the launch
+        # stream, so its initialisation is ordered before the kernel, and kept
+        # until the layer is observed.
+        with torch.cuda.stream(launch):
+            slots = mapping[:, 1].to(device=cache_k.device, dtype=torch.int64)
+            slots = torch.cat([slots, slots]).contiguous()
+            fail = torch.zeros(1, dtype=torch.int32, device=cache_k.device)
+            staging = None
+            if bits:
+                need = 2 * n * wire_tag_offset(nbytes)
+                if self._staging is None or self._staging.numel() < need:
+                    self._staging = torch.empty(need, dtype=torch.uint8, device=cache_k.device)
+                staging = self._staging
+        self.session.reload_layer(wire, nbytes, 2 * n, n, cache_k, cache_v, slots,
+                                  ticket_base=ticket_base, iv_words_dev=iv_words_dev,
+                                  codec_bits=bits, heads=self.shape.heads,
+                                  head_dim=self.shape.head_dim, layer=self.layer,
+                                  staging=staging, fail_count=fail, stream=launch)
         ev = torch.cuda.Event()
-        ev.record(self.stream if self.stream is not None else torch.cuda.current_stream())
-        self._events[self.layer] = ev
+        ev.record(launch)
+        if launch != parent:
+            parent.wait_stream(launch)
+        self._keep[self.layer] = (ev, fail, slots)
         _check(lib().secure_infer_recovery_track_layer(self.layer, ct.c_void_p(ev.cuda_event),
                                                        ct.c_void_p(fail.data_ptr())),
                "recovery_track_layer")
@@ -399,8 +501,7 @@ class NativeTransfer:
     def wait_layer(self, layer: int) -> int:
         """0 if every record of `layer` authenticated, -1 otherwise."""
         rc = int(lib().secure_infer_recovery_wait_layer_authentication(layer))
-        self._fail.pop(layer, None)
-        self._events.pop(layer, None)
+        self._keep.pop(layer, None)
         return rc
 
 
@@ -414,7 +515,8 @@ class D2HTransfer:
     [N, 2] int64 (gpu_slot, cpu_block) table.  Blocks are sealed on the device
     (gather, codec quantise, AES-GCM), copied to pinned memory on the library's
     D2H stream and authenticated + decrypted into the host pools by the worker
-    pool.  Raises if any record fails host verification (it is zeroed).
+    pool.  Raises if any record fails host verification (it is zeroed), or if
+    a mapping entry lies outside its pool (nothing is then queued for it).
     """
 
     def __init__(self, session: GcmSession, shape: LayerShape, group_blocks: int = 16,
@@ -434,6 +536,7 @@ class D2HTransfer:
             raise RuntimeError("d2h_batch_begin failed")
         try:
             for layer, src, dst in zip(layers, src_tensors, dst_tensors):
+                bits = self.shape.bits_for(layer)
                 for kind in (0, 1):
                     s_cache, d_pool = src[kind], dst[kind]
                     _dev(s_cache, "source cache")
@@ -448,8 +551,8 @@ class D2HTransfer:
                                 stream, self.session._h, ct.c_void_p(s_cache.data_ptr()),
                                 s_cache[0].numel() * s_cache.element_size(), s_cache.shape[0],
                                 ct.c_void_p(d_pool.data_ptr()), d_pool[0].numel() * d_pool.element_size(),
-                                ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer,
-                                self.shape.codec_bits, self.shape.heads, self.shape.head_dim),
+                                d_pool.shape[0], ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer,
+                                bits, self.shape.heads, self.shape.head_dim),
                                 "d2h_swap")
                         finally:
                             _check(L.secure_infer_d2h_group_end(), "d2h_group_end")
@@ -458,3 +561,21 @@ class D2HTransfer:
             rc = L.secure_infer_d2h_batch_end()
         if rc != 0:
             raise RuntimeError("d2h batch: host authentication failed")
+
+
+def retire_transfer_prefetches() -> None:
+    """No-op export the reference's EncodedStore binds (transport_codec.py:50)."""
+    lib().secure_infer_retire_transfer_prefetches()
+
+
+def inject_h2d_tamper(layer: int = -1, kind: int = -1, host_block: int = -1, shots: int = 1) -> None:
+    """Test-only: flip the first ciphertext byte of the next `shots` H2D records
+    sealed from (layer, kind, host_block) (-1 = any) after sealing
+    (PIPE_GCM_TAMPER_H2D*, secure_infer.cpp:6139-6250)."""
+    _check(lib().secure_infer_test_tamper_h2d(layer, kind, host_block, shots), "test_tamper_h2d")
+
+
+def inject_d2h_tamper(shots: int = 1) -> None:
+    """Test-only: flip the first ciphertext byte of the next `shots` D2H records
+    before host authentication (PIPE_GCM_TAMPER_D2H, secure_infer.cpp:2451-2467)."""
+    _check(lib().secure_infer_test_tamper_d2h(shots), "test_tamper_d2h")

@@ -108,13 +108,13 @@ def test_error_returns_before_any_device_work():
     assert L.secure_infer_gpu_writeback_layer(None, None, None) == -1
     desc = _lib.SiReloadDesc(nrec=0)
     assert L.secure_infer_gpu_reload_layer(None, None, ct.byref(desc)) == -1
-    assert L.secure_infer_h2d_swap(None, None, one, 16, one, 16, 1, one, 0, 0, 0, 0, 0, 0, None) == -1
+    assert L.secure_infer_h2d_swap(None, None, one, 16, 1, one, 16, 1, one, 0, 0, 0, 0, 0, 0, None) == -1
     # D2H brackets without a batch (secure_infer.cpp:2707-2970 semantics)
     assert L.secure_infer_d2h_group_begin(1) == -1
     assert L.secure_infer_d2h_group_end() == 0
     assert L.secure_infer_d2h_batch_device_barrier() == -1
     assert L.secure_infer_d2h_batch_end() == 0
-    assert L.secure_infer_d2h_swap(None, None, one, 16, 1, one, 16, one, 1, 0, 0, 0, 0, 0) == -1
+    assert L.secure_infer_d2h_swap(None, None, one, 16, 1, one, 16, 1, one, 1, 0, 0, 0, 0, 0) == -1
     # layer-group nesting is thread-local
     assert L.secure_infer_h2d_layer_group_begin(4) == 0
     assert L.secure_infer_h2d_layer_group_begin(4) == -1
@@ -146,3 +146,57 @@ def test_error_returns_before_any_device_work():
     aad = (ct.c_uint8 * 64)()
     assert L.secure_infer_build_gcm_aad(one, 16, 3, 1, 0, 0, aad) == 0      # direction must be 1 or 2
     assert L.secure_infer_build_gcm_aad(one, 16, 1, 0, 0, 0, aad) == 0      # ticket 0
+
+
+def test_swaps_refuse_ids_outside_their_pools():
+    """secure_infer_h2d_swap checks every (host block, device slot) of its
+    mapping against the pool sizes before it touches the session, a ring or
+    the device: an id outside [0, host_nblocks) or [0, nslots) refuses the
+    whole call.  (The session pointer below is never dereferenced: the
+    refusal comes first.)"""
+    import ctypes as ct
+
+    import numpy as np
+
+    from secure_infer_amd import _lib
+    L = _lib.load()
+    host = np.zeros(4 * 256, np.uint8)
+    fake_session = ct.c_void_p(16)
+    dev = ct.c_void_p(4096)
+
+    def h2d(mapping, nhost=4, nslots=8):
+        m = np.ascontiguousarray(np.array(mapping, np.int64).reshape(-1, 2))
+        return L.secure_infer_h2d_swap(None, fake_session, host.ctypes.data_as(ct.c_void_p), 256, nhost, dev,
+                                       256, nslots, m.ctypes.data_as(ct.c_void_p), m.shape[0], 0, 0, 0, 0, 0,
+                                       None)
+    assert h2d([[4, 0]]) == -1            # host block == host_nblocks
+    assert h2d([[0, 1], [-1, 2]]) == -1   # negative host block
+    assert h2d([[0, 8]]) == -1            # slot == nslots
+    assert h2d([[1, 0], [2, -3]]) == -1   # negative slot
+    assert h2d([[0, 0]], nhost=0) == -1   # empty host pool
+    assert h2d([[0, 0]], nslots=0) == -1  # empty cache
+
+
+def test_replay_set_rejects_reused_tickets():
+    import secure_infer_amd as si
+    base = 7 * 10 ** 15
+    assert si.replay_reserve(base + 5)
+    assert si.replay_reserve(base + 7)
+    assert si.replay_reserve(base + 6)      # fills the gap between two runs
+    for t in (base + 5, base + 6, base + 7):
+        assert not si.replay_reserve(t)
+    assert si.replay_reserve(base + 4) and si.replay_reserve(base + 8)
+    assert not si.replay_reserve(base + 4)
+    assert si.replay_reserve(0)             # ticket 0 is never recorded (secure_infer.cpp:779)
+    assert si.replay_reserve(0)
+
+
+def test_prefetch_retirement_is_a_no_op():
+    """EncodedStore binds secure_infer_retire_transfer_prefetches
+    unconditionally (transport_codec.py:50); this library has no speculative
+    pools, so both calls return without effect."""
+    import ctypes as ct
+    from secure_infer_amd import _lib
+    lib = ct.CDLL(str(_lib.LIB_PATH))
+    lib.secure_infer_retire_transfer_prefetches()
+    lib.secure_infer_invalidate_transfer_prefetches()

@@ -1,0 +1,130 @@
+"""One full-size layer of every benchmark workload through the fused kernels,
+at its real record count and cache size (the share / pair layouts the 256-CU
+launch takes only appear at these sizes), checked record by record:
+
+* bf16 Llama-3-8B reload: 48 blocks -> 96 records of 262,144 B into 512-slot
+  caches (8 kv heads x 128);
+* int8 Llama-3-8B reload: 64 blocks -> 128 packets of 147,472 B;
+* int4 Qwen2.5-7B reload: 64 blocks -> 128 packets of 40,976 B (4 kv heads),
+  two seeded records with one seeded ciphertext byte flipped;
+* int4 Llama-3-70B writeback: 256 blocks -> 512 packets of 81,936 B (pairs of
+  whole records per workgroup).
+
+Reload ciphertext comes from OpenSSL (the reference's host AES-128-GCM) over
+the oracle's packets; outputs must equal the input blocks (bf16) or the
+oracle decode of the packets, bit for bit, and every record's status must be
+1 except the tampered ones (0, slot zeroed on the device).  Writeback
+ciphertext and tags must equal OpenSSL's over the oracle's packets.
+"""
+import numpy as np
+import pytest
+import torch
+
+import secure_infer_amd as si
+from oracle import oracle as O
+from tests import wire as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+KEY = bytes.fromhex("000102030405060708090a0b0c0d0e0f")
+SALT = bytes.fromhex("5eed5a17")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def statuses(ww: np.ndarray, n: int, nrec: int) -> np.ndarray:
+    st, toff = W.stride(n), W.align32(n)
+    return ww.reshape(nrec, st)[:, toff + 16:toff + 20].copy().view(np.uint32).ravel()
+
+
+@pytest.mark.parametrize("bits,heads,nb", [(0, 8, 48), (8, 8, 64), (4, 4, 64)],
+                         ids=["bf16_llama3_8b", "int8_llama3_8b", "int4_qwen2_5_7b"])
+def test_full_size_reload_layer(bits, heads, nb):
+    rng = np.random.default_rng(1000 + bits)
+    dim, nslots, layer, t0 = 128, 512, 17, 123456
+    nrec = 2 * nb
+    kinds = [0] * nb + [1] * nb
+    blocks = W.bf16_blocks(rng, nrec, heads, dim)
+    if bits:
+        payloads = [O.codec_encode(blocks[r], bits, kinds[r], layer) for r in range(nrec)]
+    else:
+        payloads = [blocks[r].view(np.uint8).reshape(-1) for r in range(nrec)]
+    n = payloads[0].size
+    assert n == (128 * heads * dim * 2 if not bits else si.codec_width(bits, heads, dim))
+    wire = W.build_wire(KEY, SALT, payloads, kinds, layer, list(range(nb)) * 2, t0)
+    tampered = []
+    if bits == 4:  # 1 % of a layer's records, rounded up: two seeded records
+        tampered = sorted(int(r) for r in rng.choice(nrec, 2, replace=False))
+        for r in tampered:
+            wire[r * W.stride(n) + int(rng.integers(0, n))] ^= 0x5A
+    slot_ids = rng.permutation(nslots)[:nb].astype(np.int64)
+    slots = dev(np.concatenate([slot_ids, slot_ids]))
+    ck = torch.zeros((nslots, 128, heads, dim), dtype=torch.int16, device=DEV)
+    cv = torch.zeros_like(ck)
+    ck.view(torch.uint8).fill_(0x3C)
+    cv.view(torch.uint8).fill_(0x3C)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    staging = torch.empty(nrec * W.align32(n), dtype=torch.uint8, device=DEV) if bits else None
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    dw = dev(wire)
+    sess.reload_layer(dw, n, nrec, nb, ck, cv, slots, ticket_base=t0, codec_bits=bits, heads=heads,
+                      head_dim=dim, layer=layer, staging=staging, fail_count=fail)
+    torch.cuda.synchronize()
+    st = statuses(dw.cpu().numpy(), n, nrec)
+    want_st = np.ones(nrec, np.uint32)
+    want_st[tampered] = 0
+    assert np.array_equal(st, want_st)
+    assert int(fail.item()) == len(tampered)
+    if bits:
+        want = np.stack([O.codec_decode(payloads[r], heads, dim, bits, kinds[r]) for r in range(nrec)])
+    else:
+        want = blocks.copy()
+    want[tampered] = 0
+    want_dev = dev(want.view(np.int16))
+    idx = dev(slot_ids)
+    assert torch.equal(ck.index_select(0, idx), want_dev[:nb])
+    assert torch.equal(cv.index_select(0, idx), want_dev[nb:])
+    for r in tampered:  # what attention would read
+        c = ck if r < nb else cv
+        s = int(slot_ids[r % nb])
+        assert torch.equal(c[s], torch.zeros_like(c[s]))
+    untouched = torch.ones(nslots, dtype=torch.bool, device=DEV)
+    untouched[idx] = False
+    for c in (ck, cv):
+        assert bool((c[untouched].view(torch.uint8) == 0x3C).all())
+
+
+def test_full_size_writeback_layer_int4_llama3_70b():
+    rng = np.random.default_rng(1070)
+    heads, dim, nb, nslots, layer, bits, t0 = 8, 128, 256, 512, 61, 4, 777000
+    nrec = 2 * nb
+    kinds = [0] * nb + [1] * nb
+    slot_ids = rng.permutation(nslots)[:nb].astype(np.int64)
+    ck = torch.zeros((nslots, 128, heads, dim), dtype=torch.int16, device=DEV)
+    cv = torch.zeros_like(ck)
+    data = [W.bf16_blocks(rng, nb, heads, dim) for _ in range(2)]
+    idx = dev(slot_ids)
+    ck[idx] = dev(data[0].view(np.int16))
+    cv[idx] = dev(data[1].view(np.int16))
+    n = si.codec_width(bits, heads, dim)
+    wire = W.wire_aads(KEY, SALT, n, kinds, layer, list(range(nb)) * 2, t0)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    staging = torch.empty(nrec * W.align32(n), dtype=torch.uint8, device=DEV)
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    dw = dev(wire)
+    sess.writeback_layer(dw, n, nrec, nb, ck, cv, dev(np.concatenate([slot_ids, slot_ids])), ticket_base=t0,
+                         codec_bits=bits, heads=heads, head_dim=dim, layer=layer, staging=staging,
+                         fail_count=fail)
+    torch.cuda.synchronize()
+    assert int(fail.item()) == 0
+    ww = dw.cpu().numpy().reshape(nrec, W.stride(n))
+    toff = W.align32(n)
+    for r in range(nrec):
+        pkt = O.codec_encode(data[kinds[r]][r % nb], bits, kinds[r], layer)
+        aad = O.build_gcm_aad(2, kinds[r], layer, r % nb, 0, n, t0 + r)
+        c, tag = O.ossl_gcm_encrypt(KEY, O.iv12_from_words(W.record_iv(SALT, t0 + r)), aad, pkt)
+        assert np.array_equal(ww[r, :n], c), f"record {r} ciphertext"
+        assert ww[r, toff:toff + 16].tobytes() == tag, f"record {r} tag"

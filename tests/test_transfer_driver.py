@@ -1,0 +1,143 @@
+"""Host logic of the per-layer drivers, without a GPU: the library is replaced
+by a recorder, so these pin what NativeTransfer / D2HTransfer submit and in
+which order.
+
+* Causal groups: the reference's own test
+  (secure_infer/tests/test_grouped_loading.py) -- 41 blocks in groups of 16
+  are submitted tail first as [25, 41), [9, 25), [0, 9), each group inside its
+  own layer-group brackets sized 2 * len(group), K before V, every block
+  exactly once, the layer index unchanged within the layer
+  (native_layerwise.py:96-112).
+* Slice streams stripe each group's rows (native_layerwise.py:113-129).
+* The mixed codec policy (transport_codec.py:18-19).
+"""
+import math
+from unittest import mock
+
+import pytest
+import torch
+
+import secure_infer_amd as si
+from secure_infer_amd import gcm
+
+
+class FakeStream:
+    def __init__(self, name):
+        self.name = name
+        self.cuda_stream = id(self)
+        self.waits = []
+
+    def wait_stream(self, other):
+        self.waits.append(other.name)
+
+
+class Recorder:
+    """Stands in for libsecure_infer.so: records brackets and swaps."""
+
+    def __init__(self):
+        self.calls = []
+
+    def secure_infer_h2d_layer_group_begin(self, n):
+        self.calls.append(("begin", int(n)))
+        return 0
+
+    def secure_infer_h2d_layer_group_end(self):
+        self.calls.append(("end",))
+        return 0
+
+    def secure_infer_h2d_swap(self, stream, sess, host_base, host_block_bytes, host_nblocks, dev, slot_bytes,
+                              nslots, mapping_ptr, n, kind, layer, bits, heads, dim, fail):
+        import ctypes as ct
+        arr = (ct.c_int64 * (2 * n)).from_address(mapping_ptr.value)
+        pairs = [(arr[2 * i], arr[2 * i + 1]) for i in range(n)]
+        self.calls.append(("swap", stream.value, kind, layer, bits, pairs, host_nblocks, nslots))
+        return 0
+
+
+def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None):
+    rec = Recorder()
+    parent = FakeStream("parent")
+    shape = shape or si.LayerShape(2, 64)
+    sess = mock.Mock()
+    sess._h = None
+    nt = si.NativeTransfer(sess, shape, streams=streams or None, causal_group_blocks=group)
+    nt.layer = layer
+    host = [torch.zeros((nblocks, 4), dtype=torch.int16), torch.zeros((nblocks, 4), dtype=torch.int16)]
+    dest = [torch.zeros((nslots or nblocks + 100, 4), dtype=torch.int16) for _ in range(2)]
+    mapping = torch.stack((torch.arange(nblocks), torch.arange(nblocks) + 100), dim=1)
+    with mock.patch.object(gcm, "lib", return_value=rec), \
+         mock.patch.object(gcm, "_dev", lambda t, name: None), \
+         mock.patch.object(gcm.torch.cuda, "current_stream", return_value=parent):
+        nt.single_layer_kv_transfer((host, mapping), dest, None, False, 2, True, False)
+    return nt, rec, parent
+
+
+def test_partial_group_preserves_layer_and_mapping():
+    nt, rec, _ = run_transfer(41, 16, None)
+    begins = [c[1] for c in rec.calls if c[0] == "begin"]
+    assert begins == [32, 32, 18]
+    assert nt.layer == 8 and nt.causal_group_blocks == 16
+    swaps = [c for c in rec.calls if c[0] == "swap"]
+    assert all(c[3] == 7 for c in swaps)
+    for kind in range(2):
+        parts = [c[5] for c in swaps if c[2] == kind]
+        assert [len(p) for p in parts] == [16, 16, 9]
+        combined = [p for part in parts for p in part]
+        assert sorted(h for h, _ in combined) == list(range(41))
+        assert all(s == h + 100 for h, s in combined)
+    # tail first: the first group holds blocks 25..40
+    assert [h for h, _ in swaps[0][5]] == list(range(25, 41))
+    # per group: begin, K swap, V swap, end
+    kinds = [c[0] if c[0] != "swap" else ("K", "V")[c[2]] for c in rec.calls]
+    assert kinds == ["begin", "K", "V", "end"] * 3
+
+
+def test_record_order_is_layer_group_kind_block():
+    """Tickets are handed out in submission order, so the records of a
+    48-block layer with LOAD_CHUNK 2048 (16-block groups) take tickets in
+    (group from the tail, kind, block) order -- the order
+    reference_ticket_order() gives to device-resident wire records."""
+    _, rec, _ = run_transfer(48, 16, None, layer=0)
+    order = [(c[2], h) for c in rec.calls if c[0] == "swap" for h, _ in c[5]]
+    assert order == gcm.reference_ticket_order(48, 16)
+    assert order[:3] == [(0, 32), (0, 33), (0, 34)] and order[16] == (1, 32) and order[32] == (0, 16)
+
+
+def test_slice_streams_stripe_rows_and_join():
+    s1, s2 = FakeStream("s1"), FakeStream("s2")
+    _, rec, parent = run_transfer(10, 0, [s1, s2])
+    swaps = [c for c in rec.calls if c[0] == "swap"]
+    assert [(c[1], c[2], len(c[5])) for c in swaps] == [
+        (s1.cuda_stream, 0, 5), (s2.cuda_stream, 0, 5), (s1.cuda_stream, 1, 5), (s2.cuda_stream, 1, 5)]
+    assert s1.waits == ["parent"] and s2.waits == ["parent"]
+    assert parent.waits == ["s1", "s2"]
+
+
+def test_swap_carries_pool_sizes():
+    _, rec, _ = run_transfer(5, 0, None, nslots=64)
+    swaps = [c for c in rec.calls if c[0] == "swap"]
+    assert all(c[6] == 5 and c[7] == 64 for c in swaps)
+
+
+@pytest.mark.parametrize("layers", [1, 2, 3, 28, 32, 40, 80])
+def test_mixed_codec_policy(layers):
+    for layer in range(layers):
+        want = 8 if layer < math.ceil(layers / 3) else 4
+        assert si.layer_bits("mixed", layer, layers) == want
+        assert si.layer_bits("int8", layer, layers) == 8
+        assert si.layer_bits("int4", layer, layers) == 4
+        assert si.layer_bits("none", layer, layers) == 0
+    with pytest.raises(ValueError):
+        si.layer_bits("fp8", 0, layers)
+
+
+def test_mixed_shape_bits_reach_the_swap():
+    shape = si.LayerShape(2, 64, codec="mixed", layers=3)
+    assert [shape.bits_for(l) for l in range(3)] == [8, 4, 4]
+    with pytest.raises(ValueError):
+        shape.record_bytes
+    for layer, bits in ((0, 8), (1, 4), (2, 4)):
+        _, rec, _ = run_transfer(4, 0, None, layer=layer, shape=shape)
+        assert {c[4] for c in rec.calls if c[0] == "swap"} == {bits}
+    with pytest.raises(ValueError):
+        si.LayerShape(2, 64, codec="mixed")
