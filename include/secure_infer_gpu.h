@@ -148,6 +148,25 @@ typedef struct si_reload_desc {
 int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* session,
                                   const si_reload_desc* desc);
 
+/* secure_infer_gpu_reload_layer without any device allocation.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The kernels are the same; their scratch (GHASH
+ * accumulators, the parking area of two-record shares and, with a codec, the
+ * packet staging) lives in one 64 MiB device array per GPU
+ * (SI_NOALLOC_SCRATCH_BYTES below, held until the process ends) instead of
+ * per-stream workspaces and the caller's staging buffer: desc->staging must
+ * be NULL.  Limits: at most 8192 records, and 256 KiB of accumulators +
+ * pair parking (12 KiB per workgroup when the records outnumber the CUs) +
+ * nrec * align32(bytes) of staging (codec only) within the 64 MiB; a larger
+ * request returns -1 with a message on stderr.  The first call on a GPU
+ * clears the accumulators on `stream` and waits for it (unless the stream
+ * is capturing).  Every call on one GPU shares that GPU's array: calls whose
+ * work overlaps on one GPU (other streams, or other threads) race and must
+ * be serialised by the caller. */
+int secure_infer_gpu_reload_layer_noalloc(hipStream_t stream, si_session* session,
+                                          const si_reload_desc* desc);
+
 /* One layer of writeback: record r gathers cache[kind] + slots[r]*slot_bytes,
  * optionally quantises it with the transport codec, encrypts it and writes the
  * ciphertext and tag into its wire record (the AAD must already be there).

@@ -50,6 +50,7 @@ SIGNATURES = {
     "secure_infer_gpu_session_destroy": ([_v], _i),
     "secure_infer_gpu_session_hash_subkey": ([_v, _v], _i),
     "secure_infer_gpu_reload_layer": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),
+    "secure_infer_gpu_reload_layer_noalloc": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),
     "secure_infer_gpu_writeback_layer": ([_v, _v, ct.POINTER(SiWritebackDesc)], _i),
     "secure_infer_codec_width": ([_u32, _u32, _u32], _u64),
     "secure_infer_wire_stride": ([_u64], _u64),

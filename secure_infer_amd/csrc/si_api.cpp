@@ -623,20 +623,27 @@ static void fill_layer_ivs(const si_session* s, si::RecBatch& b, const uint32_t*
     b.nonce_base = s->session_nonce + ticket_base;
 }
 
-int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_reload_desc* d)
+// Checks of a reload descriptor shared by both reload entry points (the
+// codec staging buffer is checked by the caller: the allocation-free entry
+// point brings its own).
+static int reload_checks(const si_session* s, const si_reload_desc* d, const void* staging)
 {
     if (!d) return -1;
     if (layer_common(s, d->bytes, d->nrec, d->n_k, d->nslots, d->wire_stride, d->wire, d->slots, d->codec_bits,
-                     d->heads, d->head_dim, d->staging, d->slot_bytes))
+                     d->heads, d->head_dim, staging, d->slot_bytes))
         return -1;
     if (!d->cache_k && d->n_k) return -1;
     if (!d->cache_v && d->n_k < d->nrec) return -1;
     if (!d->iv_words && d->ticket_base == 0) return -1;
-    Workspace* ws = workspace_of(stream);
-    if (!ws) return -1;
-    std::lock_guard<std::mutex> g(ws->m);
-    si::RecAcc* acc = workspace(*ws, stream, d->nrec);
-    if (!acc) return -1;
+    return 0;
+}
+
+// The verify / decrypt launch and, with a codec, the dequantise-scatter
+// launch of one reload layer, given its accumulators, schedule (with its
+// parking area) and staging.
+static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc* d, si::RecAcc* acc,
+                         const si::Sched& sc, uint8_t* staging)
+{
     si::RecBatch b{};
     b.single = 0;
     b.encrypt = 0;
@@ -655,11 +662,9 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
     b.fail_count = d->fail_count;
     const bool codec = d->codec_bits != SI_CODEC_NONE;
     if (codec) {
-        b.staging = static_cast<uint8_t*>(d->staging);
+        b.staging = staging;
         b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
     }
-    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
-    if (sc.pairs && !(sc.park = park_area(*ws, stream, sc.nwg))) return -1;
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     if (si::launch_gcm(0, stream, s->ctx->dev, b, sc, acc, al) != hipSuccess) return -1;
     if (codec) {
@@ -675,7 +680,7 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
         cb.slot_bytes = d->slot_bytes;
         cb.slots = d->slots;
         cb.nslots = int64_t(d->nslots);
-        cb.staging = static_cast<uint8_t*>(d->staging);
+        cb.staging = staging;
         cb.staging_stride = b.staging_stride;
         cb.qbytes = 128ull * d->heads * d->head_dim * d->codec_bits / 8;
         cb.sbytes = 2ull * d->heads * d->head_dim * 4;
@@ -683,6 +688,52 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
         if (si::launch_dequant_scatter(stream, cb) != hipSuccess) return -1;
     }
     return 0;
+}
+
+int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_reload_desc* d)
+{
+    if (!d || reload_checks(s, d, d->staging)) return -1;
+    Workspace* ws = workspace_of(stream);
+    if (!ws) return -1;
+    std::lock_guard<std::mutex> g(ws->m);
+    si::RecAcc* acc = workspace(*ws, stream, d->nrec);
+    if (!acc) return -1;
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    if (sc.pairs && !(sc.park = park_area(*ws, stream, sc.nwg))) return -1;
+    return reload_launch(stream, s, d, acc, sc, static_cast<uint8_t*>(d->staging));
+}
+
+int secure_infer_gpu_reload_layer_noalloc(hipStream_t stream, si_session* s, const si_reload_desc* d)
+{
+    if (!d) return -1;
+    if (d->staging) {
+        fprintf(stderr, "[secure_infer] reload_layer_noalloc: staging must be NULL (the library's scratch "
+                        "holds it)\n");
+        return -1;
+    }
+    const bool codec = d->codec_bits != SI_CODEC_NONE;
+    // layer_common wants a staging pointer for a codec; the scratch's is
+    // only known once the request fits, so check with a stand-in first.
+    if (reload_checks(s, d, codec ? reinterpret_cast<const void*>(uintptr_t(256)) : nullptr)) return -1;
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    const uint64_t park_bytes = sc.pairs ? (uint64_t(sc.nwg) * SI_NT * sizeof(uint4) + 255) / 256 * 256 : 0;
+    const uint64_t stage_bytes = codec ? uint64_t(d->nrec) * ((d->bytes + 31) & ~uint64_t(31)) : 0;
+    if (d->nrec > SI_NOALLOC_MAX_RECORDS ||
+        SI_NOALLOC_ACC_BYTES + park_bytes + stage_bytes > SI_NOALLOC_SCRATCH_BYTES) {
+        fprintf(stderr,
+                "[secure_infer] reload_layer_noalloc: %u records of %llu B need %llu B of scratch "
+                "(at most %u records and %llu B); use secure_infer_gpu_reload_layer\n",
+                d->nrec, static_cast<unsigned long long>(d->bytes),
+                static_cast<unsigned long long>(SI_NOALLOC_ACC_BYTES + park_bytes + stage_bytes),
+                SI_NOALLOC_MAX_RECORDS, static_cast<unsigned long long>(SI_NOALLOC_SCRATCH_BYTES));
+        return -1;
+    }
+    uint8_t* base = si::noalloc_scratch(stream);
+    if (!base) return -1;
+    si::RecAcc* acc = reinterpret_cast<si::RecAcc*>(base);
+    if (sc.pairs) sc.park = reinterpret_cast<uint4*>(base + SI_NOALLOC_ACC_BYTES);
+    uint8_t* staging = codec ? base + SI_NOALLOC_ACC_BYTES + park_bytes : nullptr;
+    return reload_launch(stream, s, d, acc, sc, staging);
 }
 
 int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si_writeback_desc* d)

@@ -26,10 +26,21 @@
 // drained (s_waitcnt) before a workgroup takes its ticket; byte-granular
 // stores (partial or unaligned blocks) fall back to an agent-scope release
 // (L2 write-back) instead.
+#include <map>
+#include <mutex>
+
 #include "si_device.h"
 #include "si_kernels.h"
 
 namespace si {
+
+// The allocation-free reload's scratch: one array per GPU, held until the
+// process ends.  Host code never uses the array's name as an address (on the
+// host it is a stand-in, not a device address): noalloc_scratch() looks the
+// address up per device with hipGetSymbolAddress and every kernel argument
+// derives from that.
+static __device__ __align__(256) uint8_t scratch[SI_NOALLOC_SCRATCH_BYTES];
+static_assert(sizeof(RecAcc) == 32, "accumulator region holds 32 B per record");
 
 enum Mode : int {
     MODE_DECRYPT = 0,     // verify + decrypt, output zeroed on failure
@@ -916,6 +927,38 @@ __global__ void auth_gate_kernel(uint8_t* data, const uint32_t* status, uint64_t
     const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
     for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += stride)
         data[i] = 0;
+}
+
+__global__ void zero_words_kernel(uint4* p, uint64_t n)
+{
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
+uint8_t* noalloc_scratch(hipStream_t stream)
+{
+    static std::mutex m;
+    static std::map<int, uint8_t*> ptrs;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> g(m);
+    auto it = ptrs.find(dev);
+    if (it != ptrs.end()) return it->second;
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    // The record kernel's accumulators must start at zero; the workgroup
+    // that finalises a record returns its accumulator to zero, so this clear
+    // is needed once per device.  A fill kernel, not a memset node, in case
+    // the stream is being captured.
+    const uint64_t words = SI_NOALLOC_ACC_BYTES / 16u;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(uint32_t((words + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<uint4*>(ptr), words);
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return nullptr;
+    if (cs == hipStreamCaptureStatusNone && hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    ptrs[dev] = static_cast<uint8_t*>(ptr);
+    return ptrs[dev];
 }
 
 // ---------------------------------------------------------------- launches

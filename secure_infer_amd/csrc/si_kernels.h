@@ -62,6 +62,17 @@ struct Sched {
     uint4* park;         // pairs: each thread's segment-0 product during segment 1
                          // (one uint4 per thread of each workgroup)
 };
+// Scratch of the allocation-free reload (secure_infer_gpu_reload_layer_noalloc):
+// one device array per GPU, [accumulators of up to SI_NOALLOC_MAX_RECORDS
+// records][parking area of pairs][codec staging].
+#define SI_NOALLOC_SCRATCH_BYTES (64ull << 20)
+#define SI_NOALLOC_MAX_RECORDS 8192u
+#define SI_NOALLOC_ACC_BYTES (uint64_t(SI_NOALLOC_MAX_RECORDS) * 32u)
+// Device address of the current GPU's scratch; on a device's first call its
+// accumulator region is zeroed on `stream` (and, unless the stream is
+// capturing, waited for).  nullptr on failure.
+uint8_t* noalloc_scratch(hipStream_t stream);
+
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
                       const Sched& s, RecAcc* acc, bool aligned);
 hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, uint8_t* out,
