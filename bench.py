@@ -44,6 +44,9 @@ CONFIGS = {
                                                slots=512, bits=4, tamper=0.0),
 }
 DEFAULT = "reload_bf16_llama3_8b_6144tok"
+# RUNTIME_LOAD_CHUNK of the reference's reuse connectors (connector.py:21, 288):
+# a layer's reload is submitted in groups of 2048 / 128 = 16 blocks, tail first.
+LOAD_CHUNK_BLOCKS = 2048 // 128
 
 
 def aad_bytes(direction: int, kind: int, layer: int, block_id: int, nbytes: int, ticket: int) -> bytes:
@@ -55,6 +58,66 @@ def aad_bytes(direction: int, kind: int, layer: int, block_id: int, nbytes: int,
     out[28:36] = nbytes.to_bytes(8, "big")
     out[36:44] = ticket.to_bytes(8, "big")
     return bytes(out)
+
+
+def record_tickets(op: str, nblocks: int, ticket0: int) -> np.ndarray:
+    """Ticket of each record of a layer (records K blocks then V blocks).
+    Reload follows NativeTransfer's submission order (groups of
+    LOAD_CHUNK_BLOCKS from the tail, K then V, native_layerwise.py:96-129);
+    writeback follows the D2H branch's (all K blocks, then all V blocks,
+    npu_predict.py:895-906)."""
+    from secure_infer_amd.gcm import reference_ticket_order
+    if op == "writeback":
+        return ticket0 + np.arange(2 * nblocks, dtype=np.int64)
+    pos = {kb: i for i, kb in enumerate(reference_ticket_order(nblocks, LOAD_CHUNK_BLOCKS))}
+    return ticket0 + np.array([pos[divmod(r, nblocks)] for r in range(2 * nblocks)], np.int64)
+
+
+def iv_words_of(salt: bytes, nonce: int, tickets: np.ndarray) -> np.ndarray:
+    """salt || BE64(nonce + ticket) || BE32(2) as four big-endian words
+    (secure_infer_derive_transfer_iv, secure_infer.cpp:274-300)."""
+    t = (np.uint64(nonce) + tickets.astype(np.uint64))
+    w = np.zeros((tickets.size, 4), np.uint32)
+    w[:, 0] = int.from_bytes(salt[:4], "big")
+    w[:, 1] = (t >> np.uint64(32)).astype(np.uint32)
+    w[:, 2] = (t & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    w[:, 3] = 2
+    return w
+
+
+def cpu_check_sampled_layers(op, layers, blocks_host, cache, wire, slots, tampered, key, salt, tickets, H, D, NB,
+                         bits, nbytes, stride, tag_off, torch):
+    """Bit-exactness of the timed work on sampled layers against the oracle:
+    reload -> the cache holds decode(encode(original)) (bf16: the original),
+    zeros for tampered records; writeback -> every record's ciphertext and tag
+    equal OpenSSL's over the oracle's packet."""
+    from oracle import oracle as O
+    ok = True
+    for layer in layers:
+        orig = blocks_host[layer]  # [2, NB, 128, H, D] uint16
+        if op == "reload":
+            want = orig.copy()
+            if bits:
+                for k in range(2):
+                    for b in range(NB):
+                        want[k, b] = O.codec_decode(O.codec_encode(orig[k, b], bits, k, layer), H, D, bits, k)
+            for l2, r in tampered:
+                if l2 == layer:
+                    want[r // NB, r % NB] = 0
+            got = torch.stack([cache[layer, k][slots[layer]] for k in range(2)])
+            ok &= bool(torch.equal(got.view(torch.int16),
+                                   torch.from_numpy(want.view(np.int16)).to(got.device)))
+        else:
+            ww = wire[layer].cpu().numpy().reshape(2 * NB, stride)
+            for r in range(2 * NB):
+                k, b = divmod(r, NB)
+                t = int(tickets[layer][r])
+                pkt = O.codec_encode(orig[k, b], bits, k, layer) if bits else orig[k, b].view(np.uint8).reshape(-1)
+                aad = O.build_gcm_aad(2, k, layer, b, 0, nbytes, t)
+                iv12 = salt[:4] + t.to_bytes(8, "big")
+                c, tag = O.ossl_gcm_encrypt(key, iv12, aad, pkt)
+                ok &= bool(np.array_equal(ww[r, :nbytes], c) and ww[r, tag_off:tag_off + 16].tobytes() == tag)
+    return ok
 
 
 def algorithmic_bytes_per_record(op: str, record_bytes: int, block_bytes: int) -> int:
@@ -275,13 +338,16 @@ def main():
                                                     dtype=torch.float32).to(torch.bfloat16)
 
     # Wire records with host-built AADs.  Reload: the ciphertext is made by
-    # the GPU writeback path (bit-exact with OpenSSL, checked by the tests).
+    # the GPU writeback path (bit-exact with OpenSSL, checked by the tests)
+    # under the tickets a reload of this layer takes in the reference's order.
     wire = torch.zeros((L, nrec * stride), dtype=torch.uint8, device=dev)
     ticket0 = 1
+    tickets = [record_tickets(op, NB, ticket0 + layer * nrec) for layer in range(L)]
+    ivw = torch.from_numpy(np.stack([iv_words_of(salt, 0, t) for t in tickets])).to(dev)
     aads = np.zeros((L, nrec, 64), np.uint8)
     for layer in range(L):
         for r in range(nrec):
-            t = ticket0 + layer * nrec + r
+            t = int(tickets[layer][r])
             aads[layer, r] = np.frombuffer(aad_bytes(direction, 0 if r < n_k else 1, layer, r % NB, nbytes, t),
                                            np.uint8)
     wv = wire.view(L, nrec, stride)
@@ -291,13 +357,17 @@ def main():
 
     def writeback_layer(layer):
         sess.writeback_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1], slots2[layer],
-                             ticket_base=ticket0 + layer * nrec, codec_bits=bits, heads=H, head_dim=D,
+                             iv_words_dev=ivw[layer], codec_bits=bits, heads=H, head_dim=D,
                              layer=layer, staging=staging)
 
     def reload_layer(layer):
         sess.reload_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1], slots2[layer],
-                          ticket_base=ticket0 + layer * nrec, codec_bits=bits, heads=H, head_dim=D,
+                          iv_words_dev=ivw[layer], codec_bits=bits, heads=H, head_dim=D,
                           layer=layer, staging=staging, fail_count=fails[layer:layer + 1])
+
+    sample_layers = sorted({0, L // 2, L - 1})
+    blocks_host = {l: torch.stack([cache[l, k][slots[l]] for k in range(2)]).view(torch.int16).cpu().numpy()
+                   .view(np.uint16) for l in sample_layers}
 
     tampered = []
     if op == "reload":
@@ -341,9 +411,10 @@ def main():
     ms_per_step = total_ms / args.steps
     us_launch = total_ms * 1e3 / (args.steps * L)
 
-    # correctness of what was timed
+    # correctness of what was timed: every layer on the device (bf16 reload),
+    # sampled layers against the oracle (every workload)
     nfail = int(fails.sum().item()) if op == "reload" else 0
-    exact = None
+    exact = True
     if op == "reload" and bits == 0:
         got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
         if tampered:
@@ -351,6 +422,7 @@ def main():
                 k, b = divmod(r, NB)
                 truth[layer, k, b] = 0
         exact = bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
+
     tamper_ok = None
     if op == "reload" and tampered:
         zeroed = all(bool((cache[l, r // NB, slots[l, r % NB]] == 0).all()) for l, r in tampered)
@@ -380,6 +452,12 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "failed_records_per_step": nfail // max(args.steps, 1),
         "bit_exact": exact,
+        "bit_exact_checked": ("every layer on the device + " if (op == "reload" and bits == 0) else "") +
+                             f"layers {sample_layers} against the oracle in the CPU leg" +
+                             (" (decode(encode(original)))" if bits and op == "reload" else "") +
+                             (" (OpenSSL over the oracle's packets)" if op == "writeback" else ""),
+        "ticket_order": ("reload groups of %d blocks from the tail, K then V (reference NativeTransfer)"
+                         % LOAD_CHUNK_BLOCKS) if op == "reload" else "K blocks then V blocks (reference D2H)",
         "tamper_fail_closed": tamper_ok,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -387,8 +465,13 @@ def main():
         "issue": load_issue(args.config),
     }
     if not args.no_cpu:
+        # The CPU leg: the oracle checks the timed work on sampled layers, then
+        # OpenSSL on the host cores is timed on one layer.
+        res["bit_exact"] = exact and cpu_check_sampled_layers(
+            op, sample_layers, blocks_host, cache, wire, slots, tampered, key, salt, tickets, H, D, NB, bits, nbytes,
+            stride, tag_off, torch)
         layer = 0
-        ivs = np.array([sess.record_iv(ticket0 + r) for r in range(nrec)], np.uint32)
+        ivs = ivw[layer].cpu().numpy()
         planes = [cache[layer, k][slots[layer]].view(torch.uint8).reshape(NB, -1).cpu().numpy()
                   for k in range(2)]
         gw = wire[layer].cpu().numpy()

@@ -223,11 +223,21 @@ int secure_infer_build_gcm_aad(const void* host_ptr, size_t bytes, uint8_t direc
  * :6439-6445, D2H :8096-8115) and refuses a swap whose tickets were used. */
 int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket);
 
-/* secure_infer.cpp:1102-1148: retire / invalidate the speculative ticket and
- * keystream pools.  This library keeps no speculative state, so both are
- * no-ops; EncodedStore binds the first unconditionally (transport_codec.py:50). */
+/* secure_infer.cpp:1102-1148: drop every record sealed ahead of demand
+ * (secure_infer_h2d_prefetch) that no swap has consumed; their tickets stay
+ * used.  Call it when host blocks change after a prefetch.  EncodedStore
+ * binds the first unconditionally (transport_codec.py:50); both do the same
+ * here (this library has no address predictor to reset). */
 void secure_infer_retire_transfer_prefetches(void);
 void secure_infer_invalidate_transfer_prefetches(void);
+/* secure_infer.cpp:817-830: swaps served from prefetched records that were
+ * ready / that had to wait for their sealing to finish / swaps sealed on
+ * demand (the reference's ready / busy_fallback / missing_fallback; a busy
+ * prefetch is waited for here, not abandoned). */
+void secure_infer_get_transfer_prefetch_stats(uint64_t* ready, uint64_t* busy_fallback,
+                                              uint64_t* missing_fallback);
+/* secure_infer.cpp:5052-5070: records sealed ahead of demand and not yet consumed. */
+uint64_t secure_infer_count_ready_unconsumed_gcm_tickets(void);
 
 /* secure_infer.cpp:5883-5903: layer-group brackets (thread-local). */
 int secure_infer_h2d_layer_group_begin(size_t expected);
@@ -243,6 +253,12 @@ int secure_infer_h2d_layer_group_end(void);
  * records registered with secure_infer_recovery_track_layer have no host
  * copy: any failure among them is -1. */
 int secure_infer_recovery_wait_layer_authentication(uint32_t layer);
+/* secure_infer.cpp:5311-5314, 7336-7372: records observed after set_job_id
+ * belong to that job; wait_job_authentication waits for every record of the
+ * job on every layer (no retry) and returns 1 if all authenticated, 0 if any
+ * failed and -1 if the job has no observed records. */
+void secure_infer_recovery_set_job_id(uint64_t job_id);
+int secure_infer_recovery_wait_job_authentication(uint64_t job_id);
 /* Registers a reload of `layer` whose per-record statuses land in the device
  * u32 `fail_count` once `event` completes (library-internal bookkeeping used
  * by the Python layer driver). */
@@ -292,6 +308,28 @@ int secure_infer_h2d_swap(hipStream_t stream, si_session* session, const void* h
  * authentication.  0 shots disarms.  Production code never calls them. */
 int secure_infer_test_tamper_h2d(int32_t layer, int32_t kind, int64_t host_block, uint32_t shots);
 int secure_infer_test_tamper_d2h(uint32_t shots);
+
+/* Ahead-of-demand sealing (the reference's CPU ciphertext prefetch pool,
+ * secure_infer.cpp:3264-3710): queues the host seal of the swap with these
+ * arguments on the worker pool and returns; tickets are reserved now, in
+ * mapping order.  The next secure_infer_h2d_swap with the same session,
+ * host pool, kind, layer, codec and host-block column of its mapping copies
+ * the sealed records instead of sealing (waiting for them if still being
+ * sealed).  The records snapshot the host blocks when sealed: call
+ * secure_infer_retire_transfer_prefetches if the blocks change before the
+ * swap.  Pinned memory for prefetches is bounded by SECURE_INFER_PREFETCH_MB
+ * (default 2048); beyond it the call returns -1 and the swap seals on demand. */
+int secure_infer_h2d_prefetch(si_session* session, const void* host_base, uint64_t host_block_bytes,
+                              uint64_t host_nblocks, const int64_t* mapping, uint32_t n, uint32_t kind,
+                              uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim);
+
+/* secure_infer.cpp:6085-6137: the per-swap H2D ledger.  With
+ * SECURE_INFER_H2D_PROFILE=<path> every swap appends one CSV row (layer,
+ * kind, records, record_bytes, source, seal_us, h2d_copy_us, kernel_us) once
+ * its work is complete; flush writes the rows of completed swaps, drain
+ * waits for every pending swap first. */
+void secure_infer_flush_completed_h2d_profile(void);
+void secure_infer_drain_h2d_profile_after_job(void);
 
 /* Threads of the host crypto pool (the calling thread included): the CPUs of
  * the process affinity mask, or SECURE_INFER_HOST_THREADS.  No reference

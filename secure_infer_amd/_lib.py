@@ -71,6 +71,13 @@ SIGNATURES = {
     "secure_infer_test_tamper_d2h": ([_u32], _i),
     "secure_infer_retire_transfer_prefetches": ([], None),
     "secure_infer_invalidate_transfer_prefetches": ([], None),
+    "secure_infer_get_transfer_prefetch_stats": ([ct.POINTER(_u64)] * 3, None),
+    "secure_infer_count_ready_unconsumed_gcm_tickets": ([], _u64),
+    "secure_infer_h2d_prefetch": ([_v, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32, _u32, _u32], _i),
+    "secure_infer_flush_completed_h2d_profile": ([], None),
+    "secure_infer_drain_h2d_profile_after_job": ([], None),
+    "secure_infer_recovery_set_job_id": ([_u64], None),
+    "secure_infer_recovery_wait_job_authentication": ([_u64], _i),
     "secure_infer_d2h_batch_begin": ([_sz], _i),
     "secure_infer_d2h_group_begin": ([_sz], _i),
     "secure_infer_d2h_group_end": ([], _i),

@@ -522,10 +522,15 @@ bool replay_insert(uint64_t a, uint64_t b)
 
 thread_local int64_t t_group_expected = -1;
 
+// secure_infer_recovery_set_job_id (secure_infer.cpp:5311-5314): the job that
+// records observed from now on belong to.
+std::atomic<uint64_t> g_job_id{0};
+
 struct TrackedLayer {
     hipEvent_t event;
     const uint32_t* fail_count;
     bool owned;  // event created by the library: destroyed once observed
+    uint64_t job_id;
 };
 std::mutex g_track_lock;
 std::multimap<uint32_t, TrackedLayer> g_tracked;
@@ -984,14 +989,6 @@ int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket)
     return 0;
 }
 
-// The reference retires or invalidates its speculative keystream / ticket
-// pools here (secure_infer.cpp:1102-1148).  This library keeps no speculative
-// state (tickets are reserved when a swap is issued), so both are no-ops; they
-// are exported because EncodedStore binds the first unconditionally
-// (transport_codec.py:50).
-void secure_infer_retire_transfer_prefetches(void) {}
-void secure_infer_invalidate_transfer_prefetches(void) {}
-
 int secure_infer_h2d_layer_group_begin(size_t expected)
 {
     if (t_group_expected >= 0) return -1;
@@ -1010,7 +1007,7 @@ int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event, const ui
 {
     if (!event || !fail_count) return -1;
     std::lock_guard<std::mutex> g(g_track_lock);
-    g_tracked.emplace(layer, TrackedLayer{event, fail_count, false});
+    g_tracked.emplace(layer, TrackedLayer{event, fail_count, false, g_job_id.load()});
     return 0;
 }
 
@@ -1039,6 +1036,39 @@ int secure_infer_recovery_wait_layer_authentication(uint32_t layer)
         if (t.owned) (void)hipEventDestroy(t.event);
     }
     return (rc != 0 || rc_host != 0) ? -1 : 0;
+}
+
+void secure_infer_recovery_set_job_id(uint64_t job_id) { g_job_id.store(job_id); }
+
+int secure_infer_recovery_wait_job_authentication(uint64_t job_id)
+{
+    // Every record of the job, on every layer, without retries
+    // (secure_infer.cpp:7336-7372): 1 if all authenticated, 0 if any failed,
+    // -1 if the job has no observed records.
+    std::vector<TrackedLayer> recs;
+    {
+        std::lock_guard<std::mutex> g(g_track_lock);
+        for (auto it = g_tracked.begin(); it != g_tracked.end();) {
+            if (it->second.job_id == job_id) {
+                recs.push_back(it->second);
+                it = g_tracked.erase(it);
+            } else {
+                ++it;
+            }
+        }
+    }
+    bool valid = true;
+    for (const TrackedLayer& t : recs) {
+        uint32_t fails = 1;
+        if (hipEventSynchronize(t.event) != hipSuccess ||
+            hipMemcpy(&fails, t.fail_count, 4, hipMemcpyDeviceToHost) != hipSuccess || fails != 0)
+            valid = false;
+        if (t.owned) (void)hipEventDestroy(t.event);
+    }
+    bool found = !recs.empty();
+    const int host = si_internal::wait_observed_job(job_id, &found);
+    if (!found) return -1;
+    return (valid && host == 1) ? 1 : 0;
 }
 
 int secure_infer_gpu_set_chunk_rows(int jmax)
@@ -1082,5 +1112,7 @@ uint64_t reserve_tickets(uint32_t n)
 bool replay_reserve_range(uint64_t t0, uint64_t n) { return replay_insert(t0, t0 + n); }
 
 bool group_open() { return t_group_expected >= 0; }
+
+uint64_t current_job_id() { return g_job_id.load(); }
 
 }  // namespace si_internal

@@ -655,11 +655,26 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     // Unit index: uniform over a wave (SI_T is a multiple of 64).
     const uint32_t u = __builtin_amdgcn_readfirstlane(tid / SI_T), t = tid % SI_T;
 
+    // The AES and GHASH tables depend on the key context only: their loads
+    // go out first, in the shadow of the kernel-argument round trip that
+    // gives this workgroup's share.  Every global load of the fill is issued
+    // before its first LDS write, so it costs about one L2 round trip.
+    if (tid < SI_T) {
+        aes_fill_lds(aes, ctx->te0, tid);
+    } else {
+        const uint32_t i = tid - SI_T;  // 0..511: one entry of each table
+        const uint4 a0 = ctx->gh4u[i], a1 = ctx->gh4u2[i], a2 = ctx->gh4[i], a3 = ctx->gh4b[i];
+        s_lds[i] = a0;
+        s_lds[512 + i] = a1;
+        s_lds[5120 + i] = a2;
+        s_lds[5632 + i] = a3;
+    }
+
     // This workgroup's share of the records' concatenated rows.
     const uint64_t G = uint64_t(sch.nrec) * sch.rows;
     const uint64_t g0 = sch.use_starts ? sch.starts[blockIdx.x] : uint64_t(blockIdx.x) * G / sch.nwg;
     const uint64_t g1 = sch.use_starts ? sch.starts[blockIdx.x + 1] : (uint64_t(blockIdx.x) + 1) * G / sch.nwg;
-    if (g1 == g0) return;  // an empty share
+    if (g1 == g0) return;  // an empty share (the whole workgroup: no barrier is pending)
     const uint32_t r0 = uint32_t(g0 / sch.rows);
     const uint32_t qa0 = uint32_t(g0 - uint64_t(r0) * sch.rows);
     const uint32_t qb0 = g1 - uint64_t(r0) * sch.rows < sch.rows ? uint32_t(g1 - uint64_t(r0) * sch.rows) : sch.rows;
@@ -676,18 +691,6 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     uint4 zp0 = make_uint4(0, 0, 0, 0), zp1 = make_uint4(0, 0, 0, 0);
     zp0 = placement_power(ctx, sch, qb0, t);
     if (nseg == 2 && !pair && u == 0) zp1 = placement_power(ctx, sch, qb1, t);
-    if (tid < SI_T) {
-        aes_fill_lds(aes, ctx->te0, tid);
-    } else {
-        // Every global load of the set-up is issued before the first LDS
-        // write, so the fill costs about one L2 round trip.
-        const uint32_t i = tid - SI_T;  // 0..511: one entry of each table
-        const uint4 a0 = ctx->gh4u[i], a1 = ctx->gh4u2[i], a2 = ctx->gh4[i], a3 = ctx->gh4b[i];
-        s_lds[i] = a0;
-        s_lds[512 + i] = a1;
-        s_lds[5120 + i] = a2;
-        s_lds[5632 + i] = a3;
-    }
     if (tid < nseg) put_view(s_view + 5 * tid, view_of(batch, r0 + tid));
     if (tid == 0) *s_zero = make_uint4(0, 0, 0, 0);
     // One segment or a pair: its placement table now (thread (u, t) writes

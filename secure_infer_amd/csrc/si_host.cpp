@@ -24,6 +24,13 @@
 //    second copy stream; the group's end hands them to the worker pool, which
 //    authenticates and decrypts each record into its host destination (a
 //    record that fails is zeroed).  batch_end waits for that verification.
+//  * Ahead-of-demand sealing (the reference's CPU ciphertext prefetch,
+//    secure_infer.cpp:3264-3710): secure_infer_h2d_prefetch seals a swap's
+//    records on the worker pool before the swap is issued, under tickets
+//    reserved then; the matching secure_infer_h2d_swap only copies them.
+//  * An optional per-swap ledger (SECURE_INFER_H2D_PROFILE=<csv path>) of
+//    host seal time, H2D copy time and kernel time, like the reference's
+//    per-copy profile rows (secure_infer.cpp:1826-1951, 6085-6137).
 //  * Every block id is range-checked on the host before any work: a swap
 //    with a host block or device slot outside its pool is refused (-1).
 #include "si_host.h"
@@ -33,6 +40,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
@@ -225,6 +233,16 @@ bool tamper_h2d(uint32_t layer, uint32_t kind, int64_t host_block)
 
 // ---------------------------------------------------------------- device buffers
 
+struct Prefetch;
+
+// One ledger row of an H2D swap, written once its slot's work is complete.
+struct ProfileRow {
+    bool pending = false;
+    uint32_t layer = 0, kind = 0, n = 0, source = 0;  // source: 0 sealed on demand, 1 prefetched, 2 waited
+    uint64_t bytes = 0;
+    double seal_us = 0;
+};
+
 // A pinned host buffer mirrored by a device buffer of the same size, plus
 // device scratch for codec packets, reused across calls.
 struct Mirror {
@@ -236,6 +254,10 @@ struct Mirror {
     hipEvent_t ev_a = nullptr;  // H2D: wire records landed; D2H: records sealed
     hipEvent_t ev_b = nullptr;  // H2D: slot free again; D2H: records in host memory
     hipEvent_t ev_c = nullptr;  // H2D: the slot's kernel is done
+    // ledger (timing events, created when the ledger is on)
+    hipEvent_t p_c0 = nullptr, p_c1 = nullptr, p_k0 = nullptr, p_k1 = nullptr;
+    ProfileRow row;
+    std::shared_ptr<Prefetch> held;  // prefetched records being copied from
 
     Mirror() = default;
     Mirror(const Mirror&) = delete;
@@ -249,6 +271,15 @@ struct Mirror {
         if (ev_a) (void)hipEventDestroy(ev_a);
         if (ev_b) (void)hipEventDestroy(ev_b);
         if (ev_c) (void)hipEventDestroy(ev_c);
+        for (hipEvent_t e : {p_c0, p_c1, p_k0, p_k1})
+            if (e) (void)hipEventDestroy(e);
+    }
+
+    bool init_profile()
+    {
+        if (p_c0) return true;
+        return hipEventCreate(&p_c0) == hipSuccess && hipEventCreate(&p_c1) == hipSuccess &&
+               hipEventCreate(&p_k0) == hipSuccess && hipEventCreate(&p_k1) == hipSuccess;
     }
 
     bool init()
@@ -316,14 +347,15 @@ struct DeviceState {
     std::vector<std::unique_ptr<StatusBuf>> free_status;
 };
 
+std::mutex g_states_lock;
+std::map<int, std::unique_ptr<DeviceState>> g_states;
+
 DeviceState* device_state()
 {
-    static std::mutex m;
-    static std::map<int, std::unique_ptr<DeviceState>> states;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> g(m);
-    auto& st = states[dev];
+    std::lock_guard<std::mutex> g(g_states_lock);
+    auto& st = g_states[dev];
     if (!st) {
         auto s = std::make_unique<DeviceState>();
         s->device = dev;
@@ -408,6 +440,175 @@ bool valid_mapping(const int64_t* mapping, uint32_t n, bool host_first, uint64_t
     return true;
 }
 
+// ---------------------------------------------------------------- H2D ledger
+
+std::mutex g_profile_lock;
+FILE* g_profile = nullptr;
+bool g_profile_checked = false;
+
+bool profile_on()
+{
+    std::lock_guard<std::mutex> g(g_profile_lock);
+    if (!g_profile_checked) {
+        g_profile_checked = true;
+        const char* path = std::getenv("SECURE_INFER_H2D_PROFILE");
+        if (path && *path) {
+            g_profile = std::fopen(path, "a");
+            if (g_profile)
+                std::fprintf(g_profile, "layer,kind,records,record_bytes,source,seal_us,h2d_copy_us,kernel_us\n");
+        }
+    }
+    return g_profile != nullptr;
+}
+
+// Writes the slot's pending row; its events must be complete.
+void profile_retire(Mirror& sl)
+{
+    if (!sl.row.pending) return;
+    sl.row.pending = false;
+    float copy_ms = -1.0f, kernel_ms = -1.0f;
+    (void)hipEventElapsedTime(&copy_ms, sl.p_c0, sl.p_c1);
+    (void)hipEventElapsedTime(&kernel_ms, sl.p_k0, sl.p_k1);
+    static const char* kSource[] = {"sealed", "prefetched", "prefetch_waited"};
+    std::lock_guard<std::mutex> g(g_profile_lock);
+    if (g_profile)
+        std::fprintf(g_profile, "%u,%u,%u,%llu,%s,%.1f,%.1f,%.1f\n", sl.row.layer, sl.row.kind, sl.row.n,
+                     static_cast<unsigned long long>(sl.row.bytes), kSource[sl.row.source % 3], sl.row.seal_us,
+                     double(copy_ms) * 1e3, double(kernel_ms) * 1e3);
+}
+
+// Retires the ledger rows of every ring slot whose work is done (wait:
+// synchronise with the pending ones first), then flushes the file.
+void profile_sweep(bool wait)
+{
+    std::vector<DeviceState*> states;
+    {
+        std::lock_guard<std::mutex> g(g_states_lock);
+        for (auto& kv : g_states) states.push_back(kv.second.get());
+    }
+    for (DeviceState* ds : states) {
+        std::vector<StreamRing*> rings;
+        {
+            std::lock_guard<std::mutex> g(ds->rings_lock);
+            for (auto& kv : ds->rings) rings.push_back(kv.second.get());
+        }
+        for (StreamRing* ring : rings) {
+            std::lock_guard<std::mutex> g(ring->lock);
+            for (auto& sl : ring->slots) {
+                if (!sl->row.pending) continue;
+                const hipError_t st = wait ? hipEventSynchronize(sl->ev_b) : hipEventQuery(sl->ev_b);
+                if (st == hipSuccess) profile_retire(*sl);
+            }
+        }
+    }
+    std::lock_guard<std::mutex> g(g_profile_lock);
+    if (g_profile) std::fflush(g_profile);
+}
+
+// ---------------------------------------------------------------- ahead-of-demand sealing
+
+// A swap's records sealed before the swap is issued: [n wire records][n slot
+// ids], laid out exactly as a ring slot, in pinned memory.  It serves the
+// secure_infer_h2d_swap with the same session, host pool, kind, layer,
+// codec and host-block column of the mapping.
+struct Prefetch {
+    si_session* session = nullptr;
+    si_internal::SessionKeys keys{};
+    const uint8_t* host_base = nullptr;
+    uint64_t host_block_bytes = 0;
+    uint32_t kind = 0, layer = 0, codec = 0, heads = 0, dim = 0, n = 0;
+    std::vector<int64_t> host_blocks;
+    uint64_t bytes = 0, stride = 0, tag_off = 0, t0 = 0;
+    uint8_t* host = nullptr;
+    size_t cap = 0;
+    std::mutex m;
+    std::condition_variable cv;
+    uint32_t tasks = 0, done = 0;
+    bool failed = false;
+    double seal_us = 0;
+    ~Prefetch();
+};
+
+std::mutex g_pf_lock;
+std::vector<std::shared_ptr<Prefetch>> g_prefetch;            // sealed or sealing, not consumed
+std::vector<std::pair<uint8_t*, size_t>> g_pf_free;          // pinned buffers to reuse
+size_t g_pf_bytes = 0;                                        // pinned bytes held by prefetches
+std::atomic<uint64_t> g_pf_ready{0}, g_pf_waited{0}, g_pf_missing{0};
+
+size_t prefetch_budget()
+{
+    static const size_t b = [] {
+        size_t mb = 2048;
+        if (const char* e = std::getenv("SECURE_INFER_PREFETCH_MB")) mb = size_t(std::max(0, std::atoi(e)));
+        return mb << 20;
+    }();
+    return b;
+}
+
+Prefetch::~Prefetch()
+{
+    if (!host) return;
+    std::lock_guard<std::mutex> g(g_pf_lock);
+    g_pf_free.emplace_back(host, cap);
+}
+
+uint8_t* take_pf_buffer(size_t need, size_t& cap)
+{
+    {
+        std::lock_guard<std::mutex> g(g_pf_lock);
+        size_t best = g_pf_free.size();
+        for (size_t i = 0; i < g_pf_free.size(); ++i)
+            if (g_pf_free[i].second >= need && (best == g_pf_free.size() || g_pf_free[i].second < g_pf_free[best].second))
+                best = i;
+        if (best < g_pf_free.size()) {
+            uint8_t* p = g_pf_free[best].first;
+            cap = g_pf_free[best].second;
+            g_pf_free.erase(g_pf_free.begin() + long(best));
+            return p;
+        }
+        if (g_pf_bytes + need > prefetch_budget()) return nullptr;
+        g_pf_bytes += need;
+    }
+    uint8_t* p = nullptr;
+    if (hipHostMalloc(reinterpret_cast<void**>(&p), need, hipHostMallocDefault) != hipSuccess) {
+        std::lock_guard<std::mutex> g(g_pf_lock);
+        g_pf_bytes -= need;
+        return nullptr;
+    }
+    cap = need;
+    return p;
+}
+
+void wait_sealed(Prefetch& pf)
+{
+    std::unique_lock<std::mutex> g(pf.m);
+    pf.cv.wait(g, [&] { return pf.done == pf.tasks; });
+}
+
+// The unconsumed prefetch that serves this swap, removed from the registry.
+std::shared_ptr<Prefetch> take_prefetch(si_session* s, const void* host_base, uint64_t host_block_bytes,
+                                        const int64_t* mapping, uint32_t n, uint32_t kind, uint32_t layer,
+                                        uint32_t codec)
+{
+    std::lock_guard<std::mutex> g(g_pf_lock);
+    for (size_t i = 0; i < g_prefetch.size(); ++i) {
+        Prefetch& pf = *g_prefetch[i];
+        if (pf.session != s || pf.host_base != host_base || pf.host_block_bytes != host_block_bytes ||
+            pf.n != n || pf.kind != kind || pf.layer != layer || pf.codec != codec)
+            continue;
+        bool same = true;
+        for (uint32_t r = 0; r < n && same; ++r) same = pf.host_blocks[r] == mapping[2 * r];
+        if (!same) continue;
+        auto out = g_prefetch[i];
+        g_prefetch.erase(g_prefetch.begin() + long(i));
+        return out;
+    }
+    return nullptr;
+}
+
+void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint64_t bytes, uint64_t tag_off,
+                 uint64_t ticket, uint8_t* rec, uint32_t layer, uint32_t kind, int64_t hb, bool& ok);
+
 // ---------------------------------------------------------------- observed reloads
 
 // One observed swap: where each record came from and went to (for a strict
@@ -421,6 +622,7 @@ struct Observed {
     uint64_t slot_bytes = 0, nslots = 0;
     uint32_t kind = 0, layer = 0, codec = 0, heads = 0, dim = 0;
     hipStream_t stream = nullptr;
+    uint64_t job_id = 0;
     std::vector<int64_t> mapping;  // n (host block, device slot) pairs
     std::unique_ptr<StatusBuf> status;
 };
@@ -429,6 +631,27 @@ std::mutex g_obs_lock;
 std::multimap<uint32_t, std::shared_ptr<Observed>> g_observed;
 
 // ---------------------------------------------------------------- H2D
+
+void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint64_t bytes, uint64_t tag_off,
+                 uint64_t ticket, uint8_t* rec, uint32_t layer, uint32_t kind, int64_t hb, bool& ok)
+{
+    uint8_t* aad = rec + tag_off + 32;
+    uint8_t iv[12];
+    record_iv(keys, ticket, iv);
+    if (secure_infer_build_gcm_aad(src, bytes, 1, ticket, 0, keys.nonce, aad) != 1 ||
+        !gcm_seal(keys.key, iv, aad, 64, src, bytes, rec, rec + tag_off)) {
+        ok = false;
+        return;
+    }
+    memset(rec + bytes, 0, tag_off - bytes);
+    memset(rec + tag_off + 16, 0, 16);  // status slot
+    if (tamper_h2d(layer, kind, hb)) rec[0] ^= 0x01;
+}
+
+double us_since(std::chrono::steady_clock::time_point t0)
+{
+    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+}
 
 int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint64_t host_block_bytes,
                   uint64_t host_nblocks, void* dev_cache, uint64_t slot_bytes, uint64_t nslots,
@@ -450,46 +673,73 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     const uint64_t tag_off = tag_offset(bytes);
     const size_t wire = size_t(n) * stride;
     const size_t need = wire + size_t(n) * 8;
+    const bool prof = profile_on();
 
     std::unique_ptr<StatusBuf> status;
     if (observe && !(status = take_status(ds, n))) return -1;
+
+    // Records sealed ahead of demand for exactly this swap, if any.
+    std::shared_ptr<Prefetch> pf = take_prefetch(s, host_base, host_block_bytes, mapping, n, kind, layer, codec_bits);
+    uint32_t source = 0;
+    if (pf) {
+        std::unique_lock<std::mutex> g(pf->m);
+        source = pf->done == pf->tasks ? 1u : 2u;
+        pf->cv.wait(g, [&] { return pf->done == pf->tasks; });
+        if (pf->failed) return -1;
+        (source == 1 ? g_pf_ready : g_pf_waited).fetch_add(1);
+    } else {
+        g_pf_missing.fetch_add(1);
+    }
 
     std::lock_guard<std::mutex> g(ring->lock);
     const size_t si = ring->next;
     ring->next = (ring->next + 1) % ring->slots.size();
     Mirror& sl = *ring->slots[si];
-    if (ring->used[si] && hipEventSynchronize(sl.ev_b) != hipSuccess) return -1;
-    if (!sl.reserve(need, codec_bits ? size_t(n) * tag_off : 0)) return -1;
-
-    const uint64_t t0 = si_internal::reserve_tickets(n);
-    if (!si_internal::replay_reserve_range(t0, n)) {
-        fprintf(stderr, "[secure_infer] duplicate H2D transfer tickets rejected at %llu\n",
-                static_cast<unsigned long long>(t0));
-        return -1;
+    if (ring->used[si]) {
+        if (hipEventSynchronize(sl.ev_b) != hipSuccess) return -1;
+        profile_retire(sl);
+        sl.held.reset();  // the copy from a prefetch buffer is complete
     }
-    int64_t* slot_ids = reinterpret_cast<int64_t*>(sl.host + wire);
-    std::atomic<int> bad{0};
-    Pool::get().parallel_for(n, [&](size_t r) {
-        const int64_t hb = mapping[2 * r];
-        slot_ids[r] = mapping[2 * r + 1];
-        uint8_t* rec = sl.host + r * stride;
-        const uint8_t* src = static_cast<const uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes;
-        uint8_t* aad = rec + tag_off + 32;
-        uint8_t iv[12];
-        record_iv(keys, t0 + r, iv);
-        if (secure_infer_build_gcm_aad(src, bytes, 1, t0 + r, 0, keys.nonce, aad) != 1 ||
-            !gcm_seal(keys.key, iv, aad, 64, src, bytes, rec, rec + tag_off)) {
-            bad.store(1);
-            return;
+    if (!sl.reserve(need, codec_bits ? size_t(n) * tag_off : 0)) return -1;
+    if (prof && !sl.init_profile()) return -1;
+
+    // Host side: seal on demand into the ring slot, or take the prefetched
+    // records (their slot-id tail is written now).
+    uint8_t* src_host = sl.host;
+    uint64_t t0 = 0;
+    double seal_us = 0;
+    if (pf) {
+        t0 = pf->t0;
+        src_host = pf->host;
+        seal_us = pf->seal_us;
+    } else {
+        const auto ts = std::chrono::steady_clock::now();
+        t0 = si_internal::reserve_tickets(n);
+        if (!si_internal::replay_reserve_range(t0, n)) {
+            fprintf(stderr, "[secure_infer] duplicate H2D transfer tickets rejected at %llu\n",
+                    static_cast<unsigned long long>(t0));
+            return -1;
         }
-        memset(rec + bytes, 0, tag_off - bytes);
-        memset(rec + tag_off + 16, 0, 16);  // status slot
-        if (tamper_h2d(layer, kind, hb)) rec[0] ^= 0x01;
-    });
-    if (bad.load()) return -1;
-    if (hipMemcpyAsync(sl.dev, sl.host, need, hipMemcpyHostToDevice, ring->copy) != hipSuccess ||
+        std::atomic<int> bad{0};
+        Pool::get().parallel_for(n, [&](size_t r) {
+            const int64_t hb = mapping[2 * r];
+            bool ok = true;
+            seal_record(keys, static_cast<const uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes, bytes,
+                        tag_off, t0 + r, sl.host + r * stride, layer, kind, hb, ok);
+            if (!ok) bad.store(1);
+        });
+        if (bad.load()) return -1;
+        seal_us = us_since(ts);
+    }
+    int64_t* slot_ids = reinterpret_cast<int64_t*>(src_host + wire);
+    for (uint32_t r = 0; r < n; ++r) slot_ids[r] = mapping[2 * r + 1];
+
+    if ((prof && hipEventRecord(sl.p_c0, ring->copy) != hipSuccess) ||
+        hipMemcpyAsync(sl.dev, src_host, need, hipMemcpyHostToDevice, ring->copy) != hipSuccess ||
+        (prof && hipEventRecord(sl.p_c1, ring->copy) != hipSuccess) ||
         hipEventRecord(sl.ev_a, ring->copy) != hipSuccess || hipStreamWaitEvent(stream, sl.ev_a, 0) != hipSuccess)
         return -1;
+    sl.held = pf;
     si_reload_desc d{};
     d.wire = sl.dev;
     d.wire_stride = stride;
@@ -509,9 +759,20 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     d.layer = layer;
     d.staging = sl.stage;
     d.fail_count = fail_count;
+    if (prof && hipEventRecord(sl.p_k0, stream) != hipSuccess) return -1;
     if (secure_infer_gpu_reload_layer(stream, s, &d) != 0) return -1;
+    if (prof && hipEventRecord(sl.p_k1, stream) != hipSuccess) return -1;
     ring->used[si] = true;
     if (hipEventRecord(sl.ev_b, stream) != hipSuccess) return -1;
+    if (prof) {
+        sl.row.pending = true;
+        sl.row.layer = layer;
+        sl.row.kind = kind;
+        sl.row.n = n;
+        sl.row.bytes = bytes;
+        sl.row.source = source;
+        sl.row.seal_us = seal_us;
+    }
     if (!observe) return 0;
 
     // Status words to pinned memory once the kernel is done; the slot is free
@@ -538,6 +799,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     ob->heads = heads;
     ob->dim = head_dim;
     ob->stream = stream;
+    ob->job_id = si_internal::current_job_id();
     ob->mapping.assign(mapping, mapping + 2 * size_t(n));
     ob->status = std::move(status);
     std::lock_guard<std::mutex> go(g_obs_lock);
@@ -699,6 +961,35 @@ int wait_observed_layer(uint32_t layer, bool* found)
     }
 }
 
+int wait_observed_job(uint64_t job_id, bool* found)
+{
+    std::vector<std::shared_ptr<Observed>> recs;
+    {
+        std::lock_guard<std::mutex> g(g_obs_lock);
+        for (auto it = g_observed.begin(); it != g_observed.end();) {
+            if (it->second->job_id == job_id) {
+                recs.push_back(it->second);
+                it = g_observed.erase(it);
+            } else {
+                ++it;
+            }
+        }
+    }
+    if (recs.empty()) return 1;
+    *found = true;
+    bool valid = true;
+    for (auto& ob : recs) {
+        const uint32_t n = uint32_t(ob->mapping.size() / 2);
+        if (hipEventSynchronize(ob->status->ready) != hipSuccess) {
+            valid = false;
+        } else {
+            for (uint32_t r = 0; r < n; ++r) valid = valid && ob->status->host[r] == 1u;
+        }
+        give_status(ob->ds, std::move(ob->status));
+    }
+    return valid ? 1 : 0;
+}
+
 }  // namespace si_internal
 
 extern "C" {
@@ -715,6 +1006,100 @@ int secure_infer_h2d_swap(hipStream_t stream, si_session* s, const void* host_ba
                          mapping, n, kind, layer, codec_bits, heads, head_dim, fail_count,
                          si_internal::group_open());
 }
+
+int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t host_block_bytes, uint64_t host_nblocks,
+                              const int64_t* mapping, uint32_t n, uint32_t kind, uint32_t layer, uint32_t codec_bits,
+                              uint32_t heads, uint32_t head_dim)
+{
+    if (!s || !host_base || !mapping || n == 0 || kind > 1 || host_nblocks == 0) return -1;
+    uint64_t bytes = 0;
+    if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
+    for (uint32_t r = 0; r < n; ++r)
+        if (mapping[2 * r] < 0 || uint64_t(mapping[2 * r]) >= host_nblocks) return -1;
+    auto pf = std::make_shared<Prefetch>();
+    pf->keys = si_internal::session_keys(s);
+    if (bytes > pf->keys.max_record_bytes) return -1;
+    pf->session = s;
+    pf->host_base = static_cast<const uint8_t*>(host_base);
+    pf->host_block_bytes = host_block_bytes;
+    pf->kind = kind;
+    pf->layer = layer;
+    pf->codec = codec_bits;
+    pf->heads = heads;
+    pf->dim = head_dim;
+    pf->n = n;
+    pf->bytes = bytes;
+    pf->stride = secure_infer_wire_stride(bytes);
+    pf->tag_off = tag_offset(bytes);
+    pf->host_blocks.resize(n);
+    for (uint32_t r = 0; r < n; ++r) pf->host_blocks[r] = mapping[2 * r];
+    const size_t need = size_t(n) * pf->stride + size_t(n) * 8;
+    pf->host = take_pf_buffer(need, pf->cap);
+    if (!pf->host) return -1;  // over SECURE_INFER_PREFETCH_MB: the swap seals on demand
+    pf->t0 = si_internal::reserve_tickets(n);
+    if (!si_internal::replay_reserve_range(pf->t0, n)) return -1;
+    const uint32_t per_task = 4;
+    pf->tasks = (n + per_task - 1) / per_task;
+    {
+        std::lock_guard<std::mutex> g(g_pf_lock);
+        g_prefetch.push_back(pf);
+    }
+    const auto ts = std::chrono::steady_clock::now();
+    for (uint32_t r0 = 0; r0 < n; r0 += per_task) {
+        const uint32_t r1 = std::min(n, r0 + per_task);
+        Pool::get().submit([pf, r0, r1, ts] {
+            bool ok = true;
+            for (uint32_t r = r0; r < r1 && ok; ++r) {
+                const int64_t hb = pf->host_blocks[r];
+                seal_record(pf->keys, pf->host_base + uint64_t(hb) * pf->host_block_bytes, pf->bytes, pf->tag_off,
+                            pf->t0 + r, pf->host + uint64_t(r) * pf->stride, pf->layer, pf->kind, hb, ok);
+            }
+            std::lock_guard<std::mutex> g(pf->m);
+            if (!ok) pf->failed = true;
+            if (++pf->done == pf->tasks) {
+                pf->seal_us = us_since(ts);
+                pf->cv.notify_all();
+            }
+        });
+    }
+    return 0;
+}
+
+void secure_infer_get_transfer_prefetch_stats(uint64_t* ready, uint64_t* busy_fallback, uint64_t* missing_fallback)
+{
+    if (ready) *ready = g_pf_ready.load();
+    if (busy_fallback) *busy_fallback = g_pf_waited.load();
+    if (missing_fallback) *missing_fallback = g_pf_missing.load();
+}
+
+uint64_t secure_infer_count_ready_unconsumed_gcm_tickets(void)
+{
+    uint64_t n = 0;
+    std::lock_guard<std::mutex> g(g_pf_lock);
+    for (const auto& pf : g_prefetch) {
+        std::lock_guard<std::mutex> gp(pf->m);
+        if (pf->done == pf->tasks && !pf->failed) n += pf->n;
+    }
+    return n;
+}
+
+void secure_infer_retire_transfer_prefetches(void)
+{
+    std::vector<std::shared_ptr<Prefetch>> drop;
+    {
+        std::lock_guard<std::mutex> g(g_pf_lock);
+        drop.swap(g_prefetch);
+    }
+    // Sealing tasks still running hold their prefetch; its buffer returns to
+    // the free list when the last holder lets go.  Their tickets stay used.
+    for (auto& pf : drop) wait_sealed(*pf);
+}
+
+void secure_infer_invalidate_transfer_prefetches(void) { secure_infer_retire_transfer_prefetches(); }
+
+void secure_infer_flush_completed_h2d_profile(void) { profile_sweep(false); }
+
+void secure_infer_drain_h2d_profile_after_job(void) { profile_sweep(true); }
 
 int secure_infer_test_tamper_h2d(int32_t layer, int32_t kind, int64_t host_block, uint32_t shots)
 {

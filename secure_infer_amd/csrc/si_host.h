@@ -28,6 +28,14 @@ bool replay_reserve_range(uint64_t t0, uint64_t n);
 // True while the calling thread is inside secure_infer_h2d_layer_group_begin/end.
 bool group_open();
 
+// The job id set by secure_infer_recovery_set_job_id.
+uint64_t current_job_id();
+
+// Observed H2D swaps of job `job_id` on every layer, waited for without
+// retries: 1 if every record authenticated, 0 otherwise; *found is set when
+// the job had observed swaps (left unchanged otherwise).
+int wait_observed_job(uint64_t job_id, bool* found);
+
 // Observed H2D swaps of `layer` (host-sealed records): waits for their
 // status words, re-seals every record that failed once under a fresh ticket
 // and checks it again.  0 if every record authenticated, -1 otherwise;

@@ -408,26 +408,40 @@ class NativeTransfer:
         self._keep = {}
         self._staging = None
 
+    def _plan(self, mapping: torch.Tensor):
+        """Groups of (kind, slice index, mapping part) in submission order:
+        causal groups of ``causal_group_blocks`` from the tail, then K / V,
+        then the slice streams' stripes."""
+        n = int(mapping.shape[0])
+        group = self.causal_group_blocks
+        g = group if group and n > group else n
+        nsl = len(self.streams)
+        plan, end = [], n
+        while end > 0:
+            start = max(0, end - g)
+            m = mapping[start:end]
+            k = end - start
+            parts = []
+            for kind in (0, 1):
+                for j in range(nsl):
+                    part = m[k * j // nsl:k * (j + 1) // nsl].contiguous()
+                    if part.shape[0]:
+                        parts.append((kind, j, part))
+            plan.append((k, parts))
+            end = start
+        return plan
+
+    @staticmethod
+    def _host_pool(src: torch.Tensor) -> torch.Tensor:
+        if src.is_cuda or not src.is_contiguous():
+            raise ValueError("host pools must be contiguous CPU tensors")
+        return src
+
     def single_layer_kv_transfer(self, payload, destination, *unused) -> None:
         host, mapping = payload
         mapping = mapping.to(device="cpu", dtype=torch.int64).contiguous()
-        group = self.causal_group_blocks
-        if group and mapping.shape[0] > group:
-            layer = self.layer
-            self.causal_group_blocks = 0
-            try:
-                end = int(mapping.shape[0])
-                while end > 0:
-                    start = max(0, end - group)
-                    self.layer = layer
-                    self.single_layer_kv_transfer((host, mapping[start:end]), destination)
-                    end = start
-            finally:
-                self.causal_group_blocks = group
-                self.layer = layer + 1
-            return
-        n = int(mapping.shape[0])
-        if n == 0:
+        plan = self._plan(mapping)
+        if not plan:
             self.layer += 1
             return
         bits = self.shape.bits_for(self.layer)
@@ -436,28 +450,43 @@ class NativeTransfer:
         for st in streams:
             if st != parent:
                 st.wait_stream(parent)
-        _check(lib().secure_infer_h2d_layer_group_begin(2 * n), "h2d_layer_group_begin")
-        try:
-            for kind, (src, dst) in enumerate(zip(host, destination)):
-                if src.is_cuda or not src.is_contiguous():
-                    raise ValueError("host pools must be contiguous CPU tensors")
-                _dev(dst, "destination cache")
-                for j, st in enumerate(streams):
-                    part = mapping[n * j // len(streams):n * (j + 1) // len(streams)].contiguous()
-                    if part.shape[0] == 0:
-                        continue
+        for k, parts in plan:
+            _check(lib().secure_infer_h2d_layer_group_begin(2 * k), "h2d_layer_group_begin")
+            try:
+                for kind, j, part in parts:
+                    src, dst = self._host_pool(host[kind]), destination[kind]
+                    _dev(dst, "destination cache")
                     _check(lib().secure_infer_h2d_swap(
-                        _stream(st), self.session._h, ct.c_void_p(src.data_ptr()),
+                        _stream(streams[j]), self.session._h, ct.c_void_p(src.data_ptr()),
                         src[0].numel() * src.element_size(), src.shape[0], ct.c_void_p(dst.data_ptr()),
                         dst[0].numel() * dst.element_size(), dst.shape[0],
                         ct.c_void_p(part.data_ptr()), part.shape[0], kind, self.layer, bits,
                         self.shape.heads, self.shape.head_dim, None), "h2d_swap")
-        finally:
-            _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
+            finally:
+                _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
         for st in streams:
             if st != parent:
                 parent.wait_stream(st)
         self.layer += 1
+
+    def prefetch_kv_transfer(self, payload, layer: int) -> bool:
+        """Seal `layer`'s records on the host worker pool ahead of demand
+        (the reference's CPU ciphertext prefetch, secure_infer.cpp:3264-3710),
+        in the decomposition single_layer_kv_transfer will submit, so that
+        transfer only copies them.  Returns False if the prefetch budget is
+        spent (the transfer then seals on demand)."""
+        host, mapping = payload
+        mapping = mapping.to(device="cpu", dtype=torch.int64).contiguous()
+        bits = self.shape.bits_for(layer)
+        ok = True
+        for _, parts in self._plan(mapping):
+            for kind, _, part in parts:
+                src = self._host_pool(host[kind])
+                ok &= lib().secure_infer_h2d_prefetch(
+                    self.session._h, ct.c_void_p(src.data_ptr()), src[0].numel() * src.element_size(),
+                    src.shape[0], ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer, bits,
+                    self.shape.heads, self.shape.head_dim) == 0
+        return ok
 
     def single_layer_wire_transfer(self, payload, destination, ticket_base: int = 0,
                                    iv_words_dev: torch.Tensor | None = None) -> None:
@@ -564,8 +593,36 @@ class D2HTransfer:
 
 
 def retire_transfer_prefetches() -> None:
-    """No-op export the reference's EncodedStore binds (transport_codec.py:50)."""
+    """Drops records sealed ahead of demand that no swap consumed
+    (secure_infer.cpp:1137-1148; EncodedStore binds it, transport_codec.py:50)."""
     lib().secure_infer_retire_transfer_prefetches()
+
+
+def transfer_prefetch_stats() -> dict:
+    """Swaps served from ready prefetches / after waiting for one / sealed on
+    demand (secure_infer_get_transfer_prefetch_stats, secure_infer.cpp:817-830)."""
+    v = [ct.c_uint64() for _ in range(3)]
+    lib().secure_infer_get_transfer_prefetch_stats(*[ct.byref(x) for x in v])
+    return {"ready": v[0].value, "busy_fallback": v[1].value, "missing_fallback": v[2].value}
+
+
+def set_job_id(job_id: int) -> None:
+    """secure_infer_recovery_set_job_id (secure_infer.cpp:5311)."""
+    lib().secure_infer_recovery_set_job_id(job_id)
+
+
+def wait_job_authentication(job_id: int) -> int:
+    """1 if every record of the job authenticated, 0 if not, -1 if it has none
+    (secure_infer_recovery_wait_job_authentication, secure_infer.cpp:7336-7372)."""
+    return int(lib().secure_infer_recovery_wait_job_authentication(job_id))
+
+
+def flush_completed_h2d_profile() -> None:
+    lib().secure_infer_flush_completed_h2d_profile()
+
+
+def drain_h2d_profile_after_job() -> None:
+    lib().secure_infer_drain_h2d_profile_after_job()
 
 
 def inject_h2d_tamper(layer: int = -1, kind: int = -1, host_block: int = -1, shots: int = 1) -> None:

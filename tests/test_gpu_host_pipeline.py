@@ -162,3 +162,148 @@ def test_d2h_api_semantics():
     assert L.secure_infer_d2h_group_end() == 0
     assert L.secure_infer_d2h_batch_device_barrier() == 0
     assert L.secure_infer_d2h_batch_end() == 0
+
+
+def _layers(rng, nlayers, ncpu, heads, dim):
+    out = []
+    for layer in range(nlayers):
+        hk, hv = pools(rng, ncpu, heads, dim)
+        si.register_host_range(hk, layer, 0)
+        si.register_host_range(hv, layer, 1)
+        out.append((hk, hv))
+    return out
+
+
+def test_prefetched_records_serve_the_swaps():
+    """Ahead-of-demand sealing (secure_infer.cpp:3264-3710): every swap of a
+    3-layer reload with 16-block causal groups finds its records sealed, the
+    caches end bit-exact, and nothing is left unconsumed."""
+    rng = np.random.default_rng(141)
+    heads, dim, ncpu, nslots, nlayers = 2, 128, 41, 64, 3
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 9, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        host_layers = _layers(rng, nlayers, ncpu, heads, dim)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16)
+        slot_ids = rng.permutation(nslots)[:ncpu]
+        mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
+        before = si.transfer_prefetch_stats()
+        for layer in range(nlayers):
+            assert nt.prefetch_kv_transfer((host_layers[layer], mapping), layer)
+        caches_l = [caches(nslots, heads, dim) for _ in range(nlayers)]
+        for layer in range(nlayers):
+            nt.single_layer_kv_transfer((host_layers[layer], mapping), caches_l[layer])
+        after = si.transfer_prefetch_stats()
+        swaps = nlayers * 3 * 2  # groups of 16, 16, 9 blocks, K and V
+        served = (after["ready"] - before["ready"]) + (after["busy_fallback"] - before["busy_fallback"])
+        assert served == swaps and after["missing_fallback"] == before["missing_fallback"]
+        assert int(_lib.load().secure_infer_count_ready_unconsumed_gcm_tickets()) == 0
+        idx = torch.from_numpy(slot_ids.astype(np.int64)).to(DEV)
+        for layer in range(nlayers):
+            assert nt.wait_layer(layer) == 0
+            (hk, hv), (ck, cv) = host_layers[layer], caches_l[layer]
+            assert torch.equal(ck.index_select(0, idx).cpu(), hk) and torch.equal(cv.index_select(0, idx).cpu(), hv)
+    finally:
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()
+
+
+def test_retired_prefetch_falls_back_to_sealing_on_demand():
+    rng = np.random.default_rng(142)
+    heads, dim, ncpu, nslots = 2, 128, 4, 8
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 1, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        (hk, hv), = _layers(rng, 1, ncpu, heads, dim)
+        mapping = torch.tensor([[0, 5], [3, 1]], dtype=torch.int64)
+        nt = si.NativeTransfer(sess, shape)
+        assert nt.prefetch_kv_transfer(((hk, hv), mapping), 0)
+        hk[3].fill_(0x1234)  # host block changed after the prefetch
+        si.retire_transfer_prefetches()
+        before = si.transfer_prefetch_stats()
+        ck, cv = caches(nslots, heads, dim)
+        nt.single_layer_kv_transfer(((hk, hv), mapping), (ck, cv))
+        assert nt.wait_layer(0) == 0
+        after = si.transfer_prefetch_stats()
+        assert after["missing_fallback"] - before["missing_fallback"] == 2
+        assert torch.equal(ck[1].cpu(), hk[3]) and torch.equal(cv[5].cpu(), hv[0])
+    finally:
+        si.clear_host_ranges()
+
+
+def test_job_authentication_spans_layers():
+    """secure_infer_recovery_wait_job_authentication (secure_infer.cpp:7336-7372):
+    every record of the job on every layer, no retry; 1 / 0 / -1."""
+    rng = np.random.default_rng(143)
+    heads, dim, ncpu, nslots = 2, 128, 6, 12
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 4, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        host_layers = _layers(rng, 2, ncpu, heads, dim)
+        mapping = torch.tensor([[1, 3], [4, 0], [5, 7]], dtype=torch.int64)
+        nt = si.NativeTransfer(sess, shape)
+        si.set_job_id(7001)
+        for layer in range(2):
+            nt.single_layer_kv_transfer((host_layers[layer], mapping), caches(nslots, heads, dim))
+        assert si.wait_job_authentication(7001) == 1
+        si.set_job_id(7002)
+        si.inject_h2d_tamper(layer=1, kind=0, host_block=4, shots=1)
+        nt.layer = 0
+        for layer in range(2):
+            nt.single_layer_kv_transfer((host_layers[layer], mapping), caches(nslots, heads, dim))
+        assert si.wait_job_authentication(7002) == 0   # no strict retry on the job path
+        assert si.wait_job_authentication(7003) == -1  # no records
+    finally:
+        si.inject_h2d_tamper(shots=0)
+        si.set_job_id(0)
+        si.clear_host_ranges()
+
+
+LEDGER_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import secure_infer_amd as si
+heads, dim = 2, 128
+shape = si.LayerShape(heads, dim)
+sess = si.GcmSession(bytes(16), b"abcd", 0, max_record_bytes=shape.record_bytes)
+hk = torch.zeros((8, 128, heads, dim), dtype=torch.int16)
+hv = torch.ones((8, 128, heads, dim), dtype=torch.int16)
+ck = torch.zeros((8, 128, heads, dim), dtype=torch.int16, device="cuda")
+cv = torch.zeros_like(ck)
+nt = si.NativeTransfer(sess, shape)
+m = torch.tensor([[0, 1], [2, 3], [7, 5]], dtype=torch.int64)
+assert nt.prefetch_kv_transfer(((hk, hv), m), 0)
+nt.single_layer_kv_transfer(((hk, hv), m), (ck, cv))
+nt.single_layer_kv_transfer(((hk, hv), m), (ck, cv))
+assert nt.wait_layer(0) == 0 and nt.wait_layer(1) == 0
+si.drain_h2d_profile_after_job()
+print("done")
+"""
+
+
+def test_h2d_profile_ledger(tmp_path):
+    """SECURE_INFER_H2D_PROFILE: one CSV row per swap with host seal, H2D copy
+    and kernel time (the reference's per-copy rows, secure_infer.cpp:6085-6137)."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    csv = tmp_path / "h2d.csv"
+    env = dict(os.environ, SECURE_INFER_H2D_PROFILE=str(csv))
+    out = subprocess.run([sys.executable, "-c", LEDGER_SCRIPT, str(Path(__file__).resolve().parent.parent)],
+                         env=env, capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0 and "done" in out.stdout, out.stderr[-2000:]
+    lines = csv.read_text().strip().splitlines()
+    assert lines[0] == "layer,kind,records,record_bytes,source,seal_us,h2d_copy_us,kernel_us"
+    rows = [l.split(",") for l in lines[1:]]
+    assert len(rows) == 4
+    # layer 0 was sealed ahead of demand (ready or still sealing when its swap
+    # came), layer 1 on demand
+    src = sorted((r[0], r[1], r[4].replace("prefetch_waited", "prefetched")) for r in rows)
+    assert src == [("0", "0", "prefetched"), ("0", "1", "prefetched"), ("1", "0", "sealed"), ("1", "1", "sealed")]
+    for r in rows:
+        assert int(r[2]) == 3 and int(r[3]) == 128 * 2 * 128 * 2
+        assert float(r[5]) > 0 and float(r[6]) > 0 and float(r[7]) > 0
