@@ -143,6 +143,8 @@ typedef struct si_reload_desc {
     uint32_t layer;           /* layer index (codec header, status)            */
     void* staging;            /* device scratch, nrec*align32(bytes) (codec)   */
     uint32_t* fail_count;     /* device u32: += number of failed records; NULL ok */
+    uint32_t* status_out;     /* device, optional: nrec u32, record r's status
+                                 (1 / 0) also at status_out[r]; NULL ok      */
 } si_reload_desc;
 
 int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* session,

@@ -21,7 +21,7 @@ class SiReloadDesc(ct.Structure):
         ("iv_words", _v), ("ticket_base", _u64), ("cache_k", _v), ("cache_v", _v),
         ("slot_bytes", _u64), ("nslots", _u64), ("slots", _v), ("codec_bits", _u32),
         ("heads", _u32), ("head_dim", _u32), ("layer", _u32), ("staging", _v),
-        ("fail_count", _v),
+        ("fail_count", _v), ("status_out", _v),
     ]
 
 

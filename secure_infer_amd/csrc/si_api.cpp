@@ -368,9 +368,11 @@ uint32_t npow_for(uint64_t bytes, uint64_t aad_bytes)
 }
 
 // Per-key contexts of the kernel-level entry points (keyed by key and H);
-// those calls hold this lock for their whole duration.
+// those calls hold this lock for their whole duration.  Like every registry
+// of the library it is never destroyed: its device buffers must not be freed
+// by static destructors after the HIP runtime has begun to tear down.
 std::mutex g_ctx_lock;
-std::vector<std::unique_ptr<DevCtx>> g_ctx_cache;
+std::vector<std::unique_ptr<DevCtx>>& g_ctx_cache = *new std::vector<std::unique_ptr<DevCtx>>();
 
 // Per-stream accumulator workspaces (and the parking area of two-record
 // shares).  A launch holds its stream's workspace lock from the workspace
@@ -383,7 +385,8 @@ struct Workspace {
     size_t park_cap = 0;
 };
 std::mutex g_ws_lock;
-std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>> g_ws;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>>& g_ws =
+    *new std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>>();
 
 Workspace* workspace_of(hipStream_t stream)
 {
@@ -485,12 +488,12 @@ struct HostRange {
     size_t block_bytes;
 };
 std::mutex g_ranges_lock;
-std::vector<HostRange> g_ranges;
+std::vector<HostRange>& g_ranges = *new std::vector<HostRange>();
 
 // Tickets used so far, as disjoint half-open intervals [first, last)
 // (tickets are reserved in runs, so the set stays small).
 std::mutex g_replay_lock;
-std::map<uint64_t, uint64_t> g_replay;
+std::map<uint64_t, uint64_t>& g_replay = *new std::map<uint64_t, uint64_t>();
 
 bool replay_insert(uint64_t a, uint64_t b)
 {
@@ -533,7 +536,7 @@ struct TrackedLayer {
     uint64_t job_id;
 };
 std::mutex g_track_lock;
-std::multimap<uint32_t, TrackedLayer> g_tracked;
+std::multimap<uint32_t, TrackedLayer>& g_tracked = *new std::multimap<uint32_t, TrackedLayer>();
 
 }  // namespace
 
@@ -671,7 +674,9 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
         b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
     }
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
-    if (si::launch_gcm(0, stream, s->ctx->dev, b, sc, acc, al) != hipSuccess) return -1;
+    si::Sched sc2 = sc;
+    sc2.status_out = d->status_out;
+    if (si::launch_gcm(0, stream, s->ctx->dev, b, sc2, acc, al) != hipSuccess) return -1;
     if (codec) {
         si::CodecBatch cb{};
         cb.nrec = d->nrec;

@@ -888,6 +888,7 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
         const uint32_t ok = (diff == 0 && !v.bad) ? 1u : 0u;
         if (tid == 0) {
             *gmem(v.status) = ok;
+            if (sch.status_out) gmem(sch.status_out)[r0 + s] = ok;
             if (!ok && v.fail_count) atomicAdd(v.fail_count, 1u);
         }
         if (!ok && kMode != MODE_VERIFY && !v.skip) zero_bytes(v.dst, sch.bytes, tid, SI_NT);

@@ -112,11 +112,14 @@ public:
 private:
     Pool()
     {
-        // CPUs this process may run on (the affinity mask, not the machine).
+        // CPUs this process may run on (the affinity mask, not the machine),
+        // less one that stays free for the HIP runtime's own threads (they
+        // submit the ring's copies while the pool seals the next swap).
         unsigned n = std::thread::hardware_concurrency();
         cpu_set_t set;
         CPU_ZERO(&set);
         if (sched_getaffinity(0, sizeof(set), &set) == 0) n = unsigned(CPU_COUNT(&set));
+        if (n > 2) n -= 1;
         if (const char* e = std::getenv("SECURE_INFER_HOST_THREADS")) n = unsigned(std::atoi(e));
         if (n == 0) n = 1;
         if (n > 256) n = 256;
@@ -347,8 +350,12 @@ struct DeviceState {
     std::vector<std::unique_ptr<StatusBuf>> free_status;
 };
 
+// The host runtime's registries are created once and never destroyed: the
+// worker pool's threads, ring slots holding pinned and device buffers and
+// pending prefetches may still refer to them while the process exits, after
+// the HIP runtime has begun to tear down.
 std::mutex g_states_lock;
-std::map<int, std::unique_ptr<DeviceState>> g_states;
+std::map<int, std::unique_ptr<DeviceState>>& g_states = *new std::map<int, std::unique_ptr<DeviceState>>();
 
 DeviceState* device_state()
 {
@@ -375,7 +382,11 @@ StreamRing* ring_of(DeviceState* ds, hipStream_t stream)
         if (hipStreamCreateWithFlags(&nr->copy, hipStreamNonBlocking) != hipSuccess ||
             hipStreamCreateWithFlags(&nr->observe, hipStreamNonBlocking) != hipSuccess)
             return nullptr;
-        size_t slots = 4;
+        // Slots per stream: a layer of 16-block causal groups is 6 swaps, and
+        // a slot is reused only after its kernel and status copy are done
+        // (the reference's default budget is 32 single-record slots,
+        // secure_infer.cpp:5608-5647).
+        size_t slots = 16;
         if (const char* e = std::getenv("SECURE_INFER_H2D_SLOTS")) slots = size_t(std::max(2, std::atoi(e)));
         for (size_t i = 0; i < slots; ++i) {
             auto mbuf = std::make_unique<Mirror>();
@@ -525,13 +536,15 @@ struct Prefetch {
     std::condition_variable cv;
     uint32_t tasks = 0, done = 0;
     bool failed = false;
-    double seal_us = 0;
+    bool started = false;
+    std::chrono::steady_clock::time_point first_start{};
+    double seal_us = 0;  // first sealing task's start to the last one's end
     ~Prefetch();
 };
 
 std::mutex g_pf_lock;
-std::vector<std::shared_ptr<Prefetch>> g_prefetch;            // sealed or sealing, not consumed
-std::vector<std::pair<uint8_t*, size_t>> g_pf_free;          // pinned buffers to reuse
+std::vector<std::shared_ptr<Prefetch>>& g_prefetch = *new std::vector<std::shared_ptr<Prefetch>>();  // not consumed
+std::vector<std::pair<uint8_t*, size_t>>& g_pf_free = *new std::vector<std::pair<uint8_t*, size_t>>();  // to reuse
 size_t g_pf_bytes = 0;                                        // pinned bytes held by prefetches
 std::atomic<uint64_t> g_pf_ready{0}, g_pf_waited{0}, g_pf_missing{0};
 
@@ -628,7 +641,7 @@ struct Observed {
 };
 
 std::mutex g_obs_lock;
-std::multimap<uint32_t, std::shared_ptr<Observed>> g_observed;
+std::multimap<uint32_t, std::shared_ptr<Observed>>& g_observed = *new std::multimap<uint32_t, std::shared_ptr<Observed>>();
 
 // ---------------------------------------------------------------- H2D
 
@@ -671,6 +684,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     if (!ring) return -1;
     const uint64_t stride = secure_infer_wire_stride(bytes);
     const uint64_t tag_off = tag_offset(bytes);
+    // [wire records][slot ids, n x 8] travel; [statuses, n x 4] come back
     const size_t wire = size_t(n) * stride;
     const size_t need = wire + size_t(n) * 8;
     const bool prof = profile_on();
@@ -700,7 +714,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
         profile_retire(sl);
         sl.held.reset();  // the copy from a prefetch buffer is complete
     }
-    if (!sl.reserve(need, codec_bits ? size_t(n) * tag_off : 0)) return -1;
+    if (!sl.reserve(need + size_t(n) * 4, codec_bits ? size_t(n) * tag_off : 0)) return -1;
     if (prof && !sl.init_profile()) return -1;
 
     // Host side: seal on demand into the ring slot, or take the prefetched
@@ -759,6 +773,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     d.layer = layer;
     d.staging = sl.stage;
     d.fail_count = fail_count;
+    d.status_out = observe ? reinterpret_cast<uint32_t*>(sl.dev + need) : nullptr;
     if (prof && hipEventRecord(sl.p_k0, stream) != hipSuccess) return -1;
     if (secure_infer_gpu_reload_layer(stream, s, &d) != 0) return -1;
     if (prof && hipEventRecord(sl.p_k1, stream) != hipSuccess) return -1;
@@ -779,8 +794,8 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     // again after that copy.
     if (hipEventRecord(sl.ev_c, stream) != hipSuccess ||
         hipStreamWaitEvent(ring->observe, sl.ev_c, 0) != hipSuccess ||
-        hipMemcpy2DAsync(status->host, 4, sl.dev + tag_off + 16, stride, 4, n, hipMemcpyDeviceToHost,
-                         ring->observe) != hipSuccess ||
+        hipMemcpyAsync(status->host, sl.dev + need, size_t(n) * 4, hipMemcpyDeviceToHost, ring->observe) !=
+            hipSuccess ||
         hipEventRecord(status->ready, ring->observe) != hipSuccess ||
         hipEventRecord(sl.ev_b, ring->observe) != hipSuccess)
         return -1;
@@ -1038,16 +1053,22 @@ int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t hos
     if (!pf->host) return -1;  // over SECURE_INFER_PREFETCH_MB: the swap seals on demand
     pf->t0 = si_internal::reserve_tickets(n);
     if (!si_internal::replay_reserve_range(pf->t0, n)) return -1;
-    const uint32_t per_task = 4;
+    const uint32_t per_task = 1;  // one record per task: the pool balances records, not swaps
     pf->tasks = (n + per_task - 1) / per_task;
     {
         std::lock_guard<std::mutex> g(g_pf_lock);
         g_prefetch.push_back(pf);
     }
-    const auto ts = std::chrono::steady_clock::now();
     for (uint32_t r0 = 0; r0 < n; r0 += per_task) {
         const uint32_t r1 = std::min(n, r0 + per_task);
-        Pool::get().submit([pf, r0, r1, ts] {
+        Pool::get().submit([pf, r0, r1] {
+            {
+                std::lock_guard<std::mutex> g(pf->m);
+                if (!pf->started) {
+                    pf->started = true;
+                    pf->first_start = std::chrono::steady_clock::now();
+                }
+            }
             bool ok = true;
             for (uint32_t r = r0; r < r1 && ok; ++r) {
                 const int64_t hb = pf->host_blocks[r];
@@ -1057,7 +1078,7 @@ int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t hos
             std::lock_guard<std::mutex> g(pf->m);
             if (!ok) pf->failed = true;
             if (++pf->done == pf->tasks) {
-                pf->seal_us = us_since(ts);
+                pf->seal_us = us_since(pf->first_start);
                 pf->cv.notify_all();
             }
         });

@@ -61,6 +61,8 @@ struct Sched {
     uint32_t pairs;      // 1: workgroup w owns the whole records 2w and 2w+1
     uint4* park;         // pairs: each thread's segment-0 product during segment 1
                          // (one uint4 per thread of each workgroup)
+    uint32_t* status_out;  // layer form, optional: record r's status also at
+                           // status_out[r] (one contiguous array to copy back)
 };
 // Scratch of the allocation-free reload (secure_infer_gpu_reload_layer_noalloc):
 // one device array per GPU, [accumulators of up to SI_NOALLOC_MAX_RECORDS

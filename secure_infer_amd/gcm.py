@@ -387,6 +387,14 @@ class NativeTransfer:
     * Each (kind, slice) is sealed on the host (OpenSSL, worker pool), copied
       through the slice stream's pinned ring and verified / decrypted /
       scattered on the device; the call returns once the work is queued.
+      With ``pipeline_seal`` the layer's seals are queued on the worker pool
+      first, so later parts seal while earlier parts are copied (the
+      reference's CPU ciphertext prefetch, secure_infer.cpp:3264-3710); by
+      default ("auto") only for records of at least PIPELINE_MIN_RECORD_BYTES,
+      where a record's seal outweighs the queueing (MI355X box, 16 host
+      CPUs: bf16 Llama-3-8B layer 1229 -> 707 us end to end; 41-KB int4
+      records 812 -> 1146 us, so off for them).  A layer already sealed with
+      ``prefetch_kv_transfer`` is not sealed again.
       ``wait_layer`` returns the layer's authentication result after at most
       one strict retry per failed record (wait_for_layer_load,
       connector.py:378-410; secure_infer.cpp:7303-7333).
@@ -397,16 +405,20 @@ class NativeTransfer:
     a failure among them is final (there is no host copy to retry from).
     """
 
+    PIPELINE_MIN_RECORD_BYTES = 128 << 10
+
     def __init__(self, session: GcmSession, shape: LayerShape, stream=None, streams=None,
-                 causal_group_blocks: int = 0):
+                 causal_group_blocks: int = 0, pipeline_seal="auto"):
         self.session = session
         self.shape = shape
         self.stream = stream
         self.streams = list(streams) if streams else [stream]
         self.causal_group_blocks = int(causal_group_blocks)
+        self.pipeline_seal = pipeline_seal
         self.layer = 0
         self._keep = {}
         self._staging = None
+        self._prefetched = set()
 
     def _plan(self, mapping: torch.Tensor):
         """Groups of (kind, slice index, mapping part) in submission order:
@@ -444,6 +456,11 @@ class NativeTransfer:
         if not plan:
             self.layer += 1
             return
+        if self.layer in self._prefetched:
+            self._prefetched.discard(self.layer)
+        elif self._pipelined(self.layer) and (len(plan) > 1 or len(plan[0][1]) > 1):
+            self.prefetch_kv_transfer(payload, self.layer)
+            self._prefetched.discard(self.layer)
         bits = self.shape.bits_for(self.layer)
         parent = torch.cuda.current_stream()
         streams = [_torch_stream(s) for s in self.streams]
@@ -469,6 +486,11 @@ class NativeTransfer:
                 parent.wait_stream(st)
         self.layer += 1
 
+    def _pipelined(self, layer: int) -> bool:
+        if self.pipeline_seal == "auto":
+            return self.shape.record_bytes_for(layer) >= self.PIPELINE_MIN_RECORD_BYTES
+        return bool(self.pipeline_seal)
+
     def prefetch_kv_transfer(self, payload, layer: int) -> bool:
         """Seal `layer`'s records on the host worker pool ahead of demand
         (the reference's CPU ciphertext prefetch, secure_infer.cpp:3264-3710),
@@ -486,6 +508,7 @@ class NativeTransfer:
                     self.session._h, ct.c_void_p(src.data_ptr()), src[0].numel() * src.element_size(),
                     src.shape[0], ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer, bits,
                     self.shape.heads, self.shape.head_dim) == 0
+        self._prefetched.add(layer)
         return ok
 
     def single_layer_wire_transfer(self, payload, destination, ticket_base: int = 0,

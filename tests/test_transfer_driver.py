@@ -53,8 +53,19 @@ class Recorder:
         self.calls.append(("swap", stream.value, kind, layer, bits, pairs, host_nblocks, nslots))
         return 0
 
+    def secure_infer_codec_width(self, bits, heads, dim):
+        from secure_infer_amd import _lib
+        return _lib.load().secure_infer_codec_width(bits, heads, dim)
 
-def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None):
+    def secure_infer_h2d_prefetch(self, sess, host_base, host_block_bytes, host_nblocks, mapping_ptr, n, kind,
+                                  layer, bits, heads, dim):
+        import ctypes as ct
+        arr = (ct.c_int64 * (2 * n)).from_address(mapping_ptr.value)
+        self.calls.append(("prefetch", kind, layer, bits, [(arr[2 * i], arr[2 * i + 1]) for i in range(n)]))
+        return 0
+
+
+def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False):
     rec = Recorder()
     parent = FakeStream("parent")
     shape = shape or si.LayerShape(2, 64)
@@ -69,6 +80,8 @@ def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None):
          mock.patch.object(gcm, "_dev", lambda t, name: None), \
          mock.patch.object(gcm.torch.cuda, "current_stream", return_value=parent):
         nt.single_layer_kv_transfer((host, mapping), dest, None, False, 2, True, False)
+    if not keep_prefetch:
+        rec.calls = [c for c in rec.calls if c[0] != "prefetch"]
     return nt, rec, parent
 
 
@@ -141,3 +154,23 @@ def test_mixed_shape_bits_reach_the_swap():
         assert {c[4] for c in rec.calls if c[0] == "swap"} == {bits}
     with pytest.raises(ValueError):
         si.LayerShape(2, 64, codec="mixed")
+
+
+def test_layer_seals_are_queued_in_swap_order():
+    """pipeline_seal: before its swaps, a layer's records are queued for
+    sealing on the host pool part by part in exactly the order (and with the
+    exact mappings) the swaps then consume them, so tickets follow the
+    reference's (group, kind, block) order either way."""
+    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True,
+                             shape=si.LayerShape(8, 128))  # 256-KiB records: pipelined
+    pre = [(c[1], c[2], c[4]) for c in rec.calls if c[0] == "prefetch"]
+    swaps = [(c[2], c[3], c[5]) for c in rec.calls if c[0] == "swap"]
+    assert pre == swaps and len(pre) == 6
+    first_swap = next(i for i, c in enumerate(rec.calls) if c[0] == "swap")
+    last_prefetch = max(i for i, c in enumerate(rec.calls) if c[0] == "prefetch")
+    assert last_prefetch < first_swap
+
+
+def test_small_records_are_sealed_on_demand():
+    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True)  # 32-KiB records
+    assert not [c for c in rec.calls if c[0] == "prefetch"]
