@@ -219,7 +219,8 @@ def cpu_baseline(op: str, wire_host: np.ndarray, stride: int, nbytes: int, nrec:
 
 def ledger_split(path: Path, steps: int) -> dict | None:
     """Mean host seal / H2D copy / kernel microseconds per layer from the
-    library's H2D ledger rows (SECURE_INFER_H2D_PROFILE), by record source."""
+    library's H2D ledger rows (SECURE_INFER_H2D_PROFILE, one row per launch:
+    a causal group's K and V swaps go out as one), by record source."""
     if not path.exists():
         return None
     rows = [l.split(",") for l in path.read_text().strip().splitlines()[1:]]
@@ -228,8 +229,8 @@ def ledger_split(path: Path, steps: int) -> dict | None:
         sel = [r for r in rows if r[4] == src]
         if not sel:
             continue
-        per_layer = len(sel) / max(len({r[0] for r in sel}) * steps, 1)  # causal groups x kinds
-        out[src] = {"swaps": len(sel), "swaps_per_layer": round(per_layer, 2)}
+        per_layer = len(sel) / max(len({r[0] for r in sel}) * steps, 1)  # causal groups
+        out[src] = {"launches": len(sel), "launches_per_layer": round(per_layer, 2)}
         for col, name in ((5, "seal_us"), (6, "h2d_copy_us"), (7, "kernel_us")):
             out[src][name + "_per_layer"] = round(float(np.mean([float(r[col]) for r in sel])) * per_layer, 1)
     return out
@@ -272,9 +273,13 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
         def step(ahead):
             nt.layer = 0
             if ahead:
-                for l in range(L):
-                    nt.prefetch_kv_transfer((hosts[l], mapping_rl[l]), l)
+                queued = [nt.prefetch_kv_transfer((hosts[l], mapping_rl[l]), l) for l in range(L)]
+                if not all(queued):
+                    raise RuntimeError("prefetch budget (SECURE_INFER_PREFETCH_MB) too small for every layer")
+                deadline = time.perf_counter() + 120
                 while int(lib.secure_infer_count_ready_unconsumed_gcm_tickets()) < L * 2 * NB:
+                    if time.perf_counter() > deadline:
+                        raise RuntimeError("prefetched records not sealed within 120 s")
                     time.sleep(0.0005)
             t0 = time.perf_counter()
             for l in range(L):

@@ -143,8 +143,9 @@ typedef struct si_reload_desc {
     uint32_t layer;           /* layer index (codec header, status)            */
     void* staging;            /* device scratch, nrec*align32(bytes) (codec)   */
     uint32_t* fail_count;     /* device u32: += number of failed records; NULL ok */
-    uint32_t* status_out;     /* device, optional: nrec u32, record r's status
-                                 (1 / 0) also at status_out[r]; NULL ok      */
+    uint32_t* status_out;     /* optional: nrec u32, record r's status (1 / 0)
+                                 also at status_out[r]; device memory or
+                                 mapped pinned host memory; NULL ok          */
 } si_reload_desc;
 
 int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* session,
@@ -241,7 +242,13 @@ void secure_infer_get_transfer_prefetch_stats(uint64_t* ready, uint64_t* busy_fa
 /* secure_infer.cpp:5052-5070: records sealed ahead of demand and not yet consumed. */
 uint64_t secure_infer_count_ready_unconsumed_gcm_tickets(void);
 
-/* secure_infer.cpp:5883-5903: layer-group brackets (thread-local). */
+/* secure_infer.cpp:5883-5903: layer-group brackets (thread-local).  `expected`
+ * is the group's record count.  Swaps of the group accumulate and go out as
+ * few launches as their stream, layer and geometry allow (K swaps, then V
+ * swaps, of one stream form one launch; at most SECURE_INFER_H2D_BATCH_MB of
+ * records, default 64), issued at the latest by group_end, as the reference
+ * batches a group's swaps (:5862-5881).  group_end returns -1 if issuing
+ * them failed. */
 int secure_infer_h2d_layer_group_begin(size_t expected);
 int secure_infer_h2d_layer_group_end(void);
 
@@ -288,11 +295,12 @@ int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event,
  * secure_infer.cpp:6486-6550; slot ring :5174-5229, :5905-6059), DMA on the
  * ring's copy stream, then the fused verify + decrypt (+ dequantise) + paged
  * scatter on `stream` once the copy has landed.  Returns when the work is
- * queued; a ring slot is reused only after its kernel (and status copy)
- * completed.  Rings, copy streams and locks are per (device, stream), as the
- * reference keeps them per stream (:5389-5399).  Inside
- * secure_infer_h2d_layer_group_begin/end every record is observed for
- * secure_infer_recovery_wait_layer_authentication.  mapping pairs are (host
+ * queued; a ring slot is reused only after its kernel completed.  Rings,
+ * copy streams and locks are per (device, stream), as the reference keeps
+ * them per stream (:5389-5399).  Inside secure_infer_h2d_layer_group_begin/end
+ * the records are sealed (or taken from a prefetch) by the call, but their
+ * copy and kernel are issued with the group's other swaps (see above), and
+ * every record is observed for secure_infer_recovery_wait_layer_authentication.  mapping pairs are (host
  * block, device slot).  fail_count (device u32, may be NULL): += records
  * that failed in this launch. */
 int secure_infer_h2d_swap(hipStream_t stream, si_session* session, const void* host_base,

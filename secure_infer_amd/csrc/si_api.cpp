@@ -1005,7 +1005,7 @@ int secure_infer_h2d_layer_group_end(void)
 {
     if (t_group_expected < 0) return -1;
     t_group_expected = -1;
-    return 0;
+    return si_internal::flush_pending_h2d() == 0 ? 0 : -1;
 }
 
 int secure_infer_recovery_track_layer(uint32_t layer, hipEvent_t event, const uint32_t* fail_count)
@@ -1117,6 +1117,8 @@ uint64_t reserve_tickets(uint32_t n)
 bool replay_reserve_range(uint64_t t0, uint64_t n) { return replay_insert(t0, t0 + n); }
 
 bool group_open() { return t_group_expected >= 0; }
+
+int64_t group_expected() { return t_group_expected; }
 
 uint64_t current_job_id() { return g_job_id.load(); }
 

@@ -2,18 +2,26 @@
 //
 //  * A worker pool runs OpenSSL AES-128-GCM (EVP, one context per thread) --
 //    the reference's host crypto (inline_h2d_encrypt_commit,
-//    secure_infer.cpp:6486-6550; d2h_host_decrypt_one, :2470-2547).
+//    secure_infer.cpp:6486-6550; d2h_host_decrypt_one, :2470-2547).  Idle
+//    workers poll for work for SECURE_INFER_POOL_SPIN_US (default 200) before
+//    they park.
 //  * H2D: secure_infer_h2d_swap seals host KV blocks into wire records in a
 //    pinned ring slot of the caller's stream, copies the slot to the device
 //    on that ring's copy stream and makes the caller's stream wait for the
 //    copy before the fused verify + decrypt (+ dequant) + paged-scatter
 //    kernel.  The caller returns as soon as the work is queued, so the copy
-//    of layer l+1 overlaps the kernel of layer l.  Rings, their copy streams
-//    and their locks are per (device, caller stream), like the reference's
-//    per-stream pipelines (secure_infer.cpp:5389-5399).
-//  * Observation and strict retry: inside a layer group every record's
-//    status word is copied to pinned host memory once its kernel is done
-//    (observe_recovery_authentication, secure_infer.cpp:5316-5387);
+//    of layer l+1 overlaps the kernel of layer l.  Inside a layer group the
+//    swaps' records accumulate in one ring slot and go out as one copy
+//    sequence and one launch at the group's end (K swaps before V swaps of
+//    one stream), as the reference batches a group's swaps
+//    (secure_infer.cpp:5862-5904): each cross-stream wait and launch costs
+//    the host about 10 us in the HIP runtime.  Rings, their copy streams and
+//    their locks are per (device, caller stream), like the reference's
+//    per-stream pipelines (:5389-5399).
+//  * Observation and strict retry: inside a layer group the kernel also
+//    stores every record's status into mapped pinned host memory, read once
+//    an event after the kernel has completed (observe_recovery_authentication,
+//    secure_infer.cpp:5316-5387);
 //    secure_infer_recovery_wait_layer_authentication re-seals a record that
 //    failed once from the trusted host copy under a fresh ticket and
 //    returns -1 only when that second attempt fails too (:7303-7333).
@@ -76,8 +84,22 @@ public:
         {
             std::lock_guard<std::mutex> g(m_);
             q_.push_back(std::move(f));
+            queued_.fetch_add(1, std::memory_order_release);
         }
         cv_.notify_one();
+    }
+
+    // Queues every task under one lock with one wake-up.
+    void submit_all(std::vector<std::function<void()>>& fs)
+    {
+        if (fs.empty()) return;
+        {
+            std::lock_guard<std::mutex> g(m_);
+            for (auto& f : fs) q_.push_back(std::move(f));
+            queued_.fetch_add(fs.size(), std::memory_order_release);
+        }
+        fs.clear();
+        cv_.notify_all();
     }
 
     // f(i) for every i in [0, n), on the pool and the calling thread.
@@ -100,9 +122,22 @@ public:
                 }
             }
         };
+        // One lock and one wake-up for all helpers: a futex wake per helper
+        // costs the caller more than a 41-KB record's seal.
         const size_t helpers = std::min(threads_.size(), n - 1);
-        for (size_t h = 0; h < helpers; ++h) submit(body);
+        if (helpers) {
+            {
+                std::lock_guard<std::mutex> g(m_);
+                for (size_t h = 0; h < helpers; ++h) q_.push_back(body);
+                queued_.fetch_add(helpers, std::memory_order_release);
+            }
+            if (helpers == 1)
+                cv_.notify_one();
+            else
+                cv_.notify_all();
+        }
         body();
+        spin_until([&] { return sh->done.load(std::memory_order_acquire) == n; });
         std::unique_lock<std::mutex> g(sh->m);
         sh->cv.wait(g, [&] { return sh->done.load() == n; });
     }
@@ -123,18 +158,38 @@ private:
         if (const char* e = std::getenv("SECURE_INFER_HOST_THREADS")) n = unsigned(std::atoi(e));
         if (n == 0) n = 1;
         if (n > 256) n = 256;
+        if (const char* e = std::getenv("SECURE_INFER_POOL_SPIN_US")) spin_us_ = std::max(0, std::atoi(e));
         for (unsigned i = 0; i + 1 < n; ++i) threads_.emplace_back([this] { run(); });
+    }
+
+    // Polls `ready` for up to spin_us_ before the caller blocks: a transfer's
+    // swaps arrive tens of microseconds apart, about what waking a thread
+    // parked on a futex costs, so idle workers (and a caller waiting for its
+    // helpers) poll for a while first.
+    template <class F>
+    void spin_until(F ready) const
+    {
+        if (spin_us_ <= 0 || ready()) return;
+        const auto until = std::chrono::steady_clock::now() + std::chrono::microseconds(spin_us_);
+        for (unsigned i = 1; !ready(); ++i) {
+#if defined(__x86_64__)
+            __builtin_ia32_pause();
+#endif
+            if ((i & 63) == 0 && std::chrono::steady_clock::now() >= until) return;
+        }
     }
 
     void run()
     {
         for (;;) {
+            spin_until([&] { return queued_.load(std::memory_order_acquire) != 0; });
             std::function<void()> f;
             {
                 std::unique_lock<std::mutex> g(m_);
                 cv_.wait(g, [&] { return !q_.empty(); });
                 f = std::move(q_.front());
                 q_.pop_front();
+                queued_.fetch_sub(1, std::memory_order_relaxed);
             }
             f();
         }
@@ -142,6 +197,8 @@ private:
 
     std::vector<std::thread> threads_;
     std::deque<std::function<void()>> q_;
+    std::atomic<size_t> queued_{0};
+    int spin_us_ = 200;
     std::mutex m_;
     std::condition_variable cv_;
 };
@@ -256,11 +313,10 @@ struct Mirror {
     size_t stage_cap = 0;
     hipEvent_t ev_a = nullptr;  // H2D: wire records landed; D2H: records sealed
     hipEvent_t ev_b = nullptr;  // H2D: slot free again; D2H: records in host memory
-    hipEvent_t ev_c = nullptr;  // H2D: the slot's kernel is done
     // ledger (timing events, created when the ledger is on)
     hipEvent_t p_c0 = nullptr, p_c1 = nullptr, p_k0 = nullptr, p_k1 = nullptr;
     ProfileRow row;
-    std::shared_ptr<Prefetch> held;  // prefetched records being copied from
+    std::vector<std::shared_ptr<Prefetch>> held;  // prefetched records being copied from
 
     Mirror() = default;
     Mirror(const Mirror&) = delete;
@@ -273,7 +329,6 @@ struct Mirror {
         if (stage) (void)hipFree(stage);
         if (ev_a) (void)hipEventDestroy(ev_a);
         if (ev_b) (void)hipEventDestroy(ev_b);
-        if (ev_c) (void)hipEventDestroy(ev_c);
         for (hipEvent_t e : {p_c0, p_c1, p_k0, p_k1})
             if (e) (void)hipEventDestroy(e);
     }
@@ -288,8 +343,7 @@ struct Mirror {
     bool init()
     {
         return hipEventCreateWithFlags(&ev_a, hipEventDisableTiming) == hipSuccess &&
-               hipEventCreateWithFlags(&ev_b, hipEventDisableTiming) == hipSuccess &&
-               hipEventCreateWithFlags(&ev_c, hipEventDisableTiming) == hipSuccess;
+               hipEventCreateWithFlags(&ev_b, hipEventDisableTiming) == hipSuccess;
     }
     // Callers guarantee no queued work still uses the buffers.
     bool reserve(size_t need, size_t stage_need)
@@ -317,10 +371,16 @@ struct Mirror {
 };
 
 // Pinned status words of one observed swap and the event after their copy.
+// Per-record statuses of one observed swap: pinned, coherent host memory the
+// reload kernel's finalisers store into directly (`dev` is its device-side
+// address), readable on the host once `ready` (recorded after the kernel)
+// has completed.
 struct StatusBuf {
     uint32_t* host = nullptr;
+    uint32_t* dev = nullptr;
     size_t cap = 0;  // words
     hipEvent_t ready = nullptr;
+    bool orphaned = false;  // a failed launch may still store into it: never reused
     ~StatusBuf()
     {
         if (host) (void)hipHostFree(host);
@@ -328,14 +388,14 @@ struct StatusBuf {
     }
 };
 
-// The reload ring of one caller stream: slots, their cursor and lock, the
-// copy stream of its H2D records and the stream of its status copies.
+// The reload ring of one caller stream: slots, their cursor and lock, and
+// the copy stream of its H2D records.
 struct StreamRing {
     std::mutex lock;
     hipStream_t copy = nullptr;
-    hipStream_t observe = nullptr;
     std::vector<std::unique_ptr<Mirror>> slots;
-    std::vector<bool> used;
+    std::vector<bool> used;  // a launch was issued from the slot (wait for its ev_b)
+    std::vector<bool> busy;  // a pending launch is filling the slot
     size_t next = 0;
 };
 
@@ -379,11 +439,9 @@ StreamRing* ring_of(DeviceState* ds, hipStream_t stream)
     auto& r = ds->rings[stream];
     if (!r) {
         auto nr = std::make_unique<StreamRing>();
-        if (hipStreamCreateWithFlags(&nr->copy, hipStreamNonBlocking) != hipSuccess ||
-            hipStreamCreateWithFlags(&nr->observe, hipStreamNonBlocking) != hipSuccess)
-            return nullptr;
+        if (hipStreamCreateWithFlags(&nr->copy, hipStreamNonBlocking) != hipSuccess) return nullptr;
         // Slots per stream: a layer of 16-block causal groups is 6 swaps, and
-        // a slot is reused only after its kernel and status copy are done
+        // a slot is reused only after its kernel is done
         // (the reference's default budget is 32 single-record slots,
         // secure_infer.cpp:5608-5647).
         size_t slots = 16;
@@ -393,12 +451,16 @@ StreamRing* ring_of(DeviceState* ds, hipStream_t stream)
             if (!mbuf->init()) return nullptr;
             nr->slots.push_back(std::move(mbuf));
             nr->used.push_back(false);
+            nr->busy.push_back(false);
         }
         r = std::move(nr);
     }
     return r.get();
 }
 
+// A status buffer of at least `words` entries, all 0 (failed) until the
+// kernel stores each record's result.  Buffers come back to the free list
+// only after their `ready` event has completed, so no kernel still writes them.
 std::unique_ptr<StatusBuf> take_status(DeviceState* ds, size_t words)
 {
     {
@@ -407,14 +469,17 @@ std::unique_ptr<StatusBuf> take_status(DeviceState* ds, size_t words)
             if (ds->free_status[i]->cap >= words) {
                 auto b = std::move(ds->free_status[i]);
                 ds->free_status.erase(ds->free_status.begin() + long(i));
+                memset(b->host, 0, words * 4);
                 return b;
             }
     }
     auto b = std::make_unique<StatusBuf>();
     const size_t cap = std::max<size_t>(1024, (words + 1023) / 1024 * 1024);
     if (hipHostMalloc(reinterpret_cast<void**>(&b->host), cap * 4, hipHostMallocDefault) != hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void**>(&b->dev), b->host, 0) != hipSuccess ||
         hipEventCreateWithFlags(&b->ready, hipEventDisableTiming) != hipSuccess)
         return nullptr;
+    memset(b->host, 0, cap * 4);
     b->cap = cap;
     return b;
 }
@@ -518,10 +583,10 @@ void profile_sweep(bool wait)
 
 // ---------------------------------------------------------------- ahead-of-demand sealing
 
-// A swap's records sealed before the swap is issued: [n wire records][n slot
-// ids], laid out exactly as a ring slot, in pinned memory.  It serves the
-// secure_infer_h2d_swap with the same session, host pool, kind, layer,
-// codec and host-block column of the mapping.
+// A swap's records sealed before the swap is issued: n wire records laid out
+// as in a ring slot, in pinned memory, copied from there by the swap.  It
+// serves the secure_infer_h2d_swap with the same session, host pool, kind,
+// layer, codec and host-block column of the mapping.
 struct Prefetch {
     si_session* session = nullptr;
     si_internal::SessionKeys keys{};
@@ -565,8 +630,13 @@ Prefetch::~Prefetch()
     g_pf_free.emplace_back(host, cap);
 }
 
+// A pinned buffer of at least `need` bytes: the smallest free one that fits,
+// else a new one within the budget, after freeing free buffers too small to
+// serve (none of them is read by a queued copy any more).
 uint8_t* take_pf_buffer(size_t need, size_t& cap)
 {
+    std::vector<uint8_t*> drop;
+    bool fits = true;
     {
         std::lock_guard<std::mutex> g(g_pf_lock);
         size_t best = g_pf_free.size();
@@ -579,9 +649,16 @@ uint8_t* take_pf_buffer(size_t need, size_t& cap)
             g_pf_free.erase(g_pf_free.begin() + long(best));
             return p;
         }
-        if (g_pf_bytes + need > prefetch_budget()) return nullptr;
-        g_pf_bytes += need;
+        while (g_pf_bytes + need > prefetch_budget() && !g_pf_free.empty()) {
+            drop.push_back(g_pf_free.back().first);
+            g_pf_bytes -= g_pf_free.back().second;
+            g_pf_free.pop_back();
+        }
+        fits = g_pf_bytes + need <= prefetch_budget();
+        if (fits) g_pf_bytes += need;
     }
+    for (uint8_t* p : drop) (void)hipHostFree(p);
+    if (!fits) return nullptr;
     uint8_t* p = nullptr;
     if (hipHostMalloc(reinterpret_cast<void**>(&p), need, hipHostMallocDefault) != hipSuccess) {
         std::lock_guard<std::mutex> g(g_pf_lock);
@@ -624,8 +701,23 @@ void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint6
 
 // ---------------------------------------------------------------- observed reloads
 
+// Statuses shared by the swaps of one launch.  The buffer returns to its
+// device's free list when the last swap lets go of it -- after its `ready`
+// event completed -- unless a launch failed part-way and a kernel may still
+// store into it (then it is never reused).
+using StatusRef = std::shared_ptr<StatusBuf>;
+
+StatusRef share_status(DeviceState* ds, std::unique_ptr<StatusBuf> b)
+{
+    if (!b) return nullptr;
+    return StatusRef(b.release(), [ds](StatusBuf* p) {
+        if (p->orphaned) return;
+        give_status(ds, std::unique_ptr<StatusBuf>(p));
+    });
+}
+
 // One observed swap: where each record came from and went to (for a strict
-// retry from the trusted host copy) and its status words.
+// retry from the trusted host copy) and where its statuses are.
 struct Observed {
     DeviceState* ds = nullptr;
     si_session* session = nullptr;
@@ -637,7 +729,9 @@ struct Observed {
     hipStream_t stream = nullptr;
     uint64_t job_id = 0;
     std::vector<int64_t> mapping;  // n (host block, device slot) pairs
-    std::unique_ptr<StatusBuf> status;
+    StatusRef status;
+    uint32_t status_off = 0;       // the swap's first record among the launch's statuses
+    uint32_t status_of(uint32_t r) const { return status->host[status_off + r]; }
 };
 
 std::mutex g_obs_lock;
@@ -666,10 +760,203 @@ double us_since(std::chrono::steady_clock::time_point t0)
     return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
 }
 
+// One swap's records within a launch.
+struct H2DPart {
+    const uint8_t* src = nullptr;  // its sealed records: ring slot rows or a prefetch buffer
+    uint32_t r0 = 0, n = 0;        // rows [r0, r0 + n) of the launch
+    uint64_t t0 = 0;               // ticket of its first record
+    uint32_t source = 0;           // 0 sealed on demand, 1 prefetched, 2 prefetch waited for
+    double seal_us = 0;
+    std::shared_ptr<Prefetch> pf;
+    std::shared_ptr<Observed> ob;  // null when not observed
+};
+
+// The records of consecutive swaps that go to the device as one copy
+// sequence and one reload launch: K swaps before V swaps, all of one stream,
+// session, layer and geometry, in one ring slot laid out as
+// [cap wire records][iv words, n x 16][slot ids, n x 8].  Inside a layer
+// group the swaps accumulate until the group ends (or the next swap does not
+// fit), as the reference batches a group's swaps
+// (enqueue_h2d_gcm_batch_task, flushed by secure_infer_h2d_layer_group_end,
+// secure_infer.cpp:5862-5904); outside a group every swap is a launch of
+// its own.
+struct H2DLaunch {
+    hipStream_t stream = nullptr;
+    si_session* s = nullptr;
+    si_internal::SessionKeys keys{};
+    DeviceState* ds = nullptr;
+    StreamRing* ring = nullptr;
+    size_t slot = 0;
+    uint32_t layer = 0, codec = 0, heads = 0, dim = 0;
+    uint64_t bytes = 0, stride = 0, tag_off = 0, slot_bytes = 0, nslots = 0;
+    void* cache[2] = {nullptr, nullptr};
+    uint32_t* fail_count = nullptr;
+    bool observe = false;
+    uint32_t cap = 0, n = 0, n_k = 0;
+    std::vector<int64_t> slot_ids;
+    std::vector<H2DPart> parts;
+    StatusRef status;
+};
+
+thread_local std::unique_ptr<H2DLaunch> t_launch;
+
+// Largest pending launch in wire bytes (SECURE_INFER_H2D_BATCH_MB, default 64):
+// ring slots are sized to the launches they carry.
+uint64_t launch_byte_cap()
+{
+    static const uint64_t b = [] {
+        uint64_t mb = 64;
+        if (const char* e = std::getenv("SECURE_INFER_H2D_BATCH_MB")) mb = uint64_t(std::max(1, std::atoi(e)));
+        return mb << 20;
+    }();
+    return b;
+}
+
+// A free slot of the ring, waited for if its previous launch is still
+// running; nullptr if every slot is held by a launch not yet issued.
+Mirror* claim_slot(StreamRing* ring, size_t& idx)
+{
+    std::lock_guard<std::mutex> g(ring->lock);
+    for (size_t k = 0; k < ring->slots.size(); ++k) {
+        const size_t i = ring->next;
+        ring->next = (ring->next + 1) % ring->slots.size();
+        if (ring->busy[i]) continue;
+        Mirror& sl = *ring->slots[i];
+        if (ring->used[i]) {
+            if (hipEventSynchronize(sl.ev_b) != hipSuccess) return nullptr;
+            profile_retire(sl);
+            sl.held.clear();  // the copies from prefetch buffers are complete
+            ring->used[i] = false;
+        }
+        ring->busy[i] = true;
+        idx = i;
+        return &sl;
+    }
+    return nullptr;
+}
+
+void release_slot(StreamRing* ring, size_t idx, bool launched)
+{
+    std::lock_guard<std::mutex> g(ring->lock);
+    ring->busy[idx] = false;
+    ring->used[idx] = launched;
+}
+
+// Issues the calling thread's pending launch: copies on the ring's copy
+// stream, the caller's stream waits for them, then the fused reload.
+int flush_launch()
+{
+    std::unique_ptr<H2DLaunch> L = std::move(t_launch);
+    if (!L) return 0;
+    if (L->n == 0) {  // its only swap failed before adding records
+        release_slot(L->ring, L->slot, false);
+        return 0;
+    }
+    Mirror& sl = *L->ring->slots[L->slot];
+    const bool prof = profile_on();
+    const size_t wire_cap = size_t(L->cap) * L->stride;
+    bool contiguous = true;  // tickets t0 .. t0 + n - 1 in record order
+    for (size_t i = 1; i < L->parts.size(); ++i)
+        contiguous = contiguous && L->parts[i].t0 == L->parts[i - 1].t0 + L->parts[i - 1].n;
+    const size_t iv_bytes = contiguous ? 0 : size_t(L->n) * 16;
+    uint8_t* tail = sl.host + wire_cap;
+    if (!contiguous) {
+        uint32_t* w = reinterpret_cast<uint32_t*>(tail);
+        const uint32_t salt = (uint32_t(L->keys.salt[0]) << 24) | (uint32_t(L->keys.salt[1]) << 16) |
+                              (uint32_t(L->keys.salt[2]) << 8) | uint32_t(L->keys.salt[3]);
+        for (const H2DPart& p : L->parts)
+            for (uint32_t r = 0; r < p.n; ++r) {
+                const uint64_t c = L->keys.nonce + p.t0 + r;
+                uint32_t* o = w + 4 * size_t(p.r0 + r);
+                o[0] = salt;
+                o[1] = uint32_t(c >> 32);
+                o[2] = uint32_t(c);
+                o[3] = 2;
+            }
+    }
+    memcpy(tail + iv_bytes, L->slot_ids.data(), size_t(L->n) * 8);
+
+    bool launched = false;
+    // On failure nothing is registered; copies still queued are waited for
+    // before the prefetch buffers they read from are let go, and the status
+    // buffer is never reused (the kernel may have been queued).
+    auto fail = [&]() {
+        if (L->status) L->status->orphaned = true;
+        (void)hipStreamSynchronize(L->ring->copy);
+        if (launched) (void)hipStreamSynchronize(L->stream);
+        release_slot(L->ring, L->slot, false);
+        return -1;
+    };
+    if (prof && hipEventRecord(sl.p_c0, L->ring->copy) != hipSuccess) return fail();
+    // One copy per run of parts whose sealed records sit back to back.
+    for (size_t i = 0; i < L->parts.size();) {
+        const uint8_t* src = L->parts[i].src;
+        const uint32_t r0 = L->parts[i].r0;
+        uint32_t rows = L->parts[i].n;
+        size_t j = i + 1;
+        for (; j < L->parts.size() && L->parts[j].src == src + size_t(rows) * L->stride; ++j) rows += L->parts[j].n;
+        if (hipMemcpyAsync(sl.dev + size_t(r0) * L->stride, src, size_t(rows) * L->stride, hipMemcpyHostToDevice,
+                           L->ring->copy) != hipSuccess)
+            return fail();
+        i = j;
+    }
+    if (hipMemcpyAsync(sl.dev + wire_cap, tail, iv_bytes + size_t(L->n) * 8, hipMemcpyHostToDevice,
+                       L->ring->copy) != hipSuccess ||
+        (prof && hipEventRecord(sl.p_c1, L->ring->copy) != hipSuccess) ||
+        hipEventRecord(sl.ev_a, L->ring->copy) != hipSuccess || hipStreamWaitEvent(L->stream, sl.ev_a, 0) != hipSuccess)
+        return fail();
+
+    si_reload_desc d{};
+    d.wire = sl.dev;
+    d.wire_stride = L->stride;
+    d.bytes = L->bytes;
+    d.nrec = L->n;
+    d.n_k = L->n_k;
+    d.iv_words = contiguous ? nullptr : reinterpret_cast<const uint32_t*>(sl.dev + wire_cap);
+    d.ticket_base = contiguous ? L->parts[0].t0 : 0;
+    d.cache_k = L->cache[0] ? L->cache[0] : L->cache[1];
+    d.cache_v = L->cache[1] ? L->cache[1] : L->cache[0];
+    d.slot_bytes = L->slot_bytes;
+    d.nslots = L->nslots;
+    d.slots = reinterpret_cast<const int64_t*>(sl.dev + wire_cap + iv_bytes);
+    d.codec_bits = L->codec;
+    d.heads = L->heads;
+    d.head_dim = L->dim;
+    d.layer = L->layer;
+    d.staging = sl.stage;
+    d.fail_count = L->fail_count;
+    d.status_out = L->status ? L->status->dev : nullptr;
+    if (prof && hipEventRecord(sl.p_k0, L->stream) != hipSuccess) return fail();
+    if (secure_infer_gpu_reload_layer(L->stream, L->s, &d) != 0) return fail();
+    launched = true;
+    if ((prof && hipEventRecord(sl.p_k1, L->stream) != hipSuccess) ||
+        hipEventRecord(sl.ev_b, L->stream) != hipSuccess ||
+        (L->status && hipEventRecord(L->status->ready, L->stream) != hipSuccess))
+        return fail();
+    for (H2DPart& p : L->parts)
+        if (p.pf) sl.held.push_back(std::move(p.pf));
+    if (prof) {
+        sl.row.pending = true;
+        sl.row.layer = L->layer;
+        sl.row.kind = L->n_k == L->n ? 0u : (L->n_k == 0 ? 1u : 2u);
+        sl.row.n = L->n;
+        sl.row.bytes = L->bytes;
+        sl.row.source = L->parts[0].source;
+        sl.row.seal_us = 0;
+        for (const H2DPart& p : L->parts) sl.row.seal_us += p.seal_us;
+    }
+    release_slot(L->ring, L->slot, true);
+    if (L->observe) {
+        std::lock_guard<std::mutex> go(g_obs_lock);
+        for (H2DPart& p : L->parts) g_observed.emplace(L->layer, std::move(p.ob));
+    }
+    return 0;
+}
+
 int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint64_t host_block_bytes,
                   uint64_t host_nblocks, void* dev_cache, uint64_t slot_bytes, uint64_t nslots,
                   const int64_t* mapping, uint32_t n, uint32_t kind, uint32_t layer, uint32_t codec_bits,
-                  uint32_t heads, uint32_t head_dim, uint32_t* fail_count, bool observe)
+                  uint32_t heads, uint32_t head_dim, uint32_t* fail_count, bool observe, bool defer)
 {
     if (!s || !host_base || !dev_cache || !mapping || n == 0 || kind > 1 || nslots == 0 || host_nblocks == 0)
         return -1;
@@ -684,13 +971,17 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     if (!ring) return -1;
     const uint64_t stride = secure_infer_wire_stride(bytes);
     const uint64_t tag_off = tag_offset(bytes);
-    // [wire records][slot ids, n x 8] travel; [statuses, n x 4] come back
-    const size_t wire = size_t(n) * stride;
-    const size_t need = wire + size_t(n) * 8;
-    const bool prof = profile_on();
 
-    std::unique_ptr<StatusBuf> status;
-    if (observe && !(status = take_status(ds, n))) return -1;
+    // Joins the pending launch if it takes these records, else issues that first.
+    H2DLaunch* L = t_launch.get();
+    if (L && !(L->stream == stream && L->s == s && L->ds == ds && L->layer == layer && L->codec == codec_bits &&
+               L->heads == heads && L->dim == head_dim && L->bytes == bytes && L->slot_bytes == slot_bytes &&
+               L->nslots == nslots && L->fail_count == fail_count && L->observe == observe &&
+               (L->cache[kind] == nullptr || L->cache[kind] == dev_cache) && !(kind == 0 && L->n > L->n_k) &&
+               L->n + n <= L->cap)) {
+        if (flush_launch() != 0) return -1;
+        L = nullptr;
+    }
 
     // Records sealed ahead of demand for exactly this swap, if any.
     std::shared_ptr<Prefetch> pf = take_prefetch(s, host_base, host_block_bytes, mapping, n, kind, layer, codec_bits);
@@ -705,121 +996,108 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
         g_pf_missing.fetch_add(1);
     }
 
-    std::lock_guard<std::mutex> g(ring->lock);
-    const size_t si = ring->next;
-    ring->next = (ring->next + 1) % ring->slots.size();
-    Mirror& sl = *ring->slots[si];
-    if (ring->used[si]) {
-        if (hipEventSynchronize(sl.ev_b) != hipSuccess) return -1;
-        profile_retire(sl);
-        sl.held.reset();  // the copy from a prefetch buffer is complete
-    }
-    if (!sl.reserve(need + size_t(n) * 4, codec_bits ? size_t(n) * tag_off : 0)) return -1;
-    if (prof && !sl.init_profile()) return -1;
-
-    // Host side: seal on demand into the ring slot, or take the prefetched
-    // records (their slot-id tail is written now).
-    uint8_t* src_host = sl.host;
-    uint64_t t0 = 0;
-    double seal_us = 0;
-    if (pf) {
-        t0 = pf->t0;
-        src_host = pf->host;
-        seal_us = pf->seal_us;
-    } else {
-        const auto ts = std::chrono::steady_clock::now();
-        t0 = si_internal::reserve_tickets(n);
-        if (!si_internal::replay_reserve_range(t0, n)) {
-            fprintf(stderr, "[secure_infer] duplicate H2D transfer tickets rejected at %llu\n",
-                    static_cast<unsigned long long>(t0));
+    if (!L) {
+        auto nl = std::make_unique<H2DLaunch>();
+        uint64_t cap = n;
+        if (defer) {
+            const int64_t expected = si_internal::group_expected();
+            const uint64_t fit = std::max<uint64_t>(1, launch_byte_cap() / stride);
+            cap = std::max<uint64_t>(n, std::min<uint64_t>(expected > 0 ? uint64_t(expected) : 0, fit));
+        }
+        nl->cap = uint32_t(std::min<uint64_t>(cap, UINT32_MAX / 2));
+        if (nl->cap < n) return -1;
+        Mirror* sl = claim_slot(ring, nl->slot);
+        if (!sl) return -1;
+        nl->ring = ring;
+        if (!sl->reserve(size_t(nl->cap) * (stride + 24), codec_bits ? size_t(nl->cap) * tag_off : 0) ||
+            (profile_on() && !sl->init_profile())) {
+            release_slot(ring, nl->slot, false);
             return -1;
         }
+        if (observe && !(nl->status = share_status(ds, take_status(ds, nl->cap)))) {
+            release_slot(ring, nl->slot, false);
+            return -1;
+        }
+        nl->stream = stream;
+        nl->s = s;
+        nl->keys = keys;
+        nl->ds = ds;
+        nl->layer = layer;
+        nl->codec = codec_bits;
+        nl->heads = heads;
+        nl->dim = head_dim;
+        nl->bytes = bytes;
+        nl->stride = stride;
+        nl->tag_off = tag_off;
+        nl->slot_bytes = slot_bytes;
+        nl->nslots = nslots;
+        nl->fail_count = fail_count;
+        nl->observe = observe;
+        t_launch = std::move(nl);
+        L = t_launch.get();
+    }
+
+    // Host side: seal on demand into the slot's rows, or take the prefetched records.
+    Mirror& sl = *ring->slots[L->slot];
+    H2DPart part;
+    part.r0 = L->n;
+    part.n = n;
+    part.source = source;
+    if (pf) {
+        part.src = pf->host;
+        part.t0 = pf->t0;
+        part.seal_us = pf->seal_us;
+        part.pf = pf;
+    } else {
+        const auto ts = std::chrono::steady_clock::now();
+        part.t0 = si_internal::reserve_tickets(n);
+        if (!si_internal::replay_reserve_range(part.t0, n)) {
+            fprintf(stderr, "[secure_infer] duplicate H2D transfer tickets rejected at %llu\n",
+                    static_cast<unsigned long long>(part.t0));
+            return -1;
+        }
+        uint8_t* rows = sl.host + size_t(part.r0) * stride;
+        const uint64_t t0 = part.t0;
         std::atomic<int> bad{0};
         Pool::get().parallel_for(n, [&](size_t r) {
             const int64_t hb = mapping[2 * r];
             bool ok = true;
             seal_record(keys, static_cast<const uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes, bytes,
-                        tag_off, t0 + r, sl.host + r * stride, layer, kind, hb, ok);
+                        tag_off, t0 + r, rows + r * stride, layer, kind, hb, ok);
             if (!ok) bad.store(1);
         });
         if (bad.load()) return -1;
-        seal_us = us_since(ts);
+        part.src = rows;
+        part.seal_us = us_since(ts);
     }
-    int64_t* slot_ids = reinterpret_cast<int64_t*>(src_host + wire);
-    for (uint32_t r = 0; r < n; ++r) slot_ids[r] = mapping[2 * r + 1];
-
-    if ((prof && hipEventRecord(sl.p_c0, ring->copy) != hipSuccess) ||
-        hipMemcpyAsync(sl.dev, src_host, need, hipMemcpyHostToDevice, ring->copy) != hipSuccess ||
-        (prof && hipEventRecord(sl.p_c1, ring->copy) != hipSuccess) ||
-        hipEventRecord(sl.ev_a, ring->copy) != hipSuccess || hipStreamWaitEvent(stream, sl.ev_a, 0) != hipSuccess)
-        return -1;
-    sl.held = pf;
-    si_reload_desc d{};
-    d.wire = sl.dev;
-    d.wire_stride = stride;
-    d.bytes = bytes;
-    d.nrec = n;
-    d.n_k = kind == 0 ? n : 0;
-    d.iv_words = nullptr;
-    d.ticket_base = t0;
-    d.cache_k = dev_cache;
-    d.cache_v = dev_cache;
-    d.slot_bytes = slot_bytes;
-    d.nslots = nslots;
-    d.slots = reinterpret_cast<const int64_t*>(sl.dev + wire);
-    d.codec_bits = codec_bits;
-    d.heads = heads;
-    d.head_dim = head_dim;
-    d.layer = layer;
-    d.staging = sl.stage;
-    d.fail_count = fail_count;
-    d.status_out = observe ? reinterpret_cast<uint32_t*>(sl.dev + need) : nullptr;
-    if (prof && hipEventRecord(sl.p_k0, stream) != hipSuccess) return -1;
-    if (secure_infer_gpu_reload_layer(stream, s, &d) != 0) return -1;
-    if (prof && hipEventRecord(sl.p_k1, stream) != hipSuccess) return -1;
-    ring->used[si] = true;
-    if (hipEventRecord(sl.ev_b, stream) != hipSuccess) return -1;
-    if (prof) {
-        sl.row.pending = true;
-        sl.row.layer = layer;
-        sl.row.kind = kind;
-        sl.row.n = n;
-        sl.row.bytes = bytes;
-        sl.row.source = source;
-        sl.row.seal_us = seal_us;
+    if (observe) {
+        auto ob = std::make_shared<Observed>();
+        ob->ds = ds;
+        ob->session = s;
+        ob->host_base = static_cast<const uint8_t*>(host_base);
+        ob->host_block_bytes = host_block_bytes;
+        ob->host_nblocks = host_nblocks;
+        ob->dev_cache = dev_cache;
+        ob->slot_bytes = slot_bytes;
+        ob->nslots = nslots;
+        ob->kind = kind;
+        ob->layer = layer;
+        ob->codec = codec_bits;
+        ob->heads = heads;
+        ob->dim = head_dim;
+        ob->stream = stream;
+        ob->job_id = si_internal::current_job_id();
+        ob->mapping.assign(mapping, mapping + 2 * size_t(n));
+        ob->status = L->status;
+        ob->status_off = part.r0;
+        part.ob = std::move(ob);
     }
-    if (!observe) return 0;
-
-    // Status words to pinned memory once the kernel is done; the slot is free
-    // again after that copy.
-    if (hipEventRecord(sl.ev_c, stream) != hipSuccess ||
-        hipStreamWaitEvent(ring->observe, sl.ev_c, 0) != hipSuccess ||
-        hipMemcpyAsync(status->host, sl.dev + need, size_t(n) * 4, hipMemcpyDeviceToHost, ring->observe) !=
-            hipSuccess ||
-        hipEventRecord(status->ready, ring->observe) != hipSuccess ||
-        hipEventRecord(sl.ev_b, ring->observe) != hipSuccess)
-        return -1;
-    auto ob = std::make_shared<Observed>();
-    ob->ds = ds;
-    ob->session = s;
-    ob->host_base = static_cast<const uint8_t*>(host_base);
-    ob->host_block_bytes = host_block_bytes;
-    ob->host_nblocks = host_nblocks;
-    ob->dev_cache = dev_cache;
-    ob->slot_bytes = slot_bytes;
-    ob->nslots = nslots;
-    ob->kind = kind;
-    ob->layer = layer;
-    ob->codec = codec_bits;
-    ob->heads = heads;
-    ob->dim = head_dim;
-    ob->stream = stream;
-    ob->job_id = si_internal::current_job_id();
-    ob->mapping.assign(mapping, mapping + 2 * size_t(n));
-    ob->status = std::move(status);
-    std::lock_guard<std::mutex> go(g_obs_lock);
-    g_observed.emplace(layer, std::move(ob));
-    return 0;
+    for (uint32_t r = 0; r < n; ++r) L->slot_ids.push_back(mapping[2 * r + 1]);
+    L->cache[kind] = dev_cache;
+    L->n += n;
+    if (kind == 0) L->n_k += n;
+    L->parts.push_back(std::move(part));
+    return defer ? 0 : flush_launch();
 }
 
 // ---------------------------------------------------------------- D2H batches
@@ -903,9 +1181,12 @@ void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
 
 namespace si_internal {
 
+int flush_pending_h2d() { return flush_launch(); }
+
 int wait_observed_layer(uint32_t layer, bool* found)
 {
     *found = false;
+    if (flush_launch() != 0) return -1;
     for (unsigned round = 0;; ++round) {
         std::vector<std::shared_ptr<Observed>> recs;
         {
@@ -926,7 +1207,7 @@ int wait_observed_layer(uint32_t layer, bool* found)
                 continue;
             }
             for (uint32_t r = 0; r < n; ++r) {
-                const uint32_t st = ob->status->host[r];
+                const uint32_t st = ob->status_of(r);
                 if (st == 1u) continue;
                 if (st != 0u || round != 0) rc = -1;
                 else retry.emplace_back(ob.get(), r);
@@ -952,13 +1233,13 @@ int wait_observed_layer(uint32_t layer, bool* found)
                 }
                 if (h2d_swap_impl(ob->stream, ob->session, ob->host_base, ob->host_block_bytes,
                                   ob->host_nblocks, ob->dev_cache, ob->slot_bytes, ob->nslots, part.data(), m,
-                                  ob->kind, ob->layer, ob->codec, ob->heads, ob->dim, nullptr, true) != 0 ||
+                                  ob->kind, ob->layer, ob->codec, ob->heads, ob->dim, nullptr, true, false) != 0 ||
                     hipStreamSynchronize(ob->stream) != hipSuccess)
                     rc = -1;
                 (void)hipSetDevice(cur);
             }
         }
-        for (auto& ob : recs) give_status(ob->ds, std::move(ob->status));
+        recs.clear();
         if (rc != 0) {
             // Drop the retries' own observations too: the layer has failed.
             std::lock_guard<std::mutex> g(g_obs_lock);
@@ -966,10 +1247,7 @@ int wait_observed_layer(uint32_t layer, bool* found)
             std::vector<std::shared_ptr<Observed>> rest;
             for (auto it = range.first; it != range.second; ++it) rest.push_back(it->second);
             g_observed.erase(range.first, range.second);
-            for (auto& ob : rest) {
-                (void)hipEventSynchronize(ob->status->ready);
-                give_status(ob->ds, std::move(ob->status));
-            }
+            for (auto& ob : rest) (void)hipEventSynchronize(ob->status->ready);
             return -1;
         }
         if (retry.empty()) return 0;
@@ -978,6 +1256,7 @@ int wait_observed_layer(uint32_t layer, bool* found)
 
 int wait_observed_job(uint64_t job_id, bool* found)
 {
+    if (flush_launch() != 0) return 0;
     std::vector<std::shared_ptr<Observed>> recs;
     {
         std::lock_guard<std::mutex> g(g_obs_lock);
@@ -998,9 +1277,8 @@ int wait_observed_job(uint64_t job_id, bool* found)
         if (hipEventSynchronize(ob->status->ready) != hipSuccess) {
             valid = false;
         } else {
-            for (uint32_t r = 0; r < n; ++r) valid = valid && ob->status->host[r] == 1u;
+            for (uint32_t r = 0; r < n; ++r) valid = valid && ob->status_of(r) == 1u;
         }
-        give_status(ob->ds, std::move(ob->status));
     }
     return valid ? 1 : 0;
 }
@@ -1019,7 +1297,7 @@ int secure_infer_h2d_swap(hipStream_t stream, si_session* s, const void* host_ba
 {
     return h2d_swap_impl(stream, s, host_base, host_block_bytes, host_nblocks, dev_cache, slot_bytes, nslots,
                          mapping, n, kind, layer, codec_bits, heads, head_dim, fail_count,
-                         si_internal::group_open());
+                         si_internal::group_open(), si_internal::group_open());
 }
 
 int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t host_block_bytes, uint64_t host_nblocks,
@@ -1048,7 +1326,7 @@ int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t hos
     pf->tag_off = tag_offset(bytes);
     pf->host_blocks.resize(n);
     for (uint32_t r = 0; r < n; ++r) pf->host_blocks[r] = mapping[2 * r];
-    const size_t need = size_t(n) * pf->stride + size_t(n) * 8;
+    const size_t need = size_t(n) * pf->stride;
     pf->host = take_pf_buffer(need, pf->cap);
     if (!pf->host) return -1;  // over SECURE_INFER_PREFETCH_MB: the swap seals on demand
     pf->t0 = si_internal::reserve_tickets(n);
@@ -1059,9 +1337,11 @@ int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t hos
         std::lock_guard<std::mutex> g(g_pf_lock);
         g_prefetch.push_back(pf);
     }
+    std::vector<std::function<void()>> tasks;
+    tasks.reserve(pf->tasks);
     for (uint32_t r0 = 0; r0 < n; r0 += per_task) {
         const uint32_t r1 = std::min(n, r0 + per_task);
-        Pool::get().submit([pf, r0, r1] {
+        tasks.emplace_back([pf, r0, r1] {
             {
                 std::lock_guard<std::mutex> g(pf->m);
                 if (!pf->started) {
@@ -1083,6 +1363,7 @@ int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t hos
             }
         });
     }
+    Pool::get().submit_all(tasks);
     return 0;
 }
 
@@ -1252,17 +1533,19 @@ int secure_infer_d2h_group_end(void)
     if (!b || !b->group_open) return 0;
     b->group_open = false;
     const uint32_t per_task = 4;
+    std::vector<std::function<void()>> tasks;
     for (size_t j = b->group_first; j < b->jobs.size(); ++j) {
         D2HJob* job = b->jobs[j].get();
         for (uint32_t r0 = 0; r0 < job->n; r0 += per_task) {
             const uint32_t r1 = std::min(job->n, r0 + per_task);
-            {
-                std::lock_guard<std::mutex> g(b->m);
-                ++b->pending;
-            }
-            Pool::get().submit([b, job, r0, r1] { verify_records(b, job, r0, r1); });
+            tasks.emplace_back([b, job, r0, r1] { verify_records(b, job, r0, r1); });
         }
     }
+    {
+        std::lock_guard<std::mutex> g(b->m);
+        b->pending += tasks.size();
+    }
+    Pool::get().submit_all(tasks);
     return 0;
 }
 

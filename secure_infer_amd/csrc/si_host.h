@@ -28,6 +28,13 @@ bool replay_reserve_range(uint64_t t0, uint64_t n);
 // True while the calling thread is inside secure_infer_h2d_layer_group_begin/end.
 bool group_open();
 
+// The record count the calling thread's open layer group announced (-1: none).
+int64_t group_expected();
+
+// Issues the H2D swaps the calling thread's layer group has accumulated
+// (copies, then one reload launch); 0 on success.
+int flush_pending_h2d();
+
 // The job id set by secure_infer_recovery_set_job_id.
 uint64_t current_job_id();
 

@@ -62,7 +62,8 @@ struct Sched {
     uint4* park;         // pairs: each thread's segment-0 product during segment 1
                          // (one uint4 per thread of each workgroup)
     uint32_t* status_out;  // layer form, optional: record r's status also at
-                           // status_out[r] (one contiguous array to copy back)
+                           // status_out[r] (one contiguous array, device or
+                           // mapped pinned host memory)
 };
 // Scratch of the allocation-free reload (secure_infer_gpu_reload_layer_noalloc):
 // one device array per GPU, [accumulators of up to SI_NOALLOC_MAX_RECORDS

@@ -386,15 +386,15 @@ class NativeTransfer:
       the reload.
     * Each (kind, slice) is sealed on the host (OpenSSL, worker pool), copied
       through the slice stream's pinned ring and verified / decrypted /
-      scattered on the device; the call returns once the work is queued.
-      With ``pipeline_seal`` the layer's seals are queued on the worker pool
-      first, so later parts seal while earlier parts are copied (the
-      reference's CPU ciphertext prefetch, secure_infer.cpp:3264-3710); by
-      default ("auto") only for records of at least PIPELINE_MIN_RECORD_BYTES,
-      where a record's seal outweighs the queueing (MI355X box, 16 host
-      CPUs: bf16 Llama-3-8B layer 1229 -> 707 us end to end; 41-KB int4
-      records 812 -> 1146 us, so off for them).  A layer already sealed with
-      ``prefetch_kv_transfer`` is not sealed again.
+      scattered on the device; a group's K and V swaps of one stream go out
+      as one copy sequence and one launch at the group's end.  The call
+      returns once the work is queued.  With ``pipeline_seal`` (default) the
+      layer's seals are queued on the worker pool first, so later parts seal
+      while earlier parts are copied (the reference's CPU ciphertext
+      prefetch, secure_infer.cpp:3264-3710; MI355X box, 16 host CPUs, groups
+      of 16 blocks: 41-KB int4 records 545 -> 406 us per 28-layer-model layer
+      end to end, 256-KB bf16 records 831 -> 553 us).  A layer already sealed
+      with ``prefetch_kv_transfer`` is not sealed again.
       ``wait_layer`` returns the layer's authentication result after at most
       one strict retry per failed record (wait_for_layer_load,
       connector.py:378-410; secure_infer.cpp:7303-7333).
@@ -405,10 +405,8 @@ class NativeTransfer:
     a failure among them is final (there is no host copy to retry from).
     """
 
-    PIPELINE_MIN_RECORD_BYTES = 128 << 10
-
     def __init__(self, session: GcmSession, shape: LayerShape, stream=None, streams=None,
-                 causal_group_blocks: int = 0, pipeline_seal="auto"):
+                 causal_group_blocks: int = 0, pipeline_seal: bool = True):
         self.session = session
         self.shape = shape
         self.stream = stream
@@ -458,7 +456,7 @@ class NativeTransfer:
             return
         if self.layer in self._prefetched:
             self._prefetched.discard(self.layer)
-        elif self._pipelined(self.layer) and (len(plan) > 1 or len(plan[0][1]) > 1):
+        elif self.pipeline_seal and (len(plan) > 1 or len(plan[0][1]) > 1):
             self.prefetch_kv_transfer(payload, self.layer)
             self._prefetched.discard(self.layer)
         bits = self.shape.bits_for(self.layer)
@@ -485,11 +483,6 @@ class NativeTransfer:
             if st != parent:
                 parent.wait_stream(st)
         self.layer += 1
-
-    def _pipelined(self, layer: int) -> bool:
-        if self.pipeline_seal == "auto":
-            return self.shape.record_bytes_for(layer) >= self.PIPELINE_MIN_RECORD_BYTES
-        return bool(self.pipeline_seal)
 
     def prefetch_kv_transfer(self, payload, layer: int) -> bool:
         """Seal `layer`'s records on the host worker pool ahead of demand

@@ -6,6 +6,8 @@ host authenticates into its pools (secure_infer_d2h_*, D2HTransfer).
 Every comparison is bit-exact against the data that went in, or against the
 oracle codec (C restatement) for packets.
 """
+import ctypes as ct
+
 import numpy as np
 import pytest
 import torch
@@ -233,6 +235,62 @@ def test_retired_prefetch_falls_back_to_sealing_on_demand():
         si.clear_host_ranges()
 
 
+def test_group_launch_mixes_sources_and_ticket_runs():
+    """A layer group's K and V swaps go out as one launch even when the K
+    records come from a prefetch buffer and the V records are sealed on
+    demand under tickets that do not follow the K tickets (another prefetch
+    reserved tickets in between): the launch then carries explicit per-record
+    IV words.  A one-shot tamper of a V record is retried from its own
+    status word; the caches end bit-exact."""
+    rng = np.random.default_rng(144)
+    heads, dim, ncpu, nslots, layer = 2, 128, 9, 16, 2
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 5, max_record_bytes=shape.record_bytes)
+    L = _lib.load()
+    si.clear_host_ranges()
+    try:
+        hk, hv = pools(rng, ncpu, heads, dim)
+        other, _ = pools(rng, ncpu, heads, dim)
+        si.register_host_range(hk, layer, 0)
+        si.register_host_range(hv, layer, 1)
+        si.register_host_range(other, layer + 1, 0)
+        ck, cv = caches(nslots, heads, dim)
+        cpu_ids = np.array([8, 1, 4, 0, 6])
+        slot_ids = np.array([3, 15, 0, 9, 7])
+        m = torch.from_numpy(np.stack([cpu_ids, slot_ids], 1).astype(np.int64)).contiguous()
+        stream = torch.cuda.current_stream().cuda_stream
+        bb = hk[0].numel() * 2
+
+        def prefetch(pool, kind, lay):
+            assert L.secure_infer_h2d_prefetch(sess._h, ct.c_void_p(pool.data_ptr()), bb, ncpu,
+                                               ct.c_void_p(m.data_ptr()), len(cpu_ids), kind, lay, 0, heads, dim) == 0
+
+        def swap(pool, cache, kind):
+            return L.secure_infer_h2d_swap(ct.c_void_p(stream), sess._h, ct.c_void_p(pool.data_ptr()), bb, ncpu,
+                                           ct.c_void_p(cache.data_ptr()), bb, nslots, ct.c_void_p(m.data_ptr()),
+                                           len(cpu_ids), kind, layer, 0, heads, dim, None)
+
+        prefetch(hk, 0, layer)
+        before = si.transfer_prefetch_stats()
+        si.inject_h2d_tamper(layer=layer, kind=1, host_block=4, shots=1)
+        assert L.secure_infer_h2d_layer_group_begin(2 * len(cpu_ids)) == 0
+        assert swap(hk, ck, 0) == 0
+        prefetch(other, 0, layer + 1)  # tickets between the K and the V records
+        assert swap(hv, cv, 1) == 0
+        assert L.secure_infer_h2d_layer_group_end() == 0
+        assert si.NativeTransfer(sess, shape).wait_layer(layer) == 0
+        after = si.transfer_prefetch_stats()
+        assert after["ready"] + after["busy_fallback"] - before["ready"] - before["busy_fallback"] == 1
+        idx = torch.from_numpy(slot_ids.astype(np.int64)).to(DEV)
+        cid = torch.from_numpy(cpu_ids.astype(np.int64))
+        assert torch.equal(ck.index_select(0, idx).cpu(), hk.index_select(0, cid))
+        assert torch.equal(cv.index_select(0, idx).cpu(), hv.index_select(0, cid))
+    finally:
+        si.inject_h2d_tamper(shots=0)
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()
+
+
 def test_job_authentication_spans_layers():
     """secure_infer_recovery_wait_job_authentication (secure_infer.cpp:7336-7372):
     every record of the job on every layer, no retry; 1 / 0 / -1."""
@@ -285,8 +343,9 @@ print("done")
 
 
 def test_h2d_profile_ledger(tmp_path):
-    """SECURE_INFER_H2D_PROFILE: one CSV row per swap with host seal, H2D copy
-    and kernel time (the reference's per-copy rows, secure_infer.cpp:6085-6137)."""
+    """SECURE_INFER_H2D_PROFILE: one CSV row per launch with host seal, H2D copy
+    and kernel time (the reference's per-copy rows, secure_infer.cpp:6085-6137);
+    a layer group's K and V swaps go out as one launch (kind 2)."""
     import os
     import subprocess
     import sys
@@ -299,11 +358,11 @@ def test_h2d_profile_ledger(tmp_path):
     lines = csv.read_text().strip().splitlines()
     assert lines[0] == "layer,kind,records,record_bytes,source,seal_us,h2d_copy_us,kernel_us"
     rows = [l.split(",") for l in lines[1:]]
-    assert len(rows) == 4
+    assert len(rows) == 2
     # layer 0 was sealed ahead of demand (ready or still sealing when its swap
     # came), layer 1 on demand
     src = sorted((r[0], r[1], r[4].replace("prefetch_waited", "prefetched")) for r in rows)
-    assert src == [("0", "0", "prefetched"), ("0", "1", "prefetched"), ("1", "0", "sealed"), ("1", "1", "sealed")]
+    assert src == [("0", "2", "prefetched"), ("1", "2", "sealed")]
     for r in rows:
-        assert int(r[2]) == 3 and int(r[3]) == 128 * 2 * 128 * 2
+        assert int(r[2]) == 6 and int(r[3]) == 128 * 2 * 128 * 2
         assert float(r[5]) > 0 and float(r[6]) > 0 and float(r[7]) > 0

@@ -65,13 +65,15 @@ class Recorder:
         return 0
 
 
-def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False):
+def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False,
+                 pipeline_seal=True):
     rec = Recorder()
     parent = FakeStream("parent")
     shape = shape or si.LayerShape(2, 64)
     sess = mock.Mock()
     sess._h = None
-    nt = si.NativeTransfer(sess, shape, streams=streams or None, causal_group_blocks=group)
+    nt = si.NativeTransfer(sess, shape, streams=streams or None, causal_group_blocks=group,
+                           pipeline_seal=pipeline_seal)
     nt.layer = layer
     host = [torch.zeros((nblocks, 4), dtype=torch.int16), torch.zeros((nblocks, 4), dtype=torch.int16)]
     dest = [torch.zeros((nslots or nblocks + 100, 4), dtype=torch.int16) for _ in range(2)]
@@ -161,8 +163,7 @@ def test_layer_seals_are_queued_in_swap_order():
     sealing on the host pool part by part in exactly the order (and with the
     exact mappings) the swaps then consume them, so tickets follow the
     reference's (group, kind, block) order either way."""
-    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True,
-                             shape=si.LayerShape(8, 128))  # 256-KiB records: pipelined
+    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True)
     pre = [(c[1], c[2], c[4]) for c in rec.calls if c[0] == "prefetch"]
     swaps = [(c[2], c[3], c[5]) for c in rec.calls if c[0] == "swap"]
     assert pre == swaps and len(pre) == 6
@@ -171,6 +172,6 @@ def test_layer_seals_are_queued_in_swap_order():
     assert last_prefetch < first_swap
 
 
-def test_small_records_are_sealed_on_demand():
-    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True)  # 32-KiB records
+def test_unpipelined_layers_are_sealed_on_demand():
+    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True, pipeline_seal=False)
     assert not [c for c in rec.calls if c[0] == "prefetch"]
