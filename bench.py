@@ -217,12 +217,12 @@ def cpu_baseline(op: str, wire_host: np.ndarray, stride: int, nbytes: int, nrec:
                 us_per_layer=round(med * 1e6, 1), statuses_match_gpu=ok, matches_gpu=bool(same))
 
 
-def ledger_split(path: Path, steps: int) -> dict | None:
+def ledger_split(path: Path, steps: int) -> dict:
     """Mean host seal / H2D copy / kernel microseconds per layer from the
     library's H2D ledger rows (SECURE_INFER_H2D_PROFILE, one row per launch:
     a causal group's K and V swaps go out as one), by record source."""
     if not path.exists():
-        return None
+        return {}
     rows = [l.split(",") for l in path.read_text().strip().splitlines()[1:]]
     out = {}
     for src in ("sealed", "prefetched", "prefetch_waited"):
@@ -287,11 +287,10 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
             good = all(nt.wait_layer(l) == 0 for l in range(L))
             torch.cuda.synchronize()
             return good, time.perf_counter() - t0
+        # Timed steps run with the ledger paused (its timing events cost the
+        # host ~10 us per launch); one more step of each mode records it.
+        si.pause_h2d_profile(True)
         ok, _ = step(False)
-        si.drain_h2d_profile_after_job()
-        ledger = os.environ.get("SECURE_INFER_H2D_PROFILE")
-        if ledger and Path(ledger).exists():
-            Path(ledger).write_text(Path(ledger).read_text().splitlines()[0] + "\n")  # drop the warm-up rows
         med = {}
         for ahead in (False, True):
             times = []
@@ -304,12 +303,23 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
         if truth is not None:
             got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
             ok &= bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
-        si.drain_h2d_profile_after_job()
         out["sealed_ahead_of_demand"] = {"us_per_layer": round(med[True] * 1e6 / L, 1),
                                          "GB_s": round(algo_layer * L / med[True] / 1e9, 2),
                                          "prefetch_stats": si.transfer_prefetch_stats()}
+        ledger = os.environ.get("SECURE_INFER_H2D_PROFILE")
         if ledger:
-            out["ledger_split"] = ledger_split(Path(ledger), steps)
+            si.pause_h2d_profile(False)
+            split = {}
+            for ahead, name in ((False, "on_demand"), (True, "sealed_ahead_of_demand")):
+                si.drain_h2d_profile_after_job()
+                if Path(ledger).exists():
+                    Path(ledger).write_text(Path(ledger).read_text().splitlines()[0] + "\n")
+                good, t = step(ahead)
+                ok &= good
+                si.drain_h2d_profile_after_job()
+                split[name] = ledger_split(Path(ledger), 1)
+                split[name]["step_us_per_layer_with_ledger"] = round(t * 1e6 / L, 1)
+            out["ledger_split"] = split
         what = ("host OpenSSL seal + pinned ring + H2D (copy stream) + fused verify/decrypt/scatter, "
                 "causal groups of %d blocks; median step" % LOAD_CHUNK_BLOCKS)
     else:

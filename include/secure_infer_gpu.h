@@ -333,13 +333,17 @@ int secure_infer_h2d_prefetch(si_session* session, const void* host_base, uint64
                               uint64_t host_nblocks, const int64_t* mapping, uint32_t n, uint32_t kind,
                               uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim);
 
-/* secure_infer.cpp:6085-6137: the per-swap H2D ledger.  With
- * SECURE_INFER_H2D_PROFILE=<path> every swap appends one CSV row (layer,
- * kind, records, record_bytes, source, seal_us, h2d_copy_us, kernel_us) once
- * its work is complete; flush writes the rows of completed swaps, drain
- * waits for every pending swap first. */
+/* secure_infer.cpp:6085-6137: the H2D ledger.  With
+ * SECURE_INFER_H2D_PROFILE=<path> every launch appends one CSV row (layer,
+ * kind -- 0 K, 1 V, 2 both --, records, record_bytes, source, seal_us,
+ * h2d_copy_us, kernel_us) once its work is complete; flush writes the rows
+ * of completed launches, drain waits for every pending launch first. */
 void secure_infer_flush_completed_h2d_profile(void);
 void secure_infer_drain_h2d_profile_after_job(void);
+/* No reference counterpart: pauses (1) or resumes (0) the ledger's rows and
+ * their timing events, so a caller can time transfers without the ledger's
+ * own cost and record a ledger over other ones. */
+void secure_infer_pause_h2d_profile(int paused);
 
 /* Threads of the host crypto pool (the calling thread included): the CPUs of
  * the process affinity mask, or SECURE_INFER_HOST_THREADS.  No reference

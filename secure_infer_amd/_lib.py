@@ -76,6 +76,7 @@ SIGNATURES = {
     "secure_infer_h2d_prefetch": ([_v, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32, _u32, _u32], _i),
     "secure_infer_flush_completed_h2d_profile": ([], None),
     "secure_infer_drain_h2d_profile_after_job": ([], None),
+    "secure_infer_pause_h2d_profile": ([ct.c_int], None),
     "secure_infer_recovery_set_job_id": ([_u64], None),
     "secure_infer_recovery_wait_job_authentication": ([_u64], _i),
     "secure_infer_d2h_batch_begin": ([_sz], _i),

@@ -522,8 +522,11 @@ std::mutex g_profile_lock;
 FILE* g_profile = nullptr;
 bool g_profile_checked = false;
 
+std::atomic<bool> g_profile_paused{false};
+
 bool profile_on()
 {
+    if (g_profile_paused.load(std::memory_order_relaxed)) return false;
     std::lock_guard<std::mutex> g(g_profile_lock);
     if (!g_profile_checked) {
         g_profile_checked = true;
@@ -1402,6 +1405,8 @@ void secure_infer_invalidate_transfer_prefetches(void) { secure_infer_retire_tra
 void secure_infer_flush_completed_h2d_profile(void) { profile_sweep(false); }
 
 void secure_infer_drain_h2d_profile_after_job(void) { profile_sweep(true); }
+
+void secure_infer_pause_h2d_profile(int paused) { g_profile_paused.store(paused != 0); }
 
 int secure_infer_test_tamper_h2d(int32_t layer, int32_t kind, int64_t host_block, uint32_t shots)
 {

@@ -457,6 +457,15 @@ class NativeTransfer:
         if self.layer in self._prefetched:
             self._prefetched.discard(self.layer)
         elif self.pipeline_seal and (len(plan) > 1 or len(plan[0][1]) > 1):
+            # The swaps refuse ids outside either pool before sealing anything;
+            # sealing ahead must not spend tickets on a mapping they refuse.
+            # (numpy: a torch reduction would wake torch's CPU thread pool,
+            # whose spinning threads then compete with the sealing workers)
+            m = mapping.numpy()
+            lo, hi = m.min(0), m.max(0)
+            if (lo[0] < 0 or hi[0] >= min(host[0].shape[0], host[1].shape[0]) or lo[1] < 0
+                    or hi[1] >= min(destination[0].shape[0], destination[1].shape[0])):
+                raise RuntimeError("h2d_swap refused: a mapping entry lies outside its pool")
             self.prefetch_kv_transfer(payload, self.layer)
             self._prefetched.discard(self.layer)
         bits = self.shape.bits_for(self.layer)
@@ -465,20 +474,26 @@ class NativeTransfer:
         for st in streams:
             if st != parent:
                 st.wait_stream(parent)
+        # Per-kind pool arguments and stream handles, computed once per layer.
+        pools = []
+        for kind in (0, 1):
+            src, dst = self._host_pool(host[kind]), destination[kind]
+            _dev(dst, "destination cache")
+            pools.append((ct.c_void_p(src.data_ptr()), src.stride(0) * src.element_size(), src.shape[0],
+                          ct.c_void_p(dst.data_ptr()), dst.stride(0) * dst.element_size(), dst.shape[0]))
+        handles = [_stream(st) for st in streams]
+        L = lib()
+        swap, h = L.secure_infer_h2d_swap, self.session._h
+        heads, dim, layer = self.shape.heads, self.shape.head_dim, self.layer
         for k, parts in plan:
-            _check(lib().secure_infer_h2d_layer_group_begin(2 * k), "h2d_layer_group_begin")
+            _check(L.secure_infer_h2d_layer_group_begin(2 * k), "h2d_layer_group_begin")
             try:
                 for kind, j, part in parts:
-                    src, dst = self._host_pool(host[kind]), destination[kind]
-                    _dev(dst, "destination cache")
-                    _check(lib().secure_infer_h2d_swap(
-                        _stream(streams[j]), self.session._h, ct.c_void_p(src.data_ptr()),
-                        src[0].numel() * src.element_size(), src.shape[0], ct.c_void_p(dst.data_ptr()),
-                        dst[0].numel() * dst.element_size(), dst.shape[0],
-                        ct.c_void_p(part.data_ptr()), part.shape[0], kind, self.layer, bits,
-                        self.shape.heads, self.shape.head_dim, None), "h2d_swap")
+                    sp, sbb, sn, dp, dbb, dn = pools[kind]
+                    _check(swap(handles[j], h, sp, sbb, sn, dp, dbb, dn, ct.c_void_p(part.data_ptr()),
+                                part.shape[0], kind, layer, bits, heads, dim, None), "h2d_swap")
             finally:
-                _check(lib().secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
+                _check(L.secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
         for st in streams:
             if st != parent:
                 parent.wait_stream(st)
@@ -494,13 +509,16 @@ class NativeTransfer:
         mapping = mapping.to(device="cpu", dtype=torch.int64).contiguous()
         bits = self.shape.bits_for(layer)
         ok = True
+        pools = []
+        for kind in (0, 1):
+            src = self._host_pool(host[kind])
+            pools.append((ct.c_void_p(src.data_ptr()), src.stride(0) * src.element_size(), src.shape[0]))
+        prefetch, h = lib().secure_infer_h2d_prefetch, self.session._h
         for _, parts in self._plan(mapping):
             for kind, _, part in parts:
-                src = self._host_pool(host[kind])
-                ok &= lib().secure_infer_h2d_prefetch(
-                    self.session._h, ct.c_void_p(src.data_ptr()), src[0].numel() * src.element_size(),
-                    src.shape[0], ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer, bits,
-                    self.shape.heads, self.shape.head_dim) == 0
+                sp, sbb, sn = pools[kind]
+                ok &= prefetch(h, sp, sbb, sn, ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer, bits,
+                               self.shape.heads, self.shape.head_dim) == 0
         self._prefetched.add(layer)
         return ok
 
@@ -639,6 +657,11 @@ def flush_completed_h2d_profile() -> None:
 
 def drain_h2d_profile_after_job() -> None:
     lib().secure_infer_drain_h2d_profile_after_job()
+
+
+def pause_h2d_profile(paused: bool) -> None:
+    """Stops (True) or resumes (False) recording ledger rows and their timing events."""
+    lib().secure_infer_pause_h2d_profile(int(bool(paused)))
 
 
 def inject_h2d_tamper(layer: int = -1, kind: int = -1, host_block: int = -1, shots: int = 1) -> None:

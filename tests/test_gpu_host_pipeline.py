@@ -331,7 +331,7 @@ hk = torch.zeros((8, 128, heads, dim), dtype=torch.int16)
 hv = torch.ones((8, 128, heads, dim), dtype=torch.int16)
 ck = torch.zeros((8, 128, heads, dim), dtype=torch.int16, device="cuda")
 cv = torch.zeros_like(ck)
-nt = si.NativeTransfer(sess, shape)
+nt = si.NativeTransfer(sess, shape, pipeline_seal=False)
 m = torch.tensor([[0, 1], [2, 3], [7, 5]], dtype=torch.int64)
 assert nt.prefetch_kv_transfer(((hk, hv), m), 0)
 nt.single_layer_kv_transfer(((hk, hv), m), (ck, cv))

@@ -129,9 +129,17 @@ def test_slice_streams_stripe_rows_and_join():
 
 
 def test_swap_carries_pool_sizes():
-    _, rec, _ = run_transfer(5, 0, None, nslots=64)
+    _, rec, _ = run_transfer(5, 0, None, nslots=164)
     swaps = [c for c in rec.calls if c[0] == "swap"]
-    assert all(c[6] == 5 and c[7] == 64 for c in swaps)
+    assert swaps and all(c[6] == 5 and c[7] == 164 for c in swaps)
+
+
+@pytest.mark.parametrize("nslots", [64, 104])
+def test_out_of_pool_mapping_is_refused_before_sealing_ahead(nslots):
+    """Slots 100..104 do not fit a 64- or 104-slot cache: the layer is
+    refused before any record is sealed ahead (the swaps would refuse it)."""
+    with pytest.raises(RuntimeError):
+        run_transfer(5, 0, None, nslots=nslots, keep_prefetch=True)
 
 
 @pytest.mark.parametrize("layers", [1, 2, 3, 28, 32, 40, 80])
