@@ -259,7 +259,7 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
     for l in range(L):
         si.register_host_range(hosts[l][0], l, 0)
         si.register_host_range(hosts[l][1], l, 1)
-    d2h = si.D2HTransfer(sess, shape, group_blocks=NB)
+    d2h = si.D2HTransfer(sess, shape, group_blocks=16)  # PIPE_D2H_GROUP_BLOCKS default (npu_predict.py:88-94)
     wb_map = [torch.stack([slots[l].cpu(), torch.arange(NB)], 1).contiguous() for l in range(L)]
     # host pools hold what a writeback produced (bf16 blocks or codec packets)
     for l in range(L):
@@ -323,15 +323,19 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
         what = ("host OpenSSL seal + pinned ring + H2D (copy stream) + fused verify/decrypt/scatter, "
                 "causal groups of %d blocks; median step" % LOAD_CHUNK_BLOCKS)
     else:
+        # One batch per step over every layer with one block table, as the
+        # reference's store job submits them (npu_predict.py:874-916).
         ok = True
+        srcs = [(cache[l, 0], cache[l, 1]) for l in range(L)]
+        d2h.store(srcs, hosts, wb_map[0], layers=list(range(L)))
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
-            for l in range(L):
-                d2h.store([(cache[l, 0], cache[l, 1])], [hosts[l]], wb_map[l], layers=[l])
+            d2h.store(srcs, hosts, wb_map[0], layers=list(range(L)))
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
-        what = "fused gather/quantise/seal + D2H + host OpenSSL authenticate/decrypt into host pools"
+        what = ("fused gather/quantise/seal + D2H + host OpenSSL authenticate/decrypt into host pools, "
+                "one batch of every layer in groups of %d blocks" % d2h.group_blocks)
     si.clear_host_ranges()
     out.update({"us_per_layer": round(dt * 1e6 / L, 1), "GB_s": round(algo_layer * L / dt / 1e9, 2),
                 "steps": steps, "ok": bool(ok), "path": what})

@@ -364,11 +364,17 @@ int secure_infer_d2h_batch_end(void);
 /* Inside an open D2H group: gather (+ quantise) and seal n device blocks of
  * one (layer, kind) on `stream` (the hook's D2H branch, secure_infer.cpp:
  * 8076-8562, with gcm_encrypt_tag, ghash.aicpu:656-699), copy the records to
- * pinned memory on the library's D2H stream; at group end the worker pool
+ * pinned memory on the library's D2H stream, then the worker pool
  * authenticates and decrypts each into host_base + block*host_block_bytes
  * (d2h_host_decrypt_one, secure_infer.cpp:2470-2547).  mapping pairs are
- * (device slot, host block).  A failed record is zeroed in the host pool
- * and makes batch_end return -1 (the reference zeroes and aborts). */
+ * (device slot, host block).  A batch's swaps of one stream and layer (K
+ * before V, up to SECURE_INFER_D2H_LAUNCH_MB = 64 of records, across
+ * groups) go out as one launch, issued by the next swap that does not fit
+ * it or at the latest by batch_device_barrier / batch_end; a per-device
+ * thread hands each launch to the pool once its copy is done.  At most 6
+ * launches and SECURE_INFER_D2H_INFLIGHT_MB (128) of buffers are in flight
+ * per device; an issue beyond that waits.  A failed record is zeroed in the
+ * host pool and makes batch_end return -1 (the reference zeroes and aborts). */
 int secure_infer_d2h_swap(hipStream_t stream, si_session* session, const void* dev_cache,
                           uint64_t slot_bytes, uint64_t nslots, void* host_base,
                           uint64_t host_block_bytes, uint64_t host_nblocks, const int64_t* mapping,

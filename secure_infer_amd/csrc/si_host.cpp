@@ -26,12 +26,13 @@
 //    failed once from the trusted host copy under a fresh ticket and
 //    returns -1 only when that second attempt fails too (:7303-7333).
 //  * D2H: the reference's batch / group API with the same names and
-//    thread-local contexts (secure_infer.cpp:2707-2970).  Inside a group,
-//    secure_infer_d2h_swap gathers (+ quantises) and seals device KV blocks
-//    on the caller's stream, then copies the records to pinned memory on a
-//    second copy stream; the group's end hands them to the worker pool, which
-//    authenticates and decrypts each record into its host destination (a
-//    record that fails is zeroed).  batch_end waits for that verification.
+//    thread-local contexts (secure_infer.cpp:2707-2970).  A batch's swaps of
+//    one stream and layer accumulate into one launch (gather + quantise +
+//    seal on the caller's stream, records copied to pinned memory on a D2H
+//    stream); a per-device watcher thread hands each launch to the worker
+//    pool once its copy is done, which authenticates and decrypts each
+//    record into its host destination (a record that fails is zeroed).
+//    Launches in flight are bounded; batch_end waits for the verification.
 //  * Ahead-of-demand sealing (the reference's CPU ciphertext prefetch,
 //    secure_infer.cpp:3264-3710): secure_infer_h2d_prefetch seals a swap's
 //    records on the worker pool before the swap is issued, under tickets
@@ -405,7 +406,11 @@ struct DeviceState {
     std::mutex rings_lock;
     std::unordered_map<hipStream_t, std::unique_ptr<StreamRing>> rings;
     std::mutex pool_lock;
-    std::vector<std::unique_ptr<Mirror>> free_bufs;  // D2H buffers between batches
+    std::vector<std::unique_ptr<Mirror>> free_bufs;  // D2H buffers not in flight
+    std::condition_variable d2h_cv;                  // d2h_inflight went down (pool_lock)
+    size_t d2h_inflight = 0;                         // bytes of D2H buffers in flight (pool_lock)
+    size_t d2h_jobs = 0;                             // D2H launches in flight (pool_lock)
+    struct D2HWatcher* watcher = nullptr;            // started by the first D2H launch
     std::mutex status_lock;
     std::vector<std::unique_ptr<StatusBuf>> free_status;
 };
@@ -1105,49 +1110,138 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
 
 // ---------------------------------------------------------------- D2H batches
 
+struct D2HBatch;
+
+// One record of a D2H launch: where it authenticates into and its ticket.
+struct D2HRec {
+    uint8_t* dst = nullptr;
+    uint64_t ticket = 0;
+};
+
+// The records of consecutive D2H swaps of one batch that are gathered,
+// sealed and copied back as one launch: K swaps before V swaps, all of one
+// stream, session, layer and geometry.  The buffer is laid out
+// [n wire records][iv words, n x 16, only when the tickets are not one run]
+// [slot ids, n x 8][device fail word, 16].
 struct D2HJob {
+    D2HBatch* batch = nullptr;
+    DeviceState* ds = nullptr;
     std::unique_ptr<Mirror> buf;
-    uint32_t n = 0;
-    uint64_t bytes = 0, stride = 0, tag_off = 0, t0 = 0;
-    uint64_t fail_off = 0;  // device u32 counting records with a bad slot id
-    uint8_t* host_base = nullptr;
-    uint64_t host_block_bytes = 0;
-    std::vector<int64_t> host_blocks;
+    hipStream_t stream = nullptr;
+    si_session* s = nullptr;
     si_internal::SessionKeys keys{};
+    uint32_t layer = 0, codec = 0, heads = 0, dim = 0;
+    uint64_t bytes = 0, stride = 0, tag_off = 0, slot_bytes = 0, nslots = 0;
+    const void* cache[2] = {nullptr, nullptr};
+    uint32_t n = 0, n_k = 0;
+    std::vector<D2HRec> recs;
+    std::vector<int64_t> slot_ids;
+    std::vector<uint8_t> aads;  // n x 64, copied into the records' AAD slots at issue
+    uint64_t fail_off = 0;      // device u32 counting records with a bad slot id
+    size_t counted = 0;         // buffer bytes counted in flight for the device
+    size_t tasks_left = 0;      // verification tasks not finished (guarded by the batch's lock)
 };
 
 struct D2HBatch {
     DeviceState* ds = nullptr;
     bool group_open = false;
-    std::vector<std::unique_ptr<D2HJob>> jobs;
-    size_t group_first = 0;  // first job of the open group
+    std::vector<std::unique_ptr<D2HJob>> jobs;  // issued launches
+    std::unique_ptr<D2HJob> pending;           // launch still taking swaps
     std::vector<hipStream_t> streams;
     std::vector<hipEvent_t> joins;
     std::mutex m;
     std::condition_variable cv;
-    size_t pending = 0;  // verification tasks in flight (guarded by m)
+    size_t pending_tasks = 0;  // verification tasks in flight (guarded by m)
     std::atomic<uint64_t> failures{0};
 };
 
 thread_local std::unique_ptr<D2HBatch> t_batch;
 
-std::unique_ptr<Mirror> take_buffer(DeviceState* ds)
+// D2H launches a device keeps in flight: at most 6, and at most
+// SECURE_INFER_D2H_INFLIGHT_MB (default 128) of buffers; an issue waits for
+// earlier launches' verification beyond either.  Three or four in flight keep
+// the copy engine and the verifiers busy.  More only queue copies: with ten
+// 42-MB copies queued, enqueueing the next one blocked the issuing thread for
+// ~12 ms (MI355X, ROCm 7.2), and the GPU's queue ran dry meanwhile.
+constexpr size_t kD2HMaxJobs = 6;
+
+// Largest D2H launch in wire bytes (SECURE_INFER_D2H_LAUNCH_MB, default 64):
+// a batch's swaps of one layer merge into launches up to this size.  A store
+// job's batch spans every layer, so one layer's host authentication overlaps
+// the next layer's copy; smaller launches measured slower there (70B int4
+// layer, 42 MB: 8 MB launches 1480 us per layer, 64 MB 830 us).
+uint64_t d2h_launch_cap()
 {
-    {
-        std::lock_guard<std::mutex> g(ds->pool_lock);
-        if (!ds->free_bufs.empty()) {
-            auto b = std::move(ds->free_bufs.back());
-            ds->free_bufs.pop_back();
-            return b;
-        }
-    }
-    auto b = std::make_unique<Mirror>();
-    if (!b->init()) return nullptr;
+    static const uint64_t b = [] {
+        uint64_t mb = 64;
+        if (const char* e = std::getenv("SECURE_INFER_D2H_LAUNCH_MB")) mb = uint64_t(std::max(1, std::atoi(e)));
+        return mb << 20;
+    }();
     return b;
 }
 
-void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
+size_t d2h_inflight_budget()
 {
+    static const size_t b = [] {
+        size_t mb = 128;
+        if (const char* e = std::getenv("SECURE_INFER_D2H_INFLIGHT_MB")) mb = size_t(std::max(1, std::atoi(e)));
+        return mb << 20;
+    }();
+    return b;
+}
+
+// A D2H buffer of at least `need` bytes (and `stage` bytes of codec staging),
+// counted in flight until put_buffer.
+std::unique_ptr<Mirror> take_buffer(DeviceState* ds, size_t need, size_t stage)
+{
+    std::unique_ptr<Mirror> b;
+    {
+        std::unique_lock<std::mutex> g(ds->pool_lock);
+        ds->d2h_cv.wait(g, [&] {
+            return ds->d2h_jobs == 0 ||
+                   (ds->d2h_jobs < kD2HMaxJobs && ds->d2h_inflight + need <= d2h_inflight_budget());
+        });
+        ds->d2h_inflight += need;
+        ++ds->d2h_jobs;
+        size_t best = ds->free_bufs.size();
+        for (size_t i = 0; i < ds->free_bufs.size(); ++i)
+            if (ds->free_bufs[i]->cap >= need &&
+                (best == ds->free_bufs.size() || ds->free_bufs[i]->cap < ds->free_bufs[best]->cap))
+                best = i;
+        if (best == ds->free_bufs.size() && !ds->free_bufs.empty()) best = ds->free_bufs.size() - 1;
+        if (best < ds->free_bufs.size()) {
+            b = std::move(ds->free_bufs[best]);
+            ds->free_bufs.erase(ds->free_bufs.begin() + long(best));
+        }
+    }
+    if (!b) {
+        b = std::make_unique<Mirror>();
+        if (!b->init()) b.reset();
+    }
+    if (!b || !b->reserve(need, stage)) {
+        std::lock_guard<std::mutex> g(ds->pool_lock);
+        ds->d2h_inflight -= need;
+        --ds->d2h_jobs;
+        ds->d2h_cv.notify_all();
+        return nullptr;
+    }
+    return b;
+}
+
+void put_buffer(DeviceState* ds, std::unique_ptr<Mirror> b, size_t counted)
+{
+    std::lock_guard<std::mutex> g(ds->pool_lock);
+    ds->d2h_inflight -= counted;
+    --ds->d2h_jobs;
+    if (b) ds->free_bufs.push_back(std::move(b));
+    ds->d2h_cv.notify_all();
+}
+
+size_t job_bytes(const D2HJob& j, bool ivs) { return size_t(j.n) * (j.stride + (ivs ? 24 : 8)) + 16; }
+
+void verify_records(D2HJob* job, uint32_t r0, uint32_t r1)
+{
+    D2HBatch* b = job->batch;
     uint64_t bad = 0;
     if (hipEventSynchronize(job->buf->ev_b) != hipSuccess) {
         bad = r1 - r0;
@@ -1162,10 +1256,10 @@ void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
         }
         for (uint32_t r = r0; r < r1; ++r) {
             uint8_t* rec = job->buf->host + uint64_t(r) * job->stride;
-            uint8_t* dst = job->host_base + uint64_t(job->host_blocks[r]) * job->host_block_bytes;
+            uint8_t* dst = job->recs[r].dst;
             if (take_shot(g_tamper_d2h)) rec[0] ^= 0x01;
             uint8_t iv[12];
-            record_iv(job->keys, job->t0 + r, iv);
+            record_iv(job->keys, job->recs[r].ticket, iv);
             if (!gcm_open(job->keys.key, iv, rec + job->tag_off + 32, 64, rec, job->bytes,
                           rec + job->tag_off, dst)) {
                 memset(dst, 0, job->bytes);  // fail closed
@@ -1174,10 +1268,167 @@ void verify_records(D2HBatch* b, D2HJob* job, uint32_t r0, uint32_t r1)
         }
     }
     if (bad) b->failures.fetch_add(bad);
-    // The decrement and the notification happen under the batch's lock:
-    // batch_end may destroy the batch as soon as it sees pending == 0.
+    // The decrements and the notification happen under the batch's lock:
+    // batch_end may destroy the batch as soon as it sees pending_tasks == 0.
+    // The job's buffer goes back to the device's pool after its last task.
+    std::unique_ptr<Mirror> done;
+    bool last = false;
+    {
+        std::lock_guard<std::mutex> g(b->m);
+        if (--job->tasks_left == 0) {
+            done = std::move(job->buf);
+            last = true;
+        }
+    }
+    if (last) put_buffer(job->ds, std::move(done), job->counted);
     std::lock_guard<std::mutex> g(b->m);
-    if (--b->pending == 0) b->cv.notify_all();
+    if (--b->pending_tasks == 0) b->cv.notify_all();
+}
+
+// Hands a launch's records to the worker pool once its copies are done.
+void d2h_copied(D2HJob* job)
+{
+    const uint32_t per_task = 4;
+    std::vector<std::function<void()>> tasks;
+    for (uint32_t r0 = 0; r0 < job->n; r0 += per_task) {
+        const uint32_t r1 = std::min(job->n, r0 + per_task);
+        tasks.emplace_back([job, r0, r1] { verify_records(job, r0, r1); });
+    }
+    Pool::get().submit_all(tasks);
+}
+
+// One thread per device waits for issued launches' copies in issue order
+// (the order the D2H stream runs them) and hands each to the worker pool
+// -- the reference's host callback after a group's copy
+// (d2h_group_ready_callback via aclrtLaunchHostFunc, secure_infer.cpp:2880-2895).
+// A host function on the D2H stream itself would hold the stream until the
+// runtime's callback thread has run it, a gap after every launch's copy.
+struct D2HWatcher {
+    std::mutex m;
+    std::condition_variable cv;
+    std::deque<D2HJob*> q;
+};
+
+void d2h_watch(DeviceState* ds, D2HJob* job)
+{
+    D2HWatcher& w = *ds->watcher;
+    {
+        std::lock_guard<std::mutex> g(w.m);
+        w.q.push_back(job);
+    }
+    w.cv.notify_one();
+}
+
+bool start_watcher(DeviceState* ds)
+{
+    std::lock_guard<std::mutex> g(ds->pool_lock);
+    if (ds->watcher) return true;
+    ds->watcher = new D2HWatcher();  // never destroyed, like the worker pool
+    D2HWatcher* w = ds->watcher;
+    const int device = ds->device;
+    std::thread([w, device] {
+        (void)hipSetDevice(device);
+        for (;;) {
+            D2HJob* job = nullptr;
+            {
+                std::unique_lock<std::mutex> g(w->m);
+                w->cv.wait(g, [&] { return !w->q.empty(); });
+                job = w->q.front();
+                w->q.pop_front();
+            }
+            (void)hipEventSynchronize(job->buf->ev_b);  // the tasks check the status again
+            d2h_copied(job);
+        }
+    }).detach();
+    return true;
+}
+
+// Issues the batch's pending launch: AADs, iv words, slot ids and a zeroed
+// fail word up on the caller's stream, gather (+ quantise) + seal, then the
+// records and the fail word down on the D2H stream, whose host function
+// queues their authentication.
+int d2h_issue(D2HBatch* b)
+{
+    std::unique_ptr<D2HJob> job = std::move(b->pending);
+    if (!job || job->n == 0) return 0;
+    if (!start_watcher(job->ds)) return -1;
+    bool run = true;  // tickets t0 .. t0 + n - 1 in record order
+    for (uint32_t r = 1; r < job->n; ++r) run = run && job->recs[r].ticket == job->recs[r - 1].ticket + 1;
+    const size_t wire = size_t(job->n) * job->stride;
+    const size_t iv_bytes = run ? 0 : size_t(job->n) * 16;
+    job->fail_off = wire + iv_bytes + size_t(job->n) * 8;
+    const size_t need = job_bytes(*job, !run);
+    job->buf = take_buffer(job->ds, need, job->codec ? size_t(job->n) * job->tag_off : 0);
+    if (!job->buf) return -1;
+    job->counted = need;
+    DeviceState* ds = job->ds;
+    // On failure the buffer goes back to the pool once nothing queued uses it.
+    auto fail = [&]() {
+        (void)hipStreamSynchronize(job->stream);
+        (void)hipStreamSynchronize(ds->d2h);
+        put_buffer(ds, std::move(job->buf), job->counted);
+        return -1;
+    };
+    uint8_t* h = job->buf->host;
+    uint8_t* d = job->buf->dev;
+    for (uint32_t r = 0; r < job->n; ++r) memcpy(h + size_t(r) * job->stride + job->tag_off + 32, &job->aads[64 * size_t(r)], 64);
+    if (!run) {
+        uint32_t* w = reinterpret_cast<uint32_t*>(h + wire);
+        const uint32_t salt = (uint32_t(job->keys.salt[0]) << 24) | (uint32_t(job->keys.salt[1]) << 16) |
+                              (uint32_t(job->keys.salt[2]) << 8) | uint32_t(job->keys.salt[3]);
+        for (uint32_t r = 0; r < job->n; ++r) {
+            const uint64_t c = job->keys.nonce + job->recs[r].ticket;
+            w[4 * r] = salt;
+            w[4 * r + 1] = uint32_t(c >> 32);
+            w[4 * r + 2] = uint32_t(c);
+            w[4 * r + 3] = 2;
+        }
+    }
+    memcpy(h + wire + iv_bytes, job->slot_ids.data(), size_t(job->n) * 8);
+    memset(h + job->fail_off, 0, 16);
+    job->aads.clear();
+    job->aads.shrink_to_fit();
+    if (hipMemcpy2DAsync(d + job->tag_off + 32, job->stride, h + job->tag_off + 32, job->stride, 64, job->n,
+                         hipMemcpyHostToDevice, job->stream) != hipSuccess ||
+        hipMemcpyAsync(d + wire, h + wire, need - wire, hipMemcpyHostToDevice, job->stream) != hipSuccess)
+        return fail();
+    si_writeback_desc w{};
+    w.wire = d;
+    w.wire_stride = job->stride;
+    w.bytes = job->bytes;
+    w.nrec = job->n;
+    w.n_k = job->n_k;
+    w.iv_words = run ? nullptr : reinterpret_cast<const uint32_t*>(d + wire);
+    w.ticket_base = run ? job->recs[0].ticket : 0;
+    w.cache_k = const_cast<void*>(job->cache[0] ? job->cache[0] : job->cache[1]);
+    w.cache_v = const_cast<void*>(job->cache[1] ? job->cache[1] : job->cache[0]);
+    w.slot_bytes = job->slot_bytes;
+    w.nslots = job->nslots;
+    w.slots = reinterpret_cast<const int64_t*>(d + wire + iv_bytes);
+    w.codec_bits = job->codec;
+    w.heads = job->heads;
+    w.head_dim = job->dim;
+    w.layer = job->layer;
+    w.staging = job->buf->stage;
+    w.fail_count = reinterpret_cast<uint32_t*>(d + job->fail_off);
+    if (secure_infer_gpu_writeback_layer(job->stream, job->s, &w) != 0) return fail();
+    if (hipEventRecord(job->buf->ev_a, job->stream) != hipSuccess ||
+        hipStreamWaitEvent(ds->d2h, job->buf->ev_a, 0) != hipSuccess ||
+        hipMemcpyAsync(h, d, wire, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
+        hipMemcpyAsync(h + job->fail_off, d + job->fail_off, 16, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
+        hipEventRecord(job->buf->ev_b, ds->d2h) != hipSuccess)
+        return fail();
+    job->tasks_left = (job->n + 3) / 4;
+    {
+        std::lock_guard<std::mutex> g(b->m);
+        b->pending_tasks += job->tasks_left;
+    }
+    if (std::find(b->streams.begin(), b->streams.end(), job->stream) == b->streams.end())
+        b->streams.push_back(job->stream);
+    D2HJob* jp = job.get();
+    b->jobs.push_back(std::move(job));
+    d2h_watch(ds, jp);
+    return 0;
 }
 
 }  // namespace
@@ -1440,7 +1691,6 @@ int secure_infer_d2h_group_begin(size_t expected_tasks)
     (void)expected_tasks;
     if (!t_batch || t_batch->group_open) return -1;
     t_batch->group_open = true;
-    t_batch->group_first = t_batch->jobs.size();
     return 1;
 }
 
@@ -1456,101 +1706,73 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cac
     uint64_t bytes = 0;
     if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
     if (!valid_mapping(mapping, n, false, host_nblocks, nslots)) return -1;
-    auto job = std::make_unique<D2HJob>();
-    job->keys = si_internal::session_keys(s);
-    if (bytes > job->keys.max_record_bytes) return -1;
-    job->buf = take_buffer(b->ds);
-    if (!job->buf) return -1;
-    job->n = n;
-    job->bytes = bytes;
-    job->stride = secure_infer_wire_stride(bytes);
-    job->tag_off = tag_offset(bytes);
-    job->host_base = static_cast<uint8_t*>(host_base);
-    job->host_block_bytes = host_block_bytes;
-    job->host_blocks.resize(n);
-    // [wire records][slot ids, n x 8][fail word, 16]
-    const size_t wire = size_t(n) * job->stride;
-    job->fail_off = wire + size_t(n) * 8;
-    const size_t need = job->fail_off + 16;
-    if (!job->buf->reserve(need, codec_bits ? size_t(n) * job->tag_off : 0)) return -1;
-    job->t0 = si_internal::reserve_tickets(n);
-    if (!si_internal::replay_reserve_range(job->t0, n)) {
+    const si_internal::SessionKeys keys = si_internal::session_keys(s);
+    if (bytes > keys.max_record_bytes) return -1;
+    const uint64_t stride = secure_infer_wire_stride(bytes);
+
+    // Joins the pending launch if it takes these records, else issues that first.
+    D2HJob* J = b->pending.get();
+    if (J && !(J->stream == stream && J->s == s && J->layer == layer && J->codec == codec_bits &&
+               J->heads == heads && J->dim == head_dim && J->bytes == bytes && J->slot_bytes == slot_bytes &&
+               J->nslots == nslots && (J->cache[kind] == nullptr || J->cache[kind] == dev_cache) &&
+               !(kind == 0 && J->n > J->n_k) && (uint64_t(J->n) + n) * stride <= d2h_launch_cap())) {
+        if (d2h_issue(b) != 0) return -1;
+        J = nullptr;
+    }
+    if (!J) {
+        b->pending = std::make_unique<D2HJob>();
+        J = b->pending.get();
+        J->batch = b;
+        J->ds = b->ds;
+        J->stream = stream;
+        J->s = s;
+        J->keys = keys;
+        J->layer = layer;
+        J->codec = codec_bits;
+        J->heads = heads;
+        J->dim = head_dim;
+        J->bytes = bytes;
+        J->stride = stride;
+        J->tag_off = tag_offset(bytes);
+        J->slot_bytes = slot_bytes;
+        J->nslots = nslots;
+    }
+    const uint64_t t0 = si_internal::reserve_tickets(n);
+    if (!si_internal::replay_reserve_range(t0, n)) {
         fprintf(stderr, "[secure_infer] duplicate D2H transfer tickets rejected at %llu\n",
-                static_cast<unsigned long long>(job->t0));
+                static_cast<unsigned long long>(t0));
         return -1;
     }
-
-    // AADs (direction 2), device slot ids and the zeroed fail word go up
-    // first, on the caller's stream.
-    uint8_t* h = job->buf->host;
-    int64_t* slot_ids = reinterpret_cast<int64_t*>(h + wire);
-    memset(h + job->fail_off, 0, 16);
+    // AADs (direction 2) of the host destinations, built now.
+    const size_t a0 = J->aads.size();
+    J->aads.resize(a0 + 64 * size_t(n));
     for (uint32_t r = 0; r < n; ++r) {
         const int64_t ds_id = mapping[2 * r], hb = mapping[2 * r + 1];
-        slot_ids[r] = ds_id;
-        job->host_blocks[r] = hb;
-        const uint8_t* dst = job->host_base + uint64_t(hb) * host_block_bytes;
-        if (secure_infer_build_gcm_aad(dst, bytes, 2, job->t0 + r, 0, job->keys.nonce,
-                                       h + uint64_t(r) * job->stride + job->tag_off + 32) != 1)
+        uint8_t* dst = static_cast<uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes;
+        if (secure_infer_build_gcm_aad(dst, bytes, 2, t0 + r, 0, keys.nonce, &J->aads[a0 + 64 * size_t(r)]) != 1) {
+            J->aads.resize(a0);
             return -1;
+        }
     }
-    uint8_t* d = job->buf->dev;
-    if (hipMemcpy2DAsync(d + job->tag_off + 32, job->stride, h + job->tag_off + 32, job->stride, 64, n,
-                         hipMemcpyHostToDevice, stream) != hipSuccess ||
-        hipMemcpyAsync(d + wire, h + wire, size_t(n) * 8 + 16, hipMemcpyHostToDevice, stream) != hipSuccess)
-        return -1;
-    si_writeback_desc w{};
-    w.wire = d;
-    w.wire_stride = job->stride;
-    w.bytes = bytes;
-    w.nrec = n;
-    w.n_k = kind == 0 ? n : 0;
-    w.iv_words = nullptr;
-    w.ticket_base = job->t0;
-    w.cache_k = dev_cache;
-    w.cache_v = dev_cache;
-    w.slot_bytes = slot_bytes;
-    w.nslots = nslots;
-    w.slots = reinterpret_cast<const int64_t*>(d + wire);
-    w.codec_bits = codec_bits;
-    w.heads = heads;
-    w.head_dim = head_dim;
-    w.layer = layer;
-    w.staging = job->buf->stage;
-    w.fail_count = reinterpret_cast<uint32_t*>(d + job->fail_off);
-    if (secure_infer_gpu_writeback_layer(stream, s, &w) != 0) return -1;
-    DeviceState* ds = b->ds;
-    if (hipEventRecord(job->buf->ev_a, stream) != hipSuccess ||
-        hipStreamWaitEvent(ds->d2h, job->buf->ev_a, 0) != hipSuccess ||
-        hipMemcpyAsync(h, d, wire, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
-        hipMemcpyAsync(h + job->fail_off, d + job->fail_off, 16, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
-        hipEventRecord(job->buf->ev_b, ds->d2h) != hipSuccess)
-        return -1;
-    if (std::find(b->streams.begin(), b->streams.end(), stream) == b->streams.end())
-        b->streams.push_back(stream);
-    b->jobs.push_back(std::move(job));
+    for (uint32_t r = 0; r < n; ++r) {
+        J->recs.push_back({static_cast<uint8_t*>(host_base) + uint64_t(mapping[2 * r + 1]) * host_block_bytes,
+                           t0 + r});
+        J->slot_ids.push_back(mapping[2 * r]);
+    }
+    J->cache[kind] = dev_cache;
+    J->n += n;
+    if (kind == 0) J->n_k += n;
     return 0;
 }
 
+// The group bracket is kept for the reference's callers; records of several
+// groups can share a launch, issued at the latest by the batch's device
+// barrier or end.
 int secure_infer_d2h_group_end(void)
 {
     D2HBatch* b = t_batch.get();
     if (!b || !b->group_open) return 0;
     b->group_open = false;
-    const uint32_t per_task = 4;
-    std::vector<std::function<void()>> tasks;
-    for (size_t j = b->group_first; j < b->jobs.size(); ++j) {
-        D2HJob* job = b->jobs[j].get();
-        for (uint32_t r0 = 0; r0 < job->n; r0 += per_task) {
-            const uint32_t r1 = std::min(job->n, r0 + per_task);
-            tasks.emplace_back([b, job, r0, r1] { verify_records(b, job, r0, r1); });
-        }
-    }
-    {
-        std::lock_guard<std::mutex> g(b->m);
-        b->pending += tasks.size();
-    }
-    Pool::get().submit_all(tasks);
     return 0;
 }
 
@@ -1558,6 +1780,7 @@ int secure_infer_d2h_batch_device_barrier(void)
 {
     D2HBatch* b = t_batch.get();
     if (!b || b->group_open) return -1;
+    if (d2h_issue(b) != 0) return -1;
     hipEvent_t join = nullptr;
     if (hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess) return -1;
     b->joins.push_back(join);
@@ -1572,19 +1795,17 @@ int secure_infer_d2h_batch_end(void)
     if (!t_batch) return 0;
     if (t_batch->group_open) return -1;
     std::unique_ptr<D2HBatch> b = std::move(t_batch);
+    const bool issued = d2h_issue(b.get()) == 0;
     {
         std::unique_lock<std::mutex> g(b->m);
-        b->cv.wait(g, [&] { return b->pending == 0; });
+        b->cv.wait(g, [&] { return b->pending_tasks == 0; });
     }
     for (hipEvent_t e : b->joins) {
         (void)hipEventSynchronize(e);
         (void)hipEventDestroy(e);
     }
-    {
-        std::lock_guard<std::mutex> g(b->ds->pool_lock);
-        for (auto& job : b->jobs) b->ds->free_bufs.push_back(std::move(job->buf));
-    }
-    return b->failures.load() ? -1 : 0;
+    return (issued && b->failures.load() == 0) ? 0 : -1;
 }
 
 }  // extern "C"
+

@@ -150,6 +150,78 @@ def test_d2h_store_codec(bits):
             assert np.array_equal(dst[0][k][c].numpy(), O.codec_encode(blocks[k][sl], bits, k, layer))
 
 
+def test_d2h_launch_with_a_ticket_gap():
+    """A batch's D2H swaps of one layer share a launch; a ticket reserved by
+    someone else between them (here: new_transfer_ticket) makes the launch
+    carry explicit per-record IV words.  Host authentication must still pass
+    and the pools end bit-exact."""
+    rng = np.random.default_rng(151)
+    heads, dim, nslots, ncpu = 2, 128, 12, 10
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 6, max_record_bytes=shape.record_bytes)
+    k = torch.from_numpy(np.stack(W.bf16_blocks(rng, nslots, heads, dim)).view(np.int16)).to(DEV)
+    v = torch.from_numpy(np.stack(W.bf16_blocks(rng, nslots, heads, dim)).view(np.int16)).to(DEV)
+    hk = torch.zeros((ncpu, 128, heads, dim), dtype=torch.int16)
+    hv = torch.zeros_like(hk)
+    m = torch.tensor([[3, 0], [11, 9], [5, 4]], dtype=torch.int64)
+    L = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    bb = hk[0].numel() * 2
+
+    def swap(cache, pool, kind):
+        return L.secure_infer_d2h_swap(ct.c_void_p(stream), sess._h, ct.c_void_p(cache.data_ptr()), bb, nslots,
+                                       ct.c_void_p(pool.data_ptr()), bb, ncpu, ct.c_void_p(m.data_ptr()), 3, kind,
+                                       0, 0, heads, dim)
+
+    assert L.secure_infer_d2h_batch_begin(6) > 0
+    for cache, pool, kind in ((k, hk, 0), (v, hv, 1)):
+        assert L.secure_infer_d2h_group_begin(3) > 0
+        assert swap(cache, pool, kind) == 0
+        assert L.secure_infer_d2h_group_end() == 0
+        si.new_transfer_ticket()  # a gap between the K and the V tickets
+    assert L.secure_infer_d2h_batch_device_barrier() == 0
+    assert L.secure_infer_d2h_batch_end() == 0
+    kk, vv = host(k), host(v)
+    for sl, c in m.tolist():
+        assert np.array_equal(hk[c].numpy(), kk[sl]) and np.array_equal(hv[c].numpy(), vv[sl])
+
+
+D2H_INFLIGHT_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import secure_infer_amd as si
+heads, dim, nlayers = 2, 128, 12
+shape = si.LayerShape(heads, dim, 4)
+sess = si.GcmSession(bytes(16), b"abcd", 0, max_record_bytes=shape.record_bytes)
+g = torch.Generator(device="cuda").manual_seed(5)
+src = [tuple(torch.randn((16, 128, heads, dim), generator=g, device="cuda").to(torch.bfloat16) for _ in range(2))
+       for _ in range(nlayers)]
+dst = [tuple(torch.zeros((16, shape.record_bytes), dtype=torch.uint8) for _ in range(2)) for _ in range(nlayers)]
+m = torch.stack([torch.arange(16).flip(0), torch.arange(16)], 1).contiguous()
+si.D2HTransfer(sess, shape).store(src, dst, m, layers=list(range(nlayers)))
+ref = [tuple(torch.zeros_like(t) for t in d) for d in dst]
+for layer in range(nlayers):
+    si.D2HTransfer(sess, shape).store([src[layer]], [ref[layer]], m, layers=[layer])
+assert all(torch.equal(a, b) for d, r in zip(dst, ref) for a, b in zip(d, r))
+assert all(bool(t.any()) for d in dst for t in d)
+print("done")
+"""
+
+
+def test_d2h_batch_beyond_the_inflight_bound():
+    """SECURE_INFER_D2H_INFLIGHT_MB=1: every launch of a 12-layer int4 store
+    waits for the previous one's host authentication; the pools equal those
+    of one batch per layer."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    env = dict(os.environ, SECURE_INFER_D2H_INFLIGHT_MB="1")
+    out = subprocess.run([sys.executable, "-c", D2H_INFLIGHT_SCRIPT, str(Path(__file__).resolve().parent.parent)],
+                         env=env, capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0 and "done" in out.stdout, out.stderr[-2000:]
+
+
 def test_d2h_api_semantics():
     L = _lib.load()
     assert L.secure_infer_d2h_batch_end() == 0            # no batch: nothing to do
