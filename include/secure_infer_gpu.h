@@ -109,6 +109,20 @@ int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt
                                     uint64_t session_nonce, uint64_t max_record_bytes,
                                     si_session** out);
 int secure_infer_gpu_session_destroy(si_session* session);
+/* The reference's device session (secure_infer_experimental_device_session,
+ * secure_infer.cpp:447-521; device half key_agreement.aicpu:9-49): an X25519
+ * exchange between the host (OpenSSL) and a device kernel agrees on the
+ * AES-128 key, key = BLAKE2b-16 keyed by the shared secret over
+ * "SecureInfer X25519 BLAKE2b test v1" || host public || device public ||
+ * challenge; the device proves it with BLAKE2b-32 keyed by the key over the
+ * challenge; the IV salt is BLAKE2b-4 keyed by the shared secret over
+ * "SecureInfer IV salt v1".  Only public values, the challenge, a host seed
+ * and the proof cross PCIe: the device derives its X25519 secret from the
+ * clock jitter of racing waves mixed with the seed (HIP exposes no device
+ * random source), keeps the key in device memory and builds the kernels'
+ * context (round keys, H, GHASH tables) there.  The host keeps its own copy
+ * for OpenSSL sealing and verification.  0, or -1 (nothing created). */
+int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_bytes, si_session** out);
 /* H = E_K(0^128) of the session (host copy, 16 B). */
 int secure_infer_gpu_session_hash_subkey(const si_session* session, uint8_t out[16]);
 
@@ -318,6 +332,16 @@ int secure_infer_h2d_swap(hipStream_t stream, si_session* session, const void* h
  * authentication.  0 shots disarms.  Production code never calls them. */
 int secure_infer_test_tamper_h2d(int32_t layer, int32_t kind, int64_t host_block, uint32_t shots);
 int secure_infer_test_tamper_d2h(uint32_t shots);
+/* Test-only checks of the session agreement's device code (no reference
+ * counterpart): X25519 (RFC 7748) and keyed BLAKE2b (RFC 7693) run by one
+ * device lane; the kernels' context built on the device (on_device = 1) or
+ * on the host (0) from a key, written to out (cap bytes; out = NULL returns
+ * the size).  Production code never calls them. */
+int secure_infer_test_x25519(const uint8_t scalar[32], const uint8_t u[32], uint8_t out[32]);
+int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_t* msg, uint64_t msg_len,
+                              uint8_t* out, uint32_t out_len);
+int64_t secure_infer_test_context_image(const uint8_t key[16], uint64_t max_record_bytes, int on_device,
+                                        void* out, uint64_t cap);
 
 /* Ahead-of-demand sealing (the reference's CPU ciphertext prefetch pool,
  * secure_infer.cpp:3264-3710): queues the host seal of the swap with these

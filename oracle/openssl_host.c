@@ -176,3 +176,55 @@ int64_t si_ossl_layer(int direction, const uint8_t key[16], const uint8_t* iv12,
     free(tid);
     return (int64_t)(b.tv_sec - a.tv_sec) * 1000000000LL + (b.tv_nsec - a.tv_nsec);
 }
+
+/*
+ * X25519 and keyed BLAKE2b through OpenSSL (EVP_PKEY_X25519, EVP_MAC
+ * "BLAKE2BMAC"): an implementation independent of the restatement in
+ * oracle/agreement.py and of the device code, for the session key agreement
+ * (secure_infer.cpp:447-521, key_agreement.aicpu:9-49).
+ */
+#include <openssl/core_names.h>
+#include <openssl/params.h>
+
+int si_ossl_x25519(const uint8_t scalar[32], const uint8_t u[32], uint8_t out[32])
+{
+    EVP_PKEY* priv = EVP_PKEY_new_raw_private_key(EVP_PKEY_X25519, NULL, scalar, 32);
+    EVP_PKEY* peer = EVP_PKEY_new_raw_public_key(EVP_PKEY_X25519, NULL, u, 32);
+    EVP_PKEY_CTX* ctx = priv ? EVP_PKEY_CTX_new(priv, NULL) : NULL;
+    size_t len = 32;
+    int rc = -1;
+    if (ctx && peer && EVP_PKEY_derive_init(ctx) == 1 && EVP_PKEY_derive_set_peer(ctx, peer) == 1 &&
+        EVP_PKEY_derive(ctx, out, &len) == 1 && len == 32)
+        rc = 0;
+    EVP_PKEY_CTX_free(ctx);
+    EVP_PKEY_free(peer);
+    EVP_PKEY_free(priv);
+    return rc;
+}
+
+int si_ossl_x25519_public(const uint8_t scalar[32], uint8_t out[32])
+{
+    EVP_PKEY* priv = EVP_PKEY_new_raw_private_key(EVP_PKEY_X25519, NULL, scalar, 32);
+    size_t len = 32;
+    int rc = (priv && EVP_PKEY_get_raw_public_key(priv, out, &len) == 1 && len == 32) ? 0 : -1;
+    EVP_PKEY_free(priv);
+    return rc;
+}
+
+int si_ossl_blake2b_keyed(const uint8_t* key, size_t key_len, const uint8_t* msg, size_t msg_len, uint8_t* out,
+                          size_t out_len)
+{
+    EVP_MAC* mac = EVP_MAC_fetch(NULL, "BLAKE2BMAC", NULL);
+    EVP_MAC_CTX* ctx = mac ? EVP_MAC_CTX_new(mac) : NULL;
+    OSSL_PARAM params[2];
+    params[0] = OSSL_PARAM_construct_size_t(OSSL_MAC_PARAM_SIZE, &out_len);
+    params[1] = OSSL_PARAM_construct_end();
+    size_t len = 0;
+    int rc = -1;
+    if (ctx && EVP_MAC_init(ctx, key, key_len, params) == 1 && EVP_MAC_update(ctx, msg, msg_len) == 1 &&
+        EVP_MAC_final(ctx, out, &len, out_len) == 1 && len == out_len)
+        rc = 0;
+    EVP_MAC_CTX_free(ctx);
+    EVP_MAC_free(mac);
+    return rc;
+}

@@ -48,6 +48,10 @@ SIGNATURES = {
     "secure_infer_gpu_auth_gate_do": ([_v, _v, _v, _u64], _i),
     "secure_infer_gpu_session_create": ([_v, _v, _u64, _u64, ct.POINTER(_v)], _i),
     "secure_infer_gpu_session_destroy": ([_v], _i),
+    "secure_infer_gpu_session_agree": ([_u64, _u64, ct.POINTER(_v)], _i),
+    "secure_infer_test_x25519": ([_v, _v, _v], _i),
+    "secure_infer_test_blake2b": ([_v, _u32, _v, _u64, _v, _u32], _i),
+    "secure_infer_test_context_image": ([_v, _u64, _i, _v, _u64], ct.c_int64),
     "secure_infer_gpu_session_hash_subkey": ([_v, _v], _i),
     "secure_infer_gpu_reload_layer": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),
     "secure_infer_gpu_reload_layer_noalloc": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),

@@ -15,7 +15,7 @@ OUT = PKG / "_lib" / "libsecure_infer.so"
 SELFTEST_SRC = ROOT / "tests" / "csrc" / "codec_cvt_sweep.hip"
 SELFTEST_OUT = ROOT / "tests" / "_build" / "libsi_selftest.so"
 
-SOURCES = ["si_gcm.hip", "si_codec.hip", "si_api.cpp", "si_host.cpp"]
+SOURCES = ["si_gcm.hip", "si_codec.hip", "si_agree.hip", "si_api.cpp", "si_host.cpp"]
 LIBS = ["-lcrypto", "-lpthread"]
 
 FLAGS = [

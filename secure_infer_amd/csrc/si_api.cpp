@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <initializer_list>
+#include <utility>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -17,6 +19,12 @@
 #include "si_device.h"
 #include "si_host.h"
 #include "si_kernels.h"
+
+#include <openssl/core_names.h>
+#include <openssl/crypto.h>
+#include <openssl/evp.h>
+#include <openssl/params.h>
+#include <openssl/rand.h>
 
 namespace {
 
@@ -181,7 +189,19 @@ struct DevCtx {
     }
 };
 
-std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], uint32_t npow)
+// Te0 of the record kernels' T-table AES (public: S-box column 2, 1, 1, 3).
+void te0_table(uint32_t te0[256])
+{
+    const uint8_t* S = sbox().s;
+    for (int x = 0; x < 256; ++x) {
+        const uint32_t s = S[x], s2 = gf8_mul(uint8_t(s), 2), s3 = gf8_mul(uint8_t(s), 3);
+        te0[x] = s2 | (s << 8) | (s << 16) | (s3 << 24);
+    }
+}
+
+// The record kernels' context image: round keys, Te0, H, the powers of H and
+// the 4-bit tables of H^T, H^2T, H^UT, H^2UT.
+std::vector<uint8_t> ctx_image(const uint8_t key[16], const uint8_t h[16], uint32_t npow)
 {
     std::vector<uint8_t> img(sizeof(si::GcmCtx) + size_t(npow) * 16, 0);
     auto* c = reinterpret_cast<si::GcmCtx*>(img.data());
@@ -191,11 +211,7 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
         c->rk[i] = le32(rk + 4 * i);
         c->rk16[i] = (c->rk[i] << 16) | (c->rk[i] >> 16);
     }
-    const uint8_t* S = sbox().s;
-    for (int x = 0; x < 256; ++x) {
-        const uint32_t s = S[x], s2 = gf8_mul(uint8_t(s), 2), s3 = gf8_mul(uint8_t(s), 3);
-        c->te0[x] = s2 | (s << 8) | (s << 16) | (s3 << 24);
-    }
+    te0_table(c->te0);
     for (int k = 0; k < 4; ++k) c->h[k] = le32(h + 4 * k);
     c->npow = npow;
     Blk hb;
@@ -233,6 +249,12 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
     put(c->gh4b, ht2);
     put(c->gh4u, htu);
     put(c->gh4u2, htu2);
+    return img;
+}
+
+std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], uint32_t npow)
+{
+    const std::vector<uint8_t> img = ctx_image(key, h, npow);
     auto out = std::make_unique<DevCtx>();
     if (hipMalloc(&out->dev, img.size()) != hipSuccess) return nullptr;
     if (hipMemcpy(out->dev, img.data(), img.size(), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
@@ -573,6 +595,219 @@ int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt
     s->max_record_bytes = max_record_bytes;
     *out = s.release();
     return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- session key agreement
+
+namespace {
+
+// Host half of the agreement through OpenSSL (the reference uses Monocypher's
+// crypto_x25519 / crypto_blake2b_keyed, secure_infer.cpp:466-499).
+bool x25519_public(const uint8_t secret[32], uint8_t out[32])
+{
+    EVP_PKEY* k = EVP_PKEY_new_raw_private_key(EVP_PKEY_X25519, nullptr, secret, 32);
+    size_t len = 32;
+    const bool ok = k && EVP_PKEY_get_raw_public_key(k, out, &len) == 1 && len == 32;
+    EVP_PKEY_free(k);
+    return ok;
+}
+
+bool x25519_shared(const uint8_t secret[32], const uint8_t peer[32], uint8_t out[32])
+{
+    EVP_PKEY* k = EVP_PKEY_new_raw_private_key(EVP_PKEY_X25519, nullptr, secret, 32);
+    EVP_PKEY* p = EVP_PKEY_new_raw_public_key(EVP_PKEY_X25519, nullptr, peer, 32);
+    EVP_PKEY_CTX* c = k ? EVP_PKEY_CTX_new(k, nullptr) : nullptr;
+    size_t len = 32;
+    const bool ok = c && p && EVP_PKEY_derive_init(c) == 1 && EVP_PKEY_derive_set_peer(c, p) == 1 &&
+                    EVP_PKEY_derive(c, out, &len) == 1 && len == 32;
+    EVP_PKEY_CTX_free(c);
+    EVP_PKEY_free(p);
+    EVP_PKEY_free(k);
+    return ok;
+}
+
+// BLAKE2b keyed by `key`, `out_len` bytes, over the concatenation of parts.
+bool blake2b_keyed(const uint8_t* key, size_t key_len, std::initializer_list<std::pair<const void*, size_t>> parts,
+                   uint8_t* out, size_t out_len)
+{
+    EVP_MAC* mac = EVP_MAC_fetch(nullptr, "BLAKE2BMAC", nullptr);
+    EVP_MAC_CTX* c = mac ? EVP_MAC_CTX_new(mac) : nullptr;
+    OSSL_PARAM params[2] = {OSSL_PARAM_construct_size_t(OSSL_MAC_PARAM_SIZE, &out_len), OSSL_PARAM_construct_end()};
+    bool ok = c && EVP_MAC_init(c, key, key_len, params) == 1;
+    for (const auto& part : parts) ok = ok && EVP_MAC_update(c, static_cast<const uint8_t*>(part.first), part.second) == 1;
+    size_t len = 0;
+    ok = ok && EVP_MAC_final(c, out, &len, out_len) == 1 && len == out_len;
+    EVP_MAC_CTX_free(c);
+    EVP_MAC_free(mac);
+    return ok;
+}
+
+const char kAgreeInfo[] = "SecureInfer X25519 BLAKE2b test v1";
+const char kSaltInfo[] = "SecureInfer IV salt v1";
+
+// Builds the record kernels' context on the device from a device-resident
+// key (the key's bytes never leave the device).
+std::unique_ptr<DevCtx> build_ctx_on_device(hipStream_t stream, const uint8_t* dev_key, uint32_t npow)
+{
+    uint32_t te0[256];
+    te0_table(te0);
+    uint32_t* d_te0 = nullptr;
+    auto out = std::make_unique<DevCtx>();
+    const size_t bytes = sizeof(si::GcmCtx) + size_t(npow) * 16;
+    bool ok = hipMalloc(reinterpret_cast<void**>(&out->dev), bytes) == hipSuccess &&
+              hipMalloc(reinterpret_cast<void**>(&d_te0), sizeof(te0)) == hipSuccess &&
+              hipMemcpyAsync(d_te0, te0, sizeof(te0), hipMemcpyHostToDevice, stream) == hipSuccess &&
+              si::launch_ctx_build(stream, dev_key, d_te0, out->dev, npow) == hipSuccess &&
+              hipStreamSynchronize(stream) == hipSuccess;
+    if (d_te0) (void)hipFree(d_te0);
+    if (!ok) return nullptr;
+    out->npow = npow;
+    return out;
+}
+
+// Device buffers of one agreement, freed (the key zeroed first) on exit.
+struct AgreeBufs {
+    hipStream_t stream = nullptr;
+    si::AgreeIo* io = nullptr;
+    uint8_t* key = nullptr;
+    uint32_t* pool = nullptr;
+    uint32_t* counter = nullptr;
+    ~AgreeBufs()
+    {
+        if (stream && key) {
+            (void)si::launch_zero_bytes(stream, key, 16);
+            (void)hipStreamSynchronize(stream);
+        }
+        for (void* p : {static_cast<void*>(io), static_cast<void*>(key), static_cast<void*>(pool),
+                        static_cast<void*>(counter)})
+            if (p) (void)hipFree(p);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_bytes, si_session** out)
+{
+    if (!out || max_record_bytes == 0 || max_record_bytes > SI_MAX_RECORD_BYTES) return -1;
+    uint8_t secret[32], host_public[32], shared[32], key[16], expected[32], salt[4], h[16], rk[176], zero[16] = {0};
+    si::AgreeIo io{};
+    int rc = -1;
+    std::unique_ptr<si_session> s;
+    {
+        AgreeBufs b;
+        if (RAND_bytes(secret, 32) != 1 || RAND_bytes(io.challenge, 32) != 1 || RAND_bytes(io.seed, 32) != 1 ||
+            !x25519_public(secret, host_public))
+            goto done;
+        memcpy(io.host_public, host_public, 32);
+        io.status = -1;
+        // A private stream, as the reference's setup stream: nothing the
+        // caller has queued is waited for.
+        if (hipStreamCreateWithFlags(&b.stream, hipStreamNonBlocking) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&b.io), sizeof(si::AgreeIo)) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&b.key), 16) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&b.pool), SI_AGREE_POOL_WORDS * 4) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&b.counter), 4) != hipSuccess ||
+            hipMemcpyAsync(b.io, &io, sizeof(io), hipMemcpyHostToDevice, b.stream) != hipSuccess ||
+            si::launch_agree(b.stream, b.io, b.key, b.pool, b.counter) != hipSuccess ||
+            hipMemcpyAsync(&io, b.io, sizeof(io), hipMemcpyDeviceToHost, b.stream) != hipSuccess ||
+            hipStreamSynchronize(b.stream) != hipSuccess || io.status != 0)
+            goto done;
+        {
+            uint8_t nz = 0;
+            if (!x25519_shared(secret, io.device_public, shared)) goto done;
+            for (uint8_t v : shared) nz |= v;
+            if (!nz) goto done;
+        }
+        if (!blake2b_keyed(shared, 32,
+                           {{kAgreeInfo, sizeof(kAgreeInfo) - 1}, {host_public, 32}, {io.device_public, 32},
+                            {io.challenge, 32}},
+                           key, 16) ||
+            !blake2b_keyed(key, 16, {{io.challenge, 32}}, expected, 32) ||
+            !blake2b_keyed(shared, 32, {{kSaltInfo, sizeof(kSaltInfo) - 1}}, salt, 4) ||
+            CRYPTO_memcmp(expected, io.proof, 32) != 0)
+            goto done;
+        s = std::make_unique<si_session>();
+        s->ctx = build_ctx_on_device(b.stream, b.key, npow_for(max_record_bytes, 64));
+        if (!s->ctx) goto done;
+        // The host keeps its own copy of the agreed key for OpenSSL.
+        aes_expand(key, rk);
+        aes_encrypt(rk, zero, h);
+        memcpy(s->ctx->key, key, 16);
+        memcpy(s->ctx->h, h, 16);
+        s->salt_word = be32(salt);
+        s->session_nonce = session_nonce;
+        s->max_record_bytes = max_record_bytes;
+        rc = 0;
+    }
+done:
+    OPENSSL_cleanse(secret, sizeof(secret));
+    OPENSSL_cleanse(shared, sizeof(shared));
+    OPENSSL_cleanse(key, sizeof(key));
+    OPENSSL_cleanse(rk, sizeof(rk));
+    if (rc != 0) return -1;
+    *out = s.release();
+    return 0;
+}
+
+int64_t secure_infer_test_context_image(const uint8_t key[16], uint64_t max_record_bytes, int on_device, void* out,
+                                        uint64_t cap)
+{
+    if (!key || max_record_bytes == 0 || max_record_bytes > SI_MAX_RECORD_BYTES) return -1;
+    const uint32_t npow = npow_for(max_record_bytes, 64);
+    const uint64_t bytes = sizeof(si::GcmCtx) + uint64_t(npow) * 16;
+    if (!out) return int64_t(bytes);
+    if (cap < bytes) return -1;
+    if (!on_device) {
+        uint8_t rk[176], h[16], zero[16] = {0};
+        aes_expand(key, rk);
+        aes_encrypt(rk, zero, h);
+        const std::vector<uint8_t> img = ctx_image(key, h, npow);
+        memcpy(out, img.data(), bytes);
+        return int64_t(bytes);
+    }
+    hipStream_t st = nullptr;
+    uint8_t* d_key = nullptr;
+    bool ok = hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess &&
+              hipMalloc(reinterpret_cast<void**>(&d_key), 16) == hipSuccess &&
+              hipMemcpyAsync(d_key, key, 16, hipMemcpyHostToDevice, st) == hipSuccess;
+    std::unique_ptr<DevCtx> c = ok ? build_ctx_on_device(st, d_key, npow) : nullptr;
+    ok = c && hipMemcpy(out, c->dev, bytes, hipMemcpyDeviceToHost) == hipSuccess;
+    if (d_key) (void)hipFree(d_key);
+    if (st) (void)hipStreamDestroy(st);
+    return ok ? int64_t(bytes) : -1;
+}
+
+int secure_infer_test_x25519(const uint8_t scalar[32], const uint8_t u[32], uint8_t out[32])
+{
+    if (!scalar || !u || !out) return -1;
+    uint8_t* d = nullptr;
+    bool ok = hipMalloc(reinterpret_cast<void**>(&d), 96) == hipSuccess &&
+              hipMemcpy(d, scalar, 32, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(d + 32, u, 32, hipMemcpyHostToDevice) == hipSuccess &&
+              si::launch_x25519_test(nullptr, d, d + 32, d + 64) == hipSuccess &&
+              hipMemcpy(out, d + 64, 32, hipMemcpyDeviceToHost) == hipSuccess;
+    if (d) (void)hipFree(d);
+    return ok ? 0 : -1;
+}
+
+int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_t* msg, uint64_t msg_len,
+                              uint8_t* out, uint32_t out_len)
+{
+    if ((key_len && !key) || key_len > 64 || (msg_len && !msg) || !out || out_len == 0 || out_len > 64) return -1;
+    uint8_t* d = nullptr;
+    const uint64_t n = 64 + 64 + msg_len + 1;
+    bool ok = hipMalloc(reinterpret_cast<void**>(&d), n) == hipSuccess &&
+              (key_len == 0 || hipMemcpy(d, key, key_len, hipMemcpyHostToDevice) == hipSuccess) &&
+              (msg_len == 0 || hipMemcpy(d + 128, msg, msg_len, hipMemcpyHostToDevice) == hipSuccess) &&
+              si::launch_blake2b_test(nullptr, d, key_len, d + 128, msg_len, d + 64, out_len) == hipSuccess &&
+              hipMemcpy(out, d + 64, out_len, hipMemcpyDeviceToHost) == hipSuccess;
+    if (d) (void)hipFree(d);
+    return ok ? 0 : -1;
 }
 
 int secure_infer_gpu_session_destroy(si_session* s)

@@ -97,4 +97,26 @@ struct CodecBatch {
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b);
 hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b);
 
+// Session key agreement and device-side context set-up (si_agree.hip).
+struct AgreeIo {
+    uint8_t host_public[32];    // in
+    uint8_t challenge[32];      // in
+    uint8_t seed[32];           // in: mixed with the device's clock jitter
+    uint8_t device_public[32];  // out
+    uint8_t proof[32];          // out: BLAKE2b-32 keyed by the key over the challenge
+    int32_t status;             // out: 0 done; 1 or 2 failed (no secret / zero shared secret)
+    uint32_t pad[7];
+};
+// Entropy pool (`pool`: SI_AGREE_POOL_WORDS u32, `counter`: one u32) and the
+// agreement; the 16-byte key is written to `key_out` (device memory only).
+#define SI_AGREE_POOL_WORDS (512u * 256u)
+hipError_t launch_agree(hipStream_t stream, AgreeIo* io, uint8_t* key_out, uint32_t* pool, uint32_t* counter);
+// GcmCtx (+ npow powers) from a device-resident 16-byte key; te0 is public.
+hipError_t launch_ctx_build(hipStream_t stream, const uint8_t* key, const uint32_t* te0, GcmCtx* ctx,
+                            uint32_t npow);
+hipError_t launch_zero_bytes(hipStream_t stream, uint8_t* p, uint32_t n);
+hipError_t launch_x25519_test(hipStream_t stream, const uint8_t* scalar, const uint8_t* u, uint8_t* out);
+hipError_t launch_blake2b_test(hipStream_t stream, const uint8_t* key, uint32_t key_len, const uint8_t* msg,
+                               uint64_t msg_len, uint8_t* out, uint32_t out_len);
+
 }  // namespace si

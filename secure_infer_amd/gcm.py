@@ -257,6 +257,29 @@ class GcmSession:
         _check(lib().secure_infer_gpu_session_hash_subkey(self._h, out), "hash_subkey")
         self.hash_subkey = bytes(out)
 
+    @classmethod
+    def agree(cls, session_nonce: int = 0, max_record_bytes: int = 1 << 20) -> "GcmSession":
+        """A session whose key and IV salt are agreed with the device by an
+        X25519 + BLAKE2b exchange (the reference's device session,
+        secure_infer.cpp:447-521, key_agreement.aicpu:9-49): the key is
+        derived on the device and never crosses PCIe; the library's host
+        runtime keeps its own copy for OpenSSL.  ``key`` and ``iv_salt`` are
+        None: nothing outside the library learns them."""
+        self = cls.__new__(cls)
+        self.key = None
+        self.iv_salt = None
+        self.session_nonce = int(session_nonce)
+        self.max_record_bytes = int(max_record_bytes)
+        h = ct.c_void_p()
+        self._h = ct.c_void_p()
+        _check(lib().secure_infer_gpu_session_agree(self.session_nonce, self.max_record_bytes, ct.byref(h)),
+               "session_agree")
+        self._h = h
+        out = (ct.c_uint8 * 16)()
+        _check(lib().secure_infer_gpu_session_hash_subkey(self._h, out), "hash_subkey")
+        self.hash_subkey = bytes(out)
+        return self
+
     def close(self) -> None:
         if self._h:
             lib().secure_infer_gpu_session_destroy(self._h)
