@@ -326,10 +326,14 @@ def test_reference_ticket_order_layer_authenticates(ranges):
     assert torch.equal(cv.index_select(0, idx), want[nb:])
 
 
-def test_causal_groups_through_the_host_pipeline(ranges):
-    """NativeTransfer with 16-block causal groups over 41 host blocks: every
-    block lands bit-exactly and tickets advance by one per record."""
-    rng = np.random.default_rng(310)
+@pytest.mark.parametrize("slices", [1, 2])
+def test_causal_groups_through_the_host_pipeline(ranges, slices):
+    """NativeTransfer with 16-block causal groups over 41 host blocks, on one
+    stream or striped over two slice streams (native_layerwise.py:113-129):
+    every block lands bit-exactly and tickets advance by one per record, plus
+    one for a V record sealed with a one-shot fault and sealed again by the
+    strict retry."""
+    rng = np.random.default_rng(310 + slices)
     heads, dim, ncpu, nslots, layer = 2, 128, 41, 64, 1
     shape = si.LayerShape(heads, dim)
     sess = si.GcmSession(KEY, SALT, 5, max_record_bytes=shape.record_bytes)
@@ -339,12 +343,14 @@ def test_causal_groups_through_the_host_pipeline(ranges):
     ck, cv = caches(nslots, heads, dim)
     slot_ids = rng.permutation(nslots)[:ncpu]
     mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
-    nt = si.NativeTransfer(sess, shape, causal_group_blocks=16)
+    streams = None if slices == 1 else [torch.cuda.current_stream(), torch.cuda.Stream()]
+    nt = si.NativeTransfer(sess, shape, streams=streams, causal_group_blocks=16)
     nt.layer = layer
+    si.inject_h2d_tamper(layer=layer, kind=1, host_block=30, shots=1)
     t_before = si.new_transfer_ticket()
     nt.single_layer_kv_transfer(((hk, hv), mapping), (ck, cv))
     assert nt.layer == layer + 1
     assert nt.wait_layer(layer) == 0
-    assert si.new_transfer_ticket() - t_before == 2 * ncpu + 1
+    assert si.new_transfer_ticket() - t_before == 2 * ncpu + 1 + 1
     idx = dev(slot_ids.astype(np.int64))
     assert torch.equal(ck.index_select(0, idx).cpu(), hk) and torch.equal(cv.index_select(0, idx).cpu(), hv)
