@@ -178,6 +178,8 @@ struct FixedMul {
 
 // ---------------------------------------------------------------- contexts
 
+// A session's device context and the host's copies of its key and H.  Both
+// are wiped when the context goes (the device copy holds the round keys).
 struct DevCtx {
     si::GcmCtx* dev = nullptr;
     uint32_t npow = 0;
@@ -185,7 +187,12 @@ struct DevCtx {
     uint8_t h[16];
     ~DevCtx()
     {
-        if (dev) (void)hipFree(dev);
+        if (dev) {
+            (void)hipMemset(dev, 0, sizeof(si::GcmCtx) + size_t(npow) * 16);
+            (void)hipFree(dev);
+        }
+        OPENSSL_cleanse(key, sizeof(key));
+        OPENSSL_cleanse(h, sizeof(h));
     }
 };
 
