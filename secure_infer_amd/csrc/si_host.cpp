@@ -37,7 +37,7 @@
 //    secure_infer.cpp:3264-3710): secure_infer_h2d_prefetch seals a swap's
 //    records on the worker pool before the swap is issued, under tickets
 //    reserved then; the matching secure_infer_h2d_swap only copies them.
-//  * An optional per-swap ledger (SECURE_INFER_H2D_PROFILE=<csv path>) of
+//  * An optional per-launch ledger (SECURE_INFER_H2D_PROFILE=<csv path>) of
 //    host seal time, H2D copy time and kernel time, like the reference's
 //    per-copy profile rows (secure_infer.cpp:1826-1951, 6085-6137).
 //  * Every block id is range-checked on the host before any work: a swap
