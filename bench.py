@@ -420,15 +420,22 @@ def main():
     staging = torch.zeros(nrec * tag_off, dtype=torch.uint8, device=dev) if bits else None
     fails = torch.zeros(L, dtype=torch.int32, device=dev)
 
+    # Each layer's launch is prepared once (descriptor built and checked), as
+    # a serving loop with fixed buffers does; a step only calls the library.
+    launch_stream = si.gcm._stream(None)
+    wb_prep = [sess.prepare_writeback_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1],
+                                            slots2[layer], iv_words_dev=ivw[layer], codec_bits=bits, heads=H,
+                                            head_dim=D, layer=layer, staging=staging) for layer in range(L)]
+    rl_prep = [sess.prepare_reload_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1],
+                                         slots2[layer], iv_words_dev=ivw[layer], codec_bits=bits, heads=H,
+                                         head_dim=D, layer=layer, staging=staging,
+                                         fail_count=fails[layer:layer + 1]) for layer in range(L)]
+
     def writeback_layer(layer):
-        sess.writeback_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1], slots2[layer],
-                             iv_words_dev=ivw[layer], codec_bits=bits, heads=H, head_dim=D,
-                             layer=layer, staging=staging)
+        wb_prep[layer].launch(launch_stream)
 
     def reload_layer(layer):
-        sess.reload_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1], slots2[layer],
-                          iv_words_dev=ivw[layer], codec_bits=bits, heads=H, head_dim=D,
-                          layer=layer, staging=staging, fail_count=fails[layer:layer + 1])
+        rl_prep[layer].launch(launch_stream)
 
     sample_layers = sorted({0, L // 2, L - 1})
     blocks_host = {l: torch.stack([cache[l, k][slots[l]] for k in range(2)]).view(torch.int16).cpu().numpy()

@@ -6,7 +6,7 @@ tensors.  See ``secure_infer_amd.gcm``.
 """
 from .gcm import (  # noqa: F401
     AAD_BYTES, CODEC_MODES, SI_CODEC_INT4, SI_CODEC_INT8, SI_CODEC_NONE, D2HTransfer, GcmSession,
-    LayerShape, NativeTransfer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
+    LayerShape, NativeTransfer, PreparedLayer, aes_ctr, auth_gate, build_gcm_aad, clear_host_ranges, codec_width,
     derive_transfer_iv, drain_h2d_profile_after_job, flush_completed_h2d_profile, pause_h2d_profile, gcm_decrypt_verify,
     gcm_encrypt_tag, gcm_verify_only, gcm_verify_xor,
     inject_d2h_tamper, inject_h2d_tamper, iv_words, keystream, layer_bits, new_transfer_ticket,

@@ -297,12 +297,15 @@ class GcmSession:
     def record_iv(self, ticket: int) -> tuple[int, int, int, int]:
         return iv_words(derive_transfer_iv(self.base_iv(), ticket, 0, self.session_nonce))
 
-    def reload_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
-                     cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
-                     ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
-                     codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
-                     layer: int = 0, staging: torch.Tensor | None = None,
-                     fail_count: torch.Tensor | None = None, stream=None) -> None:
+    def prepare_reload_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
+                             cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
+                             ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
+                             codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
+                             layer: int = 0, staging: torch.Tensor | None = None,
+                             fail_count: torch.Tensor | None = None) -> "PreparedLayer":
+        """The checked descriptor of one reload layer, launched by
+        ``.launch(stream)`` as often as needed (buffers with fixed addresses, as
+        a serving loop keeps them); the tensors are kept alive with it."""
         for t, name in ((wire, "wire"), (cache_k, "cache_k"), (cache_v, "cache_v"),
                         (slots, "slots")):
             _dev(t, name)
@@ -323,15 +326,27 @@ class GcmSession:
             codec_bits=codec_bits, heads=heads, head_dim=head_dim, layer=layer,
             staging=None if staging is None else staging.data_ptr(),
             fail_count=None if fail_count is None else fail_count.data_ptr())
-        _check(lib().secure_infer_gpu_reload_layer(_stream(stream), self._h, ct.byref(d)),
-               "reload_layer")
+        return PreparedLayer(lib().secure_infer_gpu_reload_layer, self, d,
+                             (wire, cache_k, cache_v, slots, iv_words_dev, staging, fail_count), "reload_layer")
 
-    def writeback_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
-                        cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
-                        ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
-                        codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
-                        layer: int = 0, staging: torch.Tensor | None = None,
-                        fail_count: torch.Tensor | None = None, stream=None) -> None:
+    def reload_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
+                     cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
+                     ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
+                     codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
+                     layer: int = 0, staging: torch.Tensor | None = None,
+                     fail_count: torch.Tensor | None = None, stream=None) -> None:
+        """One layer of authenticated reload of device-resident wire records
+        (secure_infer_gpu_reload_layer); arguments as prepare_reload_layer."""
+        self.prepare_reload_layer(wire, nbytes, nrec, n_k, cache_k, cache_v, slots, ticket_base, iv_words_dev,
+                                  codec_bits, heads, head_dim, layer, staging, fail_count).launch(stream)
+
+    def prepare_writeback_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
+                                cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
+                                ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
+                                codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
+                                layer: int = 0, staging: torch.Tensor | None = None,
+                                fail_count: torch.Tensor | None = None) -> "PreparedLayer":
+        """The checked descriptor of one writeback layer (see prepare_reload_layer)."""
         for t, name in ((wire, "wire"), (cache_k, "cache_k"), (cache_v, "cache_v"),
                         (slots, "slots")):
             _dev(t, name)
@@ -349,8 +364,41 @@ class GcmSession:
             codec_bits=codec_bits, heads=heads, head_dim=head_dim, layer=layer,
             staging=None if staging is None else staging.data_ptr(),
             fail_count=None if fail_count is None else fail_count.data_ptr())
-        _check(lib().secure_infer_gpu_writeback_layer(_stream(stream), self._h, ct.byref(d)),
-               "writeback_layer")
+        return PreparedLayer(lib().secure_infer_gpu_writeback_layer, self, d,
+                             (wire, cache_k, cache_v, slots, iv_words_dev, staging, fail_count), "writeback_layer")
+
+    def writeback_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
+                        cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
+                        ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
+                        codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
+                        layer: int = 0, staging: torch.Tensor | None = None,
+                        fail_count: torch.Tensor | None = None, stream=None) -> None:
+        """One layer of gather (+ quantise) + seal into device wire records
+        (secure_infer_gpu_writeback_layer); arguments as prepare_writeback_layer."""
+        self.prepare_writeback_layer(wire, nbytes, nrec, n_k, cache_k, cache_v, slots, ticket_base,
+                                     iv_words_dev, codec_bits, heads, head_dim, layer, staging,
+                                     fail_count).launch(stream)
+
+
+class PreparedLayer:
+    """A layer launch whose descriptor was built and checked once: launch()
+    only calls the library (about 7 us of host time for a codec layer; the
+    per-call checks and descriptor of reload_layer cost as much again, which
+    is more than a 24-us int4 layer leaves between launches)."""
+
+    def __init__(self, fn, session: GcmSession, desc, keep, what: str):
+        self._fn = fn
+        self._session = session
+        self._desc = desc
+        self._ref = ct.byref(desc)
+        self._keep = keep
+        self._what = what
+
+    def launch(self, stream=None) -> None:
+        """On `stream` (a torch stream, a raw handle, a ct.c_void_p, or None
+        for the current stream)."""
+        h = stream if isinstance(stream, ct.c_void_p) else _stream(stream)
+        _check(self._fn(h, self._session._h, self._ref), self._what)
 
 
 DEFAULT_CHUNK_ROWS = 3
