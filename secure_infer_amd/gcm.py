@@ -382,9 +382,8 @@ class GcmSession:
 
 class PreparedLayer:
     """A layer launch whose descriptor was built and checked once: launch()
-    only calls the library (about 7 us of host time for a codec layer; the
-    per-call checks and descriptor of reload_layer cost as much again, which
-    is more than a 24-us int4 layer leaves between launches)."""
+    only calls the library (about 7 us of host time for a codec layer, where
+    reload_layer's per-call checks and descriptor cost about as much again)."""
 
     def __init__(self, fn, session: GcmSession, desc, keep, what: str):
         self._fn = fn
