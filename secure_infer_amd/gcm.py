@@ -382,8 +382,8 @@ class GcmSession:
 
 class PreparedLayer:
     """A layer launch whose descriptor was built and checked once: launch()
-    only calls the library (about 7 us of host time for a codec layer, where
-    reload_layer's per-call checks and descriptor cost about as much again)."""
+    only calls the library, where reload_layer() / writeback_layer() rebuild
+    and re-check the descriptor on every call."""
 
     def __init__(self, fn, session: GcmSession, desc, keep, what: str):
         self._fn = fn
