@@ -186,6 +186,71 @@ def test_d2h_launch_with_a_ticket_gap():
         assert np.array_equal(hk[c].numpy(), kk[sl]) and np.array_equal(hv[c].numpy(), vv[sl])
 
 
+def test_concurrent_threads_and_streams():
+    """Two threads reload different layers through their own streams (own
+    rings, workspaces and pending launches) while a third stores a batch
+    through the D2H path, all on one session and one worker pool; every
+    layer authenticates and every byte lands."""
+    import threading
+    rng = np.random.default_rng(161)
+    heads, dim, ncpu, nslots = 2, 128, 40, 64
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 12, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        layers = _layers(rng, 8, ncpu, heads, dim)
+        slot_ids = rng.permutation(nslots)[:ncpu]
+        mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
+        dst = [caches(nslots, heads, dim) for _ in range(8)]
+        src = [tuple(torch.from_numpy(np.stack(W.bf16_blocks(rng, nslots, heads, dim)).view(np.int16)).to(DEV)
+                     for _ in range(2)) for _ in range(3)]
+        pools_out = [tuple(torch.zeros((ncpu, 128, heads, dim), dtype=torch.int16) for _ in range(2))
+                     for _ in range(3)]
+        back = torch.stack([mapping[:, 1], mapping[:, 0]], 1).contiguous()
+        errors = []
+
+        def reload(first):
+            try:
+                st = torch.cuda.Stream()
+                with torch.cuda.stream(st):
+                    nt = si.NativeTransfer(sess, shape, causal_group_blocks=16)
+                    nt.layer = first
+                    for layer in range(first, first + 4):
+                        nt.single_layer_kv_transfer((layers[layer], mapping), dst[layer])
+                st.synchronize()
+            except Exception as e:  # reported by the main thread
+                errors.append(e)
+
+        def store():
+            try:
+                st = torch.cuda.Stream()
+                with torch.cuda.stream(st):
+                    si.D2HTransfer(sess, shape, stream=st).store(src, pools_out, back, layers=[20, 21, 22])
+                st.synchronize()
+            except Exception as e:
+                errors.append(e)
+
+        torch.cuda.synchronize()
+        threads = [threading.Thread(target=reload, args=(0,)), threading.Thread(target=reload, args=(4,)),
+                   threading.Thread(target=store)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errors, errors
+        nt = si.NativeTransfer(sess, shape)
+        assert all(nt.wait_layer(layer) == 0 for layer in range(8))
+        torch.cuda.synchronize()
+        idx = torch.from_numpy(slot_ids.astype(np.int64)).to(DEV)
+        for layer in range(8):
+            (hk, hv), (ck, cv) = layers[layer], dst[layer]
+            assert torch.equal(ck.index_select(0, idx).cpu(), hk) and torch.equal(cv.index_select(0, idx).cpu(), hv)
+        for (k, v), (pk, pv) in zip(src, pools_out):
+            assert torch.equal(pk, k.index_select(0, idx).cpu()) and torch.equal(pv, v.index_select(0, idx).cpu())
+    finally:
+        si.clear_host_ranges()
+
+
 D2H_INFLIGHT_SCRIPT = r"""
 import sys, numpy as np, torch
 sys.path.insert(0, sys.argv[1])
