@@ -392,8 +392,9 @@ int secure_infer_d2h_batch_end(void);
  * authenticates and decrypts each into host_base + block*host_block_bytes
  * (d2h_host_decrypt_one, secure_infer.cpp:2470-2547).  mapping pairs are
  * (device slot, host block).  A batch's swaps of one stream and layer (K
- * before V, up to SECURE_INFER_D2H_LAUNCH_MB = 64 of records, across
- * groups) go out as one launch, issued by the next swap that does not fit
+ * before V, across groups; up to a quarter of the records the batch
+ * announced, at least 8 MiB and at most SECURE_INFER_D2H_LAUNCH_MB = 64)
+ * go out as one launch, issued by the next swap that does not fit
  * it or at the latest by batch_device_barrier / batch_end; a per-device
  * thread hands each launch to the pool once its copy is done.  At most 6
  * launches and SECURE_INFER_D2H_INFLIGHT_MB (128) of buffers are in flight
