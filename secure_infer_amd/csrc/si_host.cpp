@@ -1761,7 +1761,7 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cac
     const size_t a0 = J->aads.size();
     J->aads.resize(a0 + 64 * size_t(n));
     for (uint32_t r = 0; r < n; ++r) {
-        const int64_t ds_id = mapping[2 * r], hb = mapping[2 * r + 1];
+        const int64_t hb = mapping[2 * r + 1];
         uint8_t* dst = static_cast<uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes;
         if (secure_infer_build_gcm_aad(dst, bytes, 2, t0 + r, 0, keys.nonce, &J->aads[a0 + 64 * size_t(r)]) != 1) {
             J->aads.resize(a0);
