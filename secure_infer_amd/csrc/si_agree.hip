@@ -299,6 +299,14 @@ __global__ void entropy_kernel(uint32_t* pool, uint32_t* counter, uint32_t round
     pool[gid] = acc;
 }
 
+// Clears secret bytes in private memory through volatile stores, which the
+// compiler cannot drop as dead.
+__device__ void scrub(uint8_t* p, int n)
+{
+    volatile uint8_t* v = p;
+    for (int i = 0; i < n; ++i) v[i] = 0;
+}
+
 __global__ void agree_kernel(AgreeIo* io, const uint32_t* pool, uint32_t pool_words, uint8_t* key_out)
 {
     if (threadIdx.x != 0) return;
@@ -316,6 +324,8 @@ __global__ void agree_kernel(AgreeIo* io, const uint32_t* pool, uint32_t pool_wo
     uint8_t nz = 0;
     for (int i = 0; i < 32; ++i) nz |= shared[i];
     if (!nz) {
+        scrub(secret, 32);
+        scrub(digest, 64);
         io->status = 2;
         return;
     }
@@ -333,10 +343,11 @@ __global__ void agree_kernel(AgreeIo* io, const uint32_t* pool, uint32_t pool_wo
     for (int i = 0; i < 32; ++i) {
         io->device_public[i] = dpub[i];
         io->proof[i] = proof[i];
-        secret[i] = shared[i] = digest[i] = 0;
     }
-    for (int i = 32; i < 64; ++i) digest[i] = 0;
-    for (int i = 0; i < 16; ++i) key[i] = 0;
+    scrub(secret, 32);
+    scrub(shared, 32);
+    scrub(digest, 64);
+    scrub(key, 16);
     io->status = 0;
 }
 

@@ -806,7 +806,19 @@ struct H2DLaunch {
     StatusRef status;
 };
 
-thread_local std::unique_ptr<H2DLaunch> t_launch;
+void release_slot(StreamRing* ring, size_t idx, bool launched);
+
+// The calling thread's pending launch.  A thread that ends with one (a layer
+// group never ended) gives its ring slot back; nothing of it was queued.
+struct PendingLaunch {
+    std::unique_ptr<H2DLaunch> p;
+    ~PendingLaunch()
+    {
+        if (p) release_slot(p->ring, p->slot, false);
+    }
+};
+
+thread_local PendingLaunch t_pending;
 
 // Largest pending launch in wire bytes (SECURE_INFER_H2D_BATCH_MB, default 64):
 // ring slots are sized to the launches they carry.
@@ -854,7 +866,7 @@ void release_slot(StreamRing* ring, size_t idx, bool launched)
 // stream, the caller's stream waits for them, then the fused reload.
 int flush_launch()
 {
-    std::unique_ptr<H2DLaunch> L = std::move(t_launch);
+    std::unique_ptr<H2DLaunch> L = std::move(t_pending.p);
     if (!L) return 0;
     if (L->n == 0) {  // its only swap failed before adding records
         release_slot(L->ring, L->slot, false);
@@ -981,7 +993,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     const uint64_t tag_off = tag_offset(bytes);
 
     // Joins the pending launch if it takes these records, else issues that first.
-    H2DLaunch* L = t_launch.get();
+    H2DLaunch* L = t_pending.p.get();
     if (L && !(L->stream == stream && L->s == s && L->ds == ds && L->layer == layer && L->codec == codec_bits &&
                L->heads == heads && L->dim == head_dim && L->bytes == bytes && L->slot_bytes == slot_bytes &&
                L->nslots == nslots && L->fail_count == fail_count && L->observe == observe &&
@@ -1041,8 +1053,8 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
         nl->nslots = nslots;
         nl->fail_count = fail_count;
         nl->observe = observe;
-        t_launch = std::move(nl);
-        L = t_launch.get();
+        t_pending.p = std::move(nl);
+        L = t_pending.p.get();
     }
 
     // Host side: seal on demand into the slot's rows, or take the prefetched records.

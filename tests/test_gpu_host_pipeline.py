@@ -251,6 +251,51 @@ def test_concurrent_threads_and_streams():
         si.clear_host_ranges()
 
 
+def test_thread_ending_inside_a_group_returns_its_ring_slot():
+    """A thread that ends inside a layer group leaves a launch that was never
+    issued; its ring slot goes back to the stream's ring (16 slots), so more
+    such threads than slots do not starve later swaps on that stream."""
+    import threading
+    rng = np.random.default_rng(171)
+    heads, dim, ncpu, nslots = 2, 128, 6, 8
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 13, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        hk, hv = pools(rng, ncpu, heads, dim)
+        si.register_host_range(hk, 0, 0)
+        si.register_host_range(hv, 0, 1)
+        ck, cv = caches(nslots, heads, dim)
+        st = torch.cuda.Stream()
+        L = _lib.load()
+        one = torch.tensor([[0, 1]], dtype=torch.int64)
+        rcs = []
+
+        def abandon():
+            rcs.append(L.secure_infer_h2d_layer_group_begin(2))
+            rcs.append(L.secure_infer_h2d_swap(
+                ct.c_void_p(st.cuda_stream), sess._h, ct.c_void_p(hk.data_ptr()), hk.stride(0) * 2, ncpu,
+                ct.c_void_p(ck.data_ptr()), ck.stride(0) * 2, nslots, ct.c_void_p(one.data_ptr()), 1, 0, 0, 0,
+                heads, dim, None))
+
+        for _ in range(20):
+            t = threading.Thread(target=abandon)
+            t.start()
+            t.join()
+        assert rcs == [0] * 40
+        cpu_ids, slot_ids = np.array([5, 0, 3, 2]), np.array([7, 1, 4, 0])
+        mapping = torch.from_numpy(np.stack([cpu_ids, slot_ids], 1).astype(np.int64))
+        with torch.cuda.stream(st):
+            nt = si.NativeTransfer(sess, shape)
+            nt.single_layer_kv_transfer(((hk, hv), mapping), (ck, cv))
+            assert nt.wait_layer(0) == 0
+        kk, vv = host(ck), host(cv)
+        for c, sl in zip(cpu_ids, slot_ids):
+            assert np.array_equal(kk[sl], hk[c].numpy()) and np.array_equal(vv[sl], hv[c].numpy())
+    finally:
+        si.clear_host_ranges()
+
+
 D2H_INFLIGHT_SCRIPT = r"""
 import sys, numpy as np, torch
 sys.path.insert(0, sys.argv[1])
