@@ -1166,6 +1166,25 @@ struct D2HBatch {
     std::condition_variable cv;
     size_t pending_tasks = 0;  // verification tasks in flight (guarded by m)
     std::atomic<uint64_t> failures{0};
+
+    // Waits until no worker touches the batch (its issued launches are
+    // verified) and its device joins are done.
+    void wait_done()
+    {
+        {
+            std::unique_lock<std::mutex> g(m);
+            cv.wait(g, [&] { return pending_tasks == 0; });
+        }
+        for (hipEvent_t e : joins) {
+            (void)hipEventSynchronize(e);
+            (void)hipEventDestroy(e);
+        }
+        joins.clear();
+    }
+    // A thread that ends inside a batch (no batch_end) still lets its issued
+    // launches finish before the batch goes; the launch not yet issued is
+    // dropped.
+    ~D2HBatch() { wait_done(); }
 };
 
 thread_local std::unique_ptr<D2HBatch> t_batch;
@@ -1822,14 +1841,7 @@ int secure_infer_d2h_batch_end(void)
     if (t_batch->group_open) return -1;
     std::unique_ptr<D2HBatch> b = std::move(t_batch);
     const bool issued = d2h_issue(b.get()) == 0;
-    {
-        std::unique_lock<std::mutex> g(b->m);
-        b->cv.wait(g, [&] { return b->pending_tasks == 0; });
-    }
-    for (hipEvent_t e : b->joins) {
-        (void)hipEventSynchronize(e);
-        (void)hipEventDestroy(e);
-    }
+    b->wait_done();
     return (issued && b->failures.load() == 0) ? 0 : -1;
 }
 

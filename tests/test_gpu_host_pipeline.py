@@ -7,6 +7,8 @@ Every comparison is bit-exact against the data that went in, or against the
 oracle codec (C restatement) for packets.
 """
 import ctypes as ct
+import os
+import time
 
 import numpy as np
 import pytest
@@ -251,11 +253,23 @@ def test_concurrent_threads_and_streams():
         si.clear_host_ranges()
 
 
+def run_thread_to_exit(fn):
+    """Runs fn on a new thread and waits for the OS thread to end: join
+    returns once the Python function has returned, and the library's
+    thread-local state is destroyed later, at the thread's exit."""
+    import threading
+    t = threading.Thread(target=fn)
+    t.start()
+    t.join()
+    deadline = time.monotonic() + 60
+    while os.path.exists(f"/proc/self/task/{t.native_id}") and time.monotonic() < deadline:
+        time.sleep(0.005)
+
+
 def test_thread_ending_inside_a_group_returns_its_ring_slot():
     """A thread that ends inside a layer group leaves a launch that was never
     issued; its ring slot goes back to the stream's ring (16 slots), so more
     such threads than slots do not starve later swaps on that stream."""
-    import threading
     rng = np.random.default_rng(171)
     heads, dim, ncpu, nslots = 2, 128, 6, 8
     shape = si.LayerShape(heads, dim)
@@ -279,9 +293,7 @@ def test_thread_ending_inside_a_group_returns_its_ring_slot():
                 heads, dim, None))
 
         for _ in range(20):
-            t = threading.Thread(target=abandon)
-            t.start()
-            t.join()
+            run_thread_to_exit(abandon)
         assert rcs == [0] * 40
         cpu_ids, slot_ids = np.array([5, 0, 3, 2]), np.array([7, 1, 4, 0])
         mapping = torch.from_numpy(np.stack([cpu_ids, slot_ids], 1).astype(np.int64))
@@ -294,6 +306,46 @@ def test_thread_ending_inside_a_group_returns_its_ring_slot():
             assert np.array_equal(kk[sl], hk[c].numpy()) and np.array_equal(vv[sl], hv[c].numpy())
     finally:
         si.clear_host_ranges()
+
+
+def test_thread_ending_inside_a_d2h_batch():
+    """A thread that ends between batch begin and batch end: the launch it
+    issued (device barrier) is still verified into the host pool before its
+    batch goes, the records never issued are dropped, and later batches run."""
+    rng = np.random.default_rng(181)
+    heads, dim, nslots, ncpu = 2, 128, 8, 6
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 14, max_record_bytes=shape.record_bytes)
+    k = torch.from_numpy(np.stack(W.bf16_blocks(rng, nslots, heads, dim)).view(np.int16)).to(DEV)
+    pool = torch.zeros((ncpu, 128, heads, dim), dtype=torch.int16)
+    issued = torch.tensor([[3, 1], [6, 4]], dtype=torch.int64)
+    dropped = torch.tensor([[0, 0]], dtype=torch.int64)
+    L = _lib.load()
+    rcs = []
+
+    def swap(mapping, layer):
+        rcs.append(L.secure_infer_d2h_group_begin(mapping.shape[0]))
+        rcs.append(L.secure_infer_d2h_swap(
+            ct.c_void_p(torch.cuda.current_stream().cuda_stream), sess._h, ct.c_void_p(k.data_ptr()),
+            k[0].numel() * 2, nslots, ct.c_void_p(pool.data_ptr()), pool[0].numel() * 2, ncpu,
+            ct.c_void_p(mapping.data_ptr()), mapping.shape[0], 0, layer, 0, heads, dim))
+        rcs.append(L.secure_infer_d2h_group_end())
+
+    def abandon():
+        rcs.append(L.secure_infer_d2h_batch_begin(3))
+        swap(issued, 0)
+        rcs.append(L.secure_infer_d2h_batch_device_barrier())
+        swap(dropped, 1)  # pending when the thread ends
+
+    run_thread_to_exit(abandon)
+    assert rcs == [1, 1, 0, 0, 0, 1, 0, 0]
+    kk = host(k)
+    assert np.array_equal(pool[1].numpy(), kk[3]) and np.array_equal(pool[4].numpy(), kk[6])
+    assert not pool[0].numpy().any()
+    # The runtime still serves a whole batch afterwards.
+    dst = [(torch.zeros_like(pool), torch.zeros_like(pool))]
+    si.D2HTransfer(sess, shape).store([(k, k)], dst, issued)
+    assert np.array_equal(dst[0][1][4].numpy(), kk[6])
 
 
 D2H_INFLIGHT_SCRIPT = r"""
