@@ -108,6 +108,10 @@ typedef struct si_session si_session;
 int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt[4],
                                     uint64_t session_nonce, uint64_t max_record_bytes,
                                     si_session** out);
+/* Destroy waits for the device, issues the calling thread's pending swaps,
+ * drops the session's unconsumed prefetches, and leaves its observed swaps
+ * without retry (a record that failed then fails its layer's wait).  No
+ * other thread may still use the session. */
 int secure_infer_gpu_session_destroy(si_session* session);
 /* The reference's device session (secure_infer_experimental_device_session,
  * secure_infer.cpp:447-521; device half key_agreement.aicpu:9-49): an X25519

@@ -823,6 +823,7 @@ int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_
 int secure_infer_gpu_session_destroy(si_session* s)
 {
     if (!s) return -1;
+    si_internal::forget_session(s);
     (void)hipDeviceSynchronize();
     delete s;
     return 0;

@@ -1508,7 +1508,8 @@ int wait_observed_layer(uint32_t layer, bool* found)
             for (uint32_t r = 0; r < n; ++r) {
                 const uint32_t st = ob->status_of(r);
                 if (st == 1u) continue;
-                if (st != 0u || round != 0) rc = -1;
+                // A destroyed session (forget_session) cannot re-seal.
+                if (st != 0u || round != 0 || !ob->session) rc = -1;
                 else retry.emplace_back(ob.get(), r);
             }
         }
@@ -1551,6 +1552,30 @@ int wait_observed_layer(uint32_t layer, bool* found)
         }
         if (retry.empty()) return 0;
     }
+}
+
+void forget_session(const si_session* s)
+{
+    // The calling thread's pending launches may name the session: issue them.
+    (void)flush_launch();
+    if (D2HBatch* b = t_batch.get())
+        if (b->pending && b->pending->s == s) (void)d2h_issue(b);
+    std::vector<std::shared_ptr<Prefetch>> drop;
+    {
+        std::lock_guard<std::mutex> g(g_pf_lock);
+        for (auto it = g_prefetch.begin(); it != g_prefetch.end();) {
+            if ((*it)->session == s) {
+                drop.push_back(std::move(*it));
+                it = g_prefetch.erase(it);
+            } else {
+                ++it;
+            }
+        }
+    }
+    for (auto& pf : drop) wait_sealed(*pf);
+    std::lock_guard<std::mutex> g(g_obs_lock);
+    for (auto& e : g_observed)
+        if (e.second->session == s) e.second->session = nullptr;
 }
 
 int wait_observed_job(uint64_t job_id, bool* found)

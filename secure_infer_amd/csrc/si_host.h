@@ -49,4 +49,10 @@ int wait_observed_job(uint64_t job_id, bool* found);
 // *found tells whether the layer had observed swaps.
 int wait_observed_layer(uint32_t layer, bool* found);
 
+// Called when a session is destroyed: issues the calling thread's pending
+// launches, drops the session's unconsumed prefetches (after their sealing
+// tasks end) and marks its observed swaps as not retryable (a failed record
+// then fails its layer).
+void forget_session(const si_session* s);
+
 }  // namespace si_internal

@@ -3,7 +3,8 @@ transfer path:
 
 * strict retry (secure_infer.cpp:7303-7333): a record whose sealed bytes are
   corrupted once is re-sealed from the host copy and the layer authenticates;
-  corrupted twice, the layer fails and the record's slot reads as zeros;
+  corrupted twice, the layer fails and the record's slot reads as zeros; a
+  destroyed session retries nothing and leaves no prefetched records;
 * ids outside the host pool or the device cache refuse the swap before any
   work, in both directions, and leave both sides untouched;
 * a writeback record over an out-of-range slot carries a tag that cannot
@@ -105,6 +106,46 @@ def test_strict_retry_fails_a_persistent_fault(ranges):
             assert zero_on_device(cv[s])
         else:
             assert torch.equal(cv[s].cpu(), hv[c])
+
+
+def test_destroyed_session_leaves_no_prefetch_and_no_retry(ranges):
+    """Destroying a session drops its unconsumed prefetches (a later session,
+    possibly at the same address, must not consume records sealed under the
+    old key) and leaves its observed swaps without retry: a record that
+    failed once then fails its layer's wait."""
+    from secure_infer_amd import _lib
+    rng = np.random.default_rng(311)
+    heads, dim, ncpu, nslots, layer = 4, 128, 10, 24, 5
+    shape = si.LayerShape(heads, dim)
+    hk, hv = pools(rng, ncpu, heads, dim)
+    si.register_host_range(hk, layer, 0)
+    si.register_host_range(hv, layer, 1)
+    ck, cv = caches(nslots, heads, dim)
+    cpu_ids = rng.permutation(ncpu)[:6]
+    slot_ids = rng.permutation(nslots)[:6]
+    mapping = torch.from_numpy(np.stack([cpu_ids, slot_ids], 1).astype(np.int64))
+    L = _lib.load()
+    sess = si.GcmSession(KEY, SALT, 12, max_record_bytes=shape.record_bytes)
+    nt = si.NativeTransfer(sess, shape, pipeline_seal=False)
+    assert nt.prefetch_kv_transfer(((hk, hv), mapping), layer + 1)
+    target = int(cpu_ids[2])
+    si.inject_h2d_tamper(layer=layer, kind=1, host_block=target, shots=1)
+    nt.layer = layer
+    nt.single_layer_kv_transfer(((hk, hv), mapping), (ck, cv))
+    sess.close()
+    assert int(L.secure_infer_count_ready_unconsumed_gcm_tickets()) == 0
+    assert nt.wait_layer(layer) == -1
+    s = int(slot_ids[2])
+    assert zero_on_device(cv[s])
+    # A new session serves the same layer normally.
+    sess2 = si.GcmSession(KEY, SALT, 13, max_record_bytes=shape.record_bytes)
+    nt2 = si.NativeTransfer(sess2, shape)
+    nt2.layer = layer
+    ck2, cv2 = caches(nslots, heads, dim)
+    nt2.single_layer_kv_transfer(((hk, hv), mapping), (ck2, cv2))
+    assert nt2.wait_layer(layer) == 0
+    for c, sl in zip(cpu_ids, slot_ids):
+        assert torch.equal(ck2[sl].cpu(), hk[c]) and torch.equal(cv2[sl].cpu(), hv[c])
 
 
 def test_side_stream_reload_reports_failure(ranges):
