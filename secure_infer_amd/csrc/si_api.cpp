@@ -256,12 +256,18 @@ std::vector<uint8_t> ctx_image(const uint8_t key[16], const uint8_t h[16], uint3
     put(c->gh4b, ht2);
     put(c->gh4u, htu);
     put(c->gh4u2, htu2);
+    OPENSSL_cleanse(rk, sizeof(rk));
     return img;
 }
 
 std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], uint32_t npow)
 {
-    const std::vector<uint8_t> img = ctx_image(key, h, npow);
+    // The host image holds the round keys: wiped once it is on the device.
+    struct Image {
+        std::vector<uint8_t> v;
+        ~Image() { OPENSSL_cleanse(v.data(), v.size()); }
+    } im{ctx_image(key, h, npow)};
+    const std::vector<uint8_t>& img = im.v;
     auto out = std::make_unique<DevCtx>();
     if (hipMalloc(&out->dev, img.size()) != hipSuccess) return nullptr;
     if (hipMemcpy(out->dev, img.data(), img.size(), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
@@ -463,6 +469,10 @@ uint4* park_area(Workspace& w, hipStream_t stream, size_t nwg)
 DevCtx* ctx_for_device_key(hipStream_t stream, const void* key, const void* h, uint32_t npow)
 {
     uint8_t kb[16], hb[16] = {0};
+    struct Cleanse {
+        uint8_t* p;
+        ~Cleanse() { OPENSSL_cleanse(p, 16); }
+    } cleanse{kb};
     if (hipMemcpyAsync(kb, key, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
     if (h && hipMemcpyAsync(hb, h, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
     if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
@@ -594,6 +604,7 @@ int secure_infer_gpu_session_create(const uint8_t key[16], const uint8_t iv_salt
     uint8_t rk[176], h[16], zero[16] = {0};
     aes_expand(key, rk);
     aes_encrypt(rk, zero, h);
+    OPENSSL_cleanse(rk, sizeof(rk));
     auto s = std::make_unique<si_session>();
     s->ctx = build_ctx(key, h, npow_for(max_record_bytes, 64));
     if (!s->ctx) return -1;
