@@ -341,6 +341,11 @@ int secure_infer_test_tamper_d2h(uint32_t shots);
  * device lane; the kernels' context built on the device (on_device = 1) or
  * on the host (0) from a key, written to out (cap bytes; out = NULL returns
  * the size).  Production code never calls them. */
+/* Test-only fault injection for the next secure_infer_gpu_session_agree
+ * (one shot; no reference counterpart): mode 1 flips a byte of the device's
+ * proof as it reaches the host, mode 2 sends the all-zero (low-order) public
+ * value to the device; either makes the agreement return -1.  0 disarms. */
+int secure_infer_test_tamper_agree(uint32_t mode);
 int secure_infer_test_x25519(const uint8_t scalar[32], const uint8_t u[32], uint8_t out[32]);
 int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_t* msg, uint64_t msg_len,
                               uint8_t* out, uint32_t out_len);

@@ -73,6 +73,7 @@ SIGNATURES = {
                                _u32, _u32, _v], _i),
     "secure_infer_test_tamper_h2d": ([ct.c_int32, ct.c_int32, ct.c_int64, _u32], _i),
     "secure_infer_test_tamper_d2h": ([_u32], _i),
+    "secure_infer_test_tamper_agree": ([_u32], _i),
     "secure_infer_retire_transfer_prefetches": ([], None),
     "secure_infer_invalidate_transfer_prefetches": ([], None),
     "secure_infer_get_transfer_prefetch_stats": ([ct.POINTER(_u64)] * 3, None),

@@ -662,6 +662,9 @@ bool blake2b_keyed(const uint8_t* key, size_t key_len, std::initializer_list<std
     return ok;
 }
 
+// Test-only one-shot fault for the next agreement (secure_infer_test_tamper_agree).
+std::atomic<uint32_t> g_tamper_agree{0};
+
 const char kAgreeInfo[] = "SecureInfer X25519 BLAKE2b test v1";
 const char kSaltInfo[] = "SecureInfer IV salt v1";
 
@@ -724,7 +727,9 @@ int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_b
         if (RAND_bytes(secret, 32) != 1 || RAND_bytes(io.challenge, 32) != 1 || RAND_bytes(io.seed, 32) != 1 ||
             !x25519_public(secret, host_public))
             goto done;
+        const uint32_t fault = g_tamper_agree.exchange(0);
         memcpy(io.host_public, host_public, 32);
+        if (fault == 2) memset(io.host_public, 0, 32);
         io.status = -1;
         // A private stream, as the reference's setup stream: nothing the
         // caller has queued is waited for.
@@ -738,6 +743,7 @@ int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_b
             hipMemcpyAsync(&io, b.io, sizeof(io), hipMemcpyDeviceToHost, b.stream) != hipSuccess ||
             hipStreamSynchronize(b.stream) != hipSuccess || io.status != 0)
             goto done;
+        if (fault == 1) io.proof[0] ^= 0x01;
         {
             uint8_t nz = 0;
             if (!x25519_shared(secret, io.device_public, shared)) goto done;
@@ -772,6 +778,13 @@ done:
     OPENSSL_cleanse(rk, sizeof(rk));
     if (rc != 0) return -1;
     *out = s.release();
+    return 0;
+}
+
+int secure_infer_test_tamper_agree(uint32_t mode)
+{
+    if (mode > 2) return -1;
+    g_tamper_agree.store(mode);
     return 0;
 }
 

@@ -11,7 +11,8 @@ session, secure_infer.cpp:447-521, key_agreement.aicpu:9-49):
   builder's image byte for byte;
 * an agreed session reloads host-sealed records (the host's copy of the key)
   through the device's own context bit-exactly and writes back records the
-  host authenticates; two agreements yield different hash subkeys.
+  host authenticates; two agreements yield different hash subkeys;
+* a wrong device proof or a low-order host public value makes no session.
 """
 import ctypes as ct
 import hashlib
@@ -112,3 +113,19 @@ def test_agreed_session_end_to_end():
         si.clear_host_ranges()
         sess.close()
         other.close()
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["bad_proof", "low_order_point"])
+def test_agreement_refuses_a_bad_proof_or_a_low_order_point(mode):
+    """The host rejects a device proof that does not match its own key
+    derivation (secure_infer.cpp:487-499), and the device refuses an all-zero
+    shared secret (a low-order host public value, key_agreement.aicpu:33-35);
+    either way no session is made.  The fault is one shot."""
+    L = _lib.load()
+    assert L.secure_infer_test_tamper_agree(mode) == 0
+    try:
+        with pytest.raises(RuntimeError, match="session_agree"):
+            si.GcmSession.agree(max_record_bytes=4096)
+    finally:
+        L.secure_infer_test_tamper_agree(0)
+    si.GcmSession.agree(max_record_bytes=4096).close()
