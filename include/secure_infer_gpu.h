@@ -88,6 +88,63 @@ int secure_infer_gpu_keystream_do(
 int secure_infer_gpu_auth_gate_do(hipStream_t stream, void* data, void* status,
                                   uint64_t bytes);
 
+/* launcher.asc:312-341 / 378-405: the AAD-less forms of the two above. */
+int secure_infer_gpu_gcm_verify_xor_do(
+    hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+    void* expected_tag, void* keystream, void* plaintext_output,
+    void* status_output, uint64_t bytes, uint32_t iv_word0, uint32_t iv_word1,
+    uint32_t iv_word2, uint32_t iv_word3);
+int secure_infer_gpu_gcm_verify_only_do(
+    hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+    void* expected_tag, void* status_output, uint64_t bytes,
+    uint32_t iv_word0, uint32_t iv_word1, uint32_t iv_word2, uint32_t iv_word3);
+
+/* launcher.asc:440-486, ghash.aicpu:834-940: up to 4 records of one key and
+ * size, each verified and released as by secure_infer_gpu_gcm_verify_xor_aad_do.
+ * The pointer arrays are host arrays of device pointers; iv_words holds 4
+ * words per record; aads may be NULL when aad_bytes is 0. */
+#define SI_GCM_VERIFY_XOR_BATCH_MAX 4u
+int secure_infer_gpu_gcm_verify_xor_batch_do(
+    hipStream_t stream, void* key, void* hash_subkey, void* const* ciphertexts,
+    void* const* expected_tags, void* const* keystreams,
+    void* const* plaintext_outputs, void* const* status_outputs,
+    void* const* aads, uint64_t bytes, uint64_t aad_bytes,
+    const uint32_t* iv_words, uint32_t count);
+
+/* launcher.asc:184-210, ghash.aicpu:559-580: up to 32 CTR keystreams of
+ * one key and length (outputs: host array of device pointers). */
+#define SI_AES_KEYSTREAM_BATCH_MAX 32u
+int secure_infer_gpu_keystream_batch_do(
+    hipStream_t stream, void* key, void* const* outputs,
+    const uint32_t* iv_words, uint64_t bytes, uint32_t count);
+
+/* launcher.asc:75-114, ghash.aicpu:978-1045: output (16 B) = GHASH_H over
+ * aad || input || [bits(aad)]_64 || [bits(input)]_64, XORed with tag_mask
+ * under SI_GHASH_FINALIZE_TAG; under SI_GHASH_VERIFY_TAG the status is 1
+ * iff output equals expected_tag (1 without the flag); under
+ * SI_GHASH_XOR_ON_SUCCESS plaintext_output = (input ^ keystream) masked to
+ * zero on failure, written after the verdict.  status_output may be NULL.
+ * Needs H only (no key). */
+#define SI_GHASH_FINALIZE_TAG 1u
+#define SI_GHASH_VERIFY_TAG 2u
+#define SI_GHASH_XOR_ON_SUCCESS 4u
+int secure_infer_gpu_ghash_do(
+    hipStream_t stream, void* input, void* hash_subkey, void* output,
+    void* aad, void* tag_mask, void* expected_tag, void* keystream,
+    void* plaintext_output, void* status_output, uint64_t input_bytes,
+    uint64_t aad_bytes, uint32_t flags);
+
+/* launcher.asc:19-32, key_agreement.aicpu:9-49: the device half of the
+ * session agreement (every pointer device memory: host_public 32 B and
+ * challenge 32 B in; device_key 16 B, device_public 32 B, proof 32 B and an
+ * int32 status out).  status: 0 done; 1, 2 or 3 the step it stopped at
+ * (2: the shared secret is zero).  The device secret comes from clock
+ * jitter on the GPU and a host seed, not from /dev/urandom.  The key stays
+ * in device memory unless the caller copies it. */
+int secure_infer_gpu_key_agreement_do(
+    hipStream_t stream, void* host_public, void* challenge, void* device_key,
+    void* device_public, void* proof, void* status);
+
 /* ------------------------------------------------------------------ */
 /* 2. Sessions and layer-level fused entry points.
  *

@@ -46,6 +46,12 @@ SIGNATURES = {
     "secure_infer_gpu_aes_ctr_do": ([_v] * 4 + [_u64] + [_u32] * 4, _i),
     "secure_infer_gpu_keystream_do": ([_v] * 3 + [_u64] + [_u32] * 4, _i),
     "secure_infer_gpu_auth_gate_do": ([_v, _v, _v, _u64], _i),
+    "secure_infer_gpu_gcm_verify_xor_do": ([_v] * 8 + [_u64] + [_u32] * 4, _i),
+    "secure_infer_gpu_gcm_verify_only_do": ([_v] * 6 + [_u64] + [_u32] * 4, _i),
+    "secure_infer_gpu_gcm_verify_xor_batch_do": ([_v] * 9 + [_u64, _u64, _v, _u32], _i),
+    "secure_infer_gpu_keystream_batch_do": ([_v, _v, _v, _v, _u64, _u32], _i),
+    "secure_infer_gpu_ghash_do": ([_v] * 10 + [_u64, _u64, _u32], _i),
+    "secure_infer_gpu_key_agreement_do": ([_v] * 7, _i),
     "secure_infer_gpu_session_create": ([_v, _v, _u64, _u64, ct.POINTER(_v)], _i),
     "secure_infer_gpu_session_destroy": ([_v], _i),
     "secure_infer_gpu_session_agree": ([_u64, _u64, ct.POINTER(_v)], _i),

@@ -307,77 +307,56 @@ __device__ void scrub(uint8_t* p, int n)
     for (int i = 0; i < n; ++i) v[i] = 0;
 }
 
-__global__ void agree_kernel(AgreeIo* io, const uint32_t* pool, uint32_t pool_words, uint8_t* key_out)
+// The device half of key_agreement.aicpu:9-49 with its status codes: 1 while
+// the secret is drawn, 2 once it is (a zero shared secret stops there), 3
+// while the key and proof are derived, 0 when done.  The device public value
+// is written as soon as it is known, the key and the proof at the end.
+__global__ void agree_kernel(const uint8_t* host_public, const uint8_t* challenge, AgreeSeed seed,
+                             const uint32_t* pool, uint32_t pool_words, uint8_t* key_out,
+                             uint8_t* device_public, uint8_t* proof_out, int32_t* status)
 {
     if (threadIdx.x != 0) return;
     uint8_t secret[32], shared[32], base[32] = {9}, digest[64];
+    *status = 1;
     B2b s;
     b2b_init(s, nullptr, 0, 64);
-    b2b_update(s, io->seed, 32);
+    b2b_update(s, seed.b, 32);
     b2b_update(s, reinterpret_cast<const uint8_t*>(pool), uint64_t(pool_words) * 4);
     b2b_final(s, digest);
     for (int i = 0; i < 32; ++i) secret[i] = digest[i];
-    io->status = 1;
+    *status = 2;
     uint8_t dpub[32];
     x25519(dpub, secret, base);
-    x25519(shared, secret, io->host_public);
+    for (int i = 0; i < 32; ++i) device_public[i] = dpub[i];
+    x25519(shared, secret, host_public);
     uint8_t nz = 0;
     for (int i = 0; i < 32; ++i) nz |= shared[i];
     if (!nz) {
         scrub(secret, 32);
         scrub(digest, 64);
-        io->status = 2;
+        scrub(reinterpret_cast<uint8_t*>(&s), int(sizeof(s)));
         return;
     }
+    *status = 3;
     uint8_t key[16], proof[32];
     b2b_init(s, shared, 32, 16);
     b2b_update(s, reinterpret_cast<const uint8_t*>(kInfo), sizeof(kInfo) - 1);
-    b2b_update(s, io->host_public, 32);
+    b2b_update(s, host_public, 32);
     b2b_update(s, dpub, 32);
-    b2b_update(s, io->challenge, 32);
+    b2b_update(s, challenge, 32);
     b2b_final(s, key);
     b2b_init(s, key, 16, 32);
-    b2b_update(s, io->challenge, 32);
+    b2b_update(s, challenge, 32);
     b2b_final(s, proof);
     for (int i = 0; i < 16; ++i) key_out[i] = key[i];
-    for (int i = 0; i < 32; ++i) {
-        io->device_public[i] = dpub[i];
-        io->proof[i] = proof[i];
-    }
+    for (int i = 0; i < 32; ++i) proof_out[i] = proof[i];
     scrub(secret, 32);
     scrub(shared, 32);
     scrub(digest, 64);
     scrub(key, 16);
-    io->status = 0;
-}
-
-// GF(2^128) product of two elements in memory byte order held as four
-// little-endian words (SP 800-38D Algorithm 1).
-__device__ uint4 gf_mul4(uint4 x, uint4 y)
-{
-    const uint32_t xw[4] = {x.x, x.y, x.z, x.w}, yw[4] = {y.x, y.y, y.z, y.w};
-    uint64_t vh = 0, vl = 0, zh = 0, zl = 0;
-    for (int i = 0; i < 8; ++i) {
-        vh = vh << 8 | ((yw[i >> 2] >> (8 * (i & 3))) & 0xff);
-        vl = vl << 8 | ((yw[2 + (i >> 2)] >> (8 * (i & 3))) & 0xff);
-    }
-    for (int i = 0; i < 128; ++i) {
-        const uint32_t byte = (xw[i >> 5] >> (8 * ((i >> 3) & 3))) & 0xff;
-        if ((byte >> (7 - (i & 7))) & 1) {
-            zh ^= vh;
-            zl ^= vl;
-        }
-        const uint64_t lsb = vl & 1;
-        vl = (vl >> 1) | (vh << 63);
-        vh >>= 1;
-        if (lsb) vh ^= 0xe100000000000000ull;
-    }
-    uint32_t z[4] = {0, 0, 0, 0};
-    for (int i = 0; i < 8; ++i) {
-        z[i >> 2] |= uint32_t((zh >> (56 - 8 * i)) & 0xff) << (8 * (i & 3));
-        z[2 + (i >> 2)] |= uint32_t((zl >> (56 - 8 * i)) & 0xff) << (8 * (i & 3));
-    }
-    return make_uint4(z[0], z[1], z[2], z[3]);
+    scrub(reinterpret_cast<uint8_t*>(&s), int(sizeof(s)));
+    __threadfence();
+    *status = 0;
 }
 
 __device__ uint4 gf_one() { return make_uint4(0x80u, 0u, 0u, 0u); }
@@ -517,13 +496,16 @@ __global__ void zero_bytes_kernel(uint8_t* p, uint32_t n)
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_agree(hipStream_t stream, AgreeIo* io, uint8_t* key_out, uint32_t* pool, uint32_t* counter)
+hipError_t launch_agree(hipStream_t stream, const uint8_t* host_public, const uint8_t* challenge,
+                        const AgreeSeed& seed, uint32_t* pool, uint32_t* counter, uint8_t* key_out,
+                        uint8_t* device_public, uint8_t* proof, int32_t* status)
 {
     constexpr uint32_t kBlocks = 512, kThreads = 256, kRounds = 8;
     static_assert(kBlocks * kThreads == SI_AGREE_POOL_WORDS, "pool size");
     hipLaunchKernelGGL(zero_bytes_kernel, dim3(1), dim3(64), 0, stream, reinterpret_cast<uint8_t*>(counter), 4u);
     hipLaunchKernelGGL(entropy_kernel, dim3(kBlocks), dim3(kThreads), 0, stream, pool, counter, kRounds);
-    hipLaunchKernelGGL(agree_kernel, dim3(1), dim3(64), 0, stream, io, pool, kBlocks * kThreads, key_out);
+    hipLaunchKernelGGL(agree_kernel, dim3(1), dim3(64), 0, stream, host_public, challenge, seed, pool,
+                       kBlocks * kThreads, key_out, device_public, proof, status);
     return hipGetLastError();
 }
 

@@ -466,16 +466,10 @@ uint4* park_area(Workspace& w, hipStream_t stream, size_t nwg)
     return w.park;
 }
 
-DevCtx* ctx_for_device_key(hipStream_t stream, const void* key, const void* h, uint32_t npow)
+// The cached context of (key, H) from host copies, built on a miss (the
+// caller holds g_ctx_lock).
+DevCtx* ctx_for(const uint8_t kb[16], const uint8_t hb[16], uint32_t npow)
 {
-    uint8_t kb[16], hb[16] = {0};
-    struct Cleanse {
-        uint8_t* p;
-        ~Cleanse() { OPENSSL_cleanse(p, 16); }
-    } cleanse{kb};
-    if (hipMemcpyAsync(kb, key, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
-    if (h && hipMemcpyAsync(hb, h, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
-    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
     for (auto& c : g_ctx_cache)
         if (!memcmp(c->key, kb, 16) && !memcmp(c->h, hb, 16) && c->npow >= npow) return c.get();
     auto c = build_ctx(kb, hb, npow);
@@ -488,16 +482,38 @@ DevCtx* ctx_for_device_key(hipStream_t stream, const void* key, const void* h, u
     return g_ctx_cache.back().get();
 }
 
+// The context of a device-resident key (and H, or zeros): both read back on
+// the stream first.
+DevCtx* ctx_for_device_key(hipStream_t stream, const void* key, const void* h, uint32_t npow)
+{
+    uint8_t kb[16], hb[16] = {0};
+    struct Cleanse {
+        uint8_t* p;
+        ~Cleanse() { OPENSSL_cleanse(p, 16); }
+    } cleanse{kb};
+    if (hipMemcpyAsync(kb, key, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+    if (h && hipMemcpyAsync(hb, h, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    return ctx_for(kb, hb, npow);
+}
+
+// A context of H alone (GHASH needs no key): keyed by the all-zero key.
+DevCtx* ctx_for_hash_subkey(hipStream_t stream, const void* h, uint32_t npow)
+{
+    uint8_t hb[16];
+    static const uint8_t kZeroKey[16] = {0};
+    if (hipMemcpyAsync(hb, h, 16, hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    return ctx_for(kZeroKey, hb, npow);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int run_single(int mode, hipStream_t stream, void* src, void* key, void* h, void* tag, void* dst,
-               void* status, const void* ks, uint64_t bytes, const uint32_t iv[4], void* aad,
-               uint64_t aad_bytes)
+// One record through the record kernel with context c (the caller holds
+// g_ctx_lock, so c stays cached until the launch is queued).
+int run_single_ctx(int mode, hipStream_t stream, DevCtx* c, void* src, void* tag, void* dst, void* status,
+                   const void* ks, uint64_t bytes, const uint32_t iv[4], void* aad, uint64_t aad_bytes)
 {
-    if (bytes > SI_MAX_RECORD_BYTES) return -1;
-    std::lock_guard<std::mutex> g(g_ctx_lock);
-    DevCtx* c = ctx_for_device_key(stream, key, h, npow_for(bytes, aad_bytes));
-    if (!c) return -1;
     Workspace* ws = workspace_of(stream);
     if (!ws) return -1;
     std::lock_guard<std::mutex> gw(ws->m);
@@ -515,6 +531,17 @@ int run_single(int mode, hipStream_t stream, void* src, void* key, void* h, void
     const si::Sched s = make_sched(1, bytes, aad_bytes, c->h);
     const bool al = aligned16(src) && (!dst || aligned16(dst)) && (!ks || aligned16(ks));
     return si::launch_gcm(mode, stream, c->dev, b, s, acc, al) == hipSuccess ? 0 : -1;
+}
+
+int run_single(int mode, hipStream_t stream, void* src, void* key, void* h, void* tag, void* dst,
+               void* status, const void* ks, uint64_t bytes, const uint32_t iv[4], void* aad,
+               uint64_t aad_bytes)
+{
+    if (bytes > SI_MAX_RECORD_BYTES) return -1;
+    std::lock_guard<std::mutex> g(g_ctx_lock);
+    DevCtx* c = ctx_for_device_key(stream, key, h, npow_for(bytes, aad_bytes));
+    if (!c) return -1;
+    return run_single_ctx(mode, stream, c, src, tag, dst, status, ks, bytes, iv, aad, aad_bytes);
 }
 
 // ---------------------------------------------------------------- control plane state
@@ -688,6 +715,9 @@ std::unique_ptr<DevCtx> build_ctx_on_device(hipStream_t stream, const uint8_t* d
     return out;
 }
 
+// Address of a field of a device-resident struct.
+uint8_t* field(void* dev_struct, size_t offset) { return static_cast<uint8_t*>(dev_struct) + offset; }
+
 // Device buffers of one agreement, freed on exit.  The key and the entropy
 // pool (with the seed, the pool determines the device's X25519 secret) are
 // zeroed first.
@@ -720,11 +750,12 @@ int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_b
     if (!out || max_record_bytes == 0 || max_record_bytes > SI_MAX_RECORD_BYTES) return -1;
     uint8_t secret[32], host_public[32], shared[32], key[16], expected[32], salt[4], h[16], rk[176], zero[16] = {0};
     si::AgreeIo io{};
+    si::AgreeSeed seed{};
     int rc = -1;
     std::unique_ptr<si_session> s;
     {
         AgreeBufs b;
-        if (RAND_bytes(secret, 32) != 1 || RAND_bytes(io.challenge, 32) != 1 || RAND_bytes(io.seed, 32) != 1 ||
+        if (RAND_bytes(secret, 32) != 1 || RAND_bytes(io.challenge, 32) != 1 || RAND_bytes(seed.b, 32) != 1 ||
             !x25519_public(secret, host_public))
             goto done;
         const uint32_t fault = g_tamper_agree.exchange(0);
@@ -739,7 +770,11 @@ int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_b
             hipMalloc(reinterpret_cast<void**>(&b.pool), SI_AGREE_POOL_WORDS * 4) != hipSuccess ||
             hipMalloc(reinterpret_cast<void**>(&b.counter), 4) != hipSuccess ||
             hipMemcpyAsync(b.io, &io, sizeof(io), hipMemcpyHostToDevice, b.stream) != hipSuccess ||
-            si::launch_agree(b.stream, b.io, b.key, b.pool, b.counter) != hipSuccess ||
+            si::launch_agree(b.stream, field(b.io, offsetof(si::AgreeIo, host_public)),
+                             field(b.io, offsetof(si::AgreeIo, challenge)), seed, b.pool, b.counter, b.key,
+                             field(b.io, offsetof(si::AgreeIo, device_public)),
+                             field(b.io, offsetof(si::AgreeIo, proof)),
+                             reinterpret_cast<int32_t*>(field(b.io, offsetof(si::AgreeIo, status)))) != hipSuccess ||
             hipMemcpyAsync(&io, b.io, sizeof(io), hipMemcpyDeviceToHost, b.stream) != hipSuccess ||
             hipStreamSynchronize(b.stream) != hipSuccess || io.status != 0)
             goto done;
@@ -773,6 +808,7 @@ int secure_infer_gpu_session_agree(uint64_t session_nonce, uint64_t max_record_b
     }
 done:
     OPENSSL_cleanse(secret, sizeof(secret));
+    OPENSSL_cleanse(seed.b, sizeof(seed.b));
     OPENSSL_cleanse(shared, sizeof(shared));
     OPENSSL_cleanse(key, sizeof(key));
     OPENSSL_cleanse(rk, sizeof(rk));
@@ -1179,6 +1215,117 @@ int secure_infer_gpu_auth_gate_do(hipStream_t stream, void* data, void* status, 
     if (!data || !status) return -1;
     return si::launch_auth_gate(stream, static_cast<uint8_t*>(data),
                                 static_cast<const uint32_t*>(status), bytes) == hipSuccess ? 0 : -1;
+}
+
+int secure_infer_gpu_gcm_verify_xor_do(hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+                                       void* expected_tag, void* keystream, void* plaintext_output,
+                                       void* status_output, uint64_t bytes, uint32_t iv0, uint32_t iv1,
+                                       uint32_t iv2, uint32_t iv3)
+{
+    return secure_infer_gpu_gcm_verify_xor_aad_do(stream, ciphertext, key, hash_subkey, expected_tag, keystream,
+                                                  plaintext_output, status_output, bytes, iv0, iv1, iv2, iv3,
+                                                  nullptr, 0);
+}
+
+int secure_infer_gpu_gcm_verify_only_do(hipStream_t stream, void* ciphertext, void* key, void* hash_subkey,
+                                        void* expected_tag, void* status_output, uint64_t bytes, uint32_t iv0,
+                                        uint32_t iv1, uint32_t iv2, uint32_t iv3)
+{
+    return secure_infer_gpu_gcm_verify_only_aad_do(stream, ciphertext, key, hash_subkey, expected_tag,
+                                                   status_output, bytes, iv0, iv1, iv2, iv3, nullptr, 0);
+}
+
+int secure_infer_gpu_gcm_verify_xor_batch_do(hipStream_t stream, void* key, void* hash_subkey,
+                                             void* const* ciphertexts, void* const* expected_tags,
+                                             void* const* keystreams, void* const* plaintext_outputs,
+                                             void* const* status_outputs, void* const* aads, uint64_t bytes,
+                                             uint64_t aad_bytes, const uint32_t* iv_words, uint32_t count)
+{
+    if (!key || !hash_subkey || !ciphertexts || !expected_tags || !keystreams || !plaintext_outputs ||
+        !status_outputs || !iv_words || bytes == 0 || bytes > SI_MAX_RECORD_BYTES || (aad_bytes != 0 && !aads) ||
+        count == 0 || count > SI_GCM_VERIFY_XOR_BATCH_MAX)
+        return -1;
+    for (uint32_t i = 0; i < count; ++i)
+        if (!ciphertexts[i] || !expected_tags[i] || !keystreams[i] || !plaintext_outputs[i] || !status_outputs[i] ||
+            (aad_bytes != 0 && !aads[i]))
+            return -1;
+    std::lock_guard<std::mutex> g(g_ctx_lock);
+    DevCtx* c = ctx_for_device_key(stream, key, hash_subkey, npow_for(bytes, aad_bytes));
+    if (!c) return -1;
+    for (uint32_t i = 0; i < count; ++i)
+        if (run_single_ctx(3, stream, c, ciphertexts[i], expected_tags[i], plaintext_outputs[i], status_outputs[i],
+                           keystreams[i], bytes, iv_words + 4 * size_t(i), aad_bytes ? aads[i] : nullptr,
+                           aad_bytes) != 0)
+            return -1;
+    return 0;
+}
+
+int secure_infer_gpu_keystream_batch_do(hipStream_t stream, void* key, void* const* outputs,
+                                        const uint32_t* iv_words, uint64_t bytes, uint32_t count)
+{
+    if (!key || !outputs || !iv_words || bytes == 0 || count == 0 || count > SI_AES_KEYSTREAM_BATCH_MAX) return -1;
+    for (uint32_t i = 0; i < count; ++i)
+        if (!outputs[i]) return -1;
+    std::lock_guard<std::mutex> g(g_ctx_lock);
+    DevCtx* c = ctx_for_device_key(stream, key, nullptr, 1);
+    if (!c) return -1;
+    for (uint32_t i = 0; i < count; ++i)
+        if (si::launch_ctr(stream, c->dev, nullptr, static_cast<uint8_t*>(outputs[i]), bytes,
+                           iv_words + 4 * size_t(i)) != hipSuccess)
+            return -1;
+    return 0;
+}
+
+int secure_infer_gpu_ghash_do(hipStream_t stream, void* input, void* hash_subkey, void* output, void* aad,
+                              void* tag_mask, void* expected_tag, void* keystream, void* plaintext_output,
+                              void* status_output, uint64_t input_bytes, uint64_t aad_bytes, uint32_t flags)
+{
+    if (!input || !hash_subkey || !output || input_bytes == 0 || input_bytes > SI_MAX_RECORD_BYTES ||
+        aad_bytes > SI_MAX_RECORD_BYTES || (aad_bytes != 0 && !aad) ||
+        ((flags & SI_GHASH_FINALIZE_TAG) && !tag_mask) || ((flags & SI_GHASH_VERIFY_TAG) && !expected_tag) ||
+        ((flags & SI_GHASH_XOR_ON_SUCCESS) && (!keystream || !plaintext_output)))
+        return -1;
+    std::lock_guard<std::mutex> g(g_ctx_lock);
+    DevCtx* c = ctx_for_hash_subkey(stream, hash_subkey, npow_for(input_bytes, aad_bytes));
+    if (!c) return -1;
+    si::GhashJob j{};
+    j.input = static_cast<const uint8_t*>(input);
+    j.aad = static_cast<const uint8_t*>(aad);
+    j.tag_mask = static_cast<const uint8_t*>(tag_mask);
+    j.expected_tag = static_cast<const uint8_t*>(expected_tag);
+    j.keystream = static_cast<const uint8_t*>(keystream);
+    j.plaintext = static_cast<uint8_t*>(plaintext_output);
+    j.status = static_cast<uint32_t*>(status_output);
+    j.output = static_cast<uint8_t*>(output);
+    j.input_bytes = input_bytes;
+    j.aad_bytes = aad_bytes;
+    j.flags = flags;
+    return si::launch_ghash(stream, c->dev, j) == hipSuccess ? 0 : -1;
+}
+
+int secure_infer_gpu_key_agreement_do(hipStream_t stream, void* host_public, void* challenge, void* device_key,
+                                      void* device_public, void* proof, void* status)
+{
+    if (!host_public || !challenge || !device_key || !device_public || !proof || !status) return -1;
+    si::AgreeSeed seed{};
+    if (RAND_bytes(seed.b, 32) != 1) return -1;
+    // The entropy pool and its counter live on the stream's own schedule:
+    // allocated, filled, hashed, zeroed and freed in stream order.
+    const size_t pool_bytes = size_t(SI_AGREE_POOL_WORDS) * 4 + 16;
+    uint32_t* pool = nullptr;
+    if (hipMallocAsync(reinterpret_cast<void**>(&pool), pool_bytes, stream) != hipSuccess) {
+        OPENSSL_cleanse(seed.b, sizeof(seed.b));
+        return -1;
+    }
+    const hipError_t e = si::launch_agree(stream, static_cast<const uint8_t*>(host_public),
+                                          static_cast<const uint8_t*>(challenge), seed, pool,
+                                          pool + SI_AGREE_POOL_WORDS, static_cast<uint8_t*>(device_key),
+                                          static_cast<uint8_t*>(device_public), static_cast<uint8_t*>(proof),
+                                          static_cast<int32_t*>(status));
+    OPENSSL_cleanse(seed.b, sizeof(seed.b));
+    const hipError_t z = si::launch_zero_bytes(stream, reinterpret_cast<uint8_t*>(pool), uint32_t(pool_bytes));
+    const hipError_t f = hipFreeAsync(pool, stream);
+    return (e == hipSuccess && z == hipSuccess && f == hipSuccess) ? 0 : -1;
 }
 
 // ---------------------------------------------------------------- control plane

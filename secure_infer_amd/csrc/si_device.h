@@ -533,6 +533,36 @@ __device__ __forceinline__ void gh_mul_part(const uint32_t (&x_mem)[NS][4], cons
     }
 }
 
+// GF(2^128) product of two elements in memory byte order held as four
+// little-endian words (SP 800-38D Algorithm 1), bit-serial: for the rare
+// general products (set-up work, the GHASH mirror), not for the rows.
+__device__ inline uint4 gf_mul4(uint4 x, uint4 y)
+{
+    const uint32_t xw[4] = {x.x, x.y, x.z, x.w}, yw[4] = {y.x, y.y, y.z, y.w};
+    uint64_t vh = 0, vl = 0, zh = 0, zl = 0;
+    for (int i = 0; i < 8; ++i) {
+        vh = vh << 8 | ((yw[i >> 2] >> (8 * (i & 3))) & 0xff);
+        vl = vl << 8 | ((yw[2 + (i >> 2)] >> (8 * (i & 3))) & 0xff);
+    }
+    for (int i = 0; i < 128; ++i) {
+        const uint32_t byte = (xw[i >> 5] >> (8 * ((i >> 3) & 3))) & 0xff;
+        if ((byte >> (7 - (i & 7))) & 1) {
+            zh ^= vh;
+            zl ^= vl;
+        }
+        const uint64_t lsb = vl & 1;
+        vl = (vl >> 1) | (vh << 63);
+        vh >>= 1;
+        if (lsb) vh ^= 0xe100000000000000ull;
+    }
+    uint32_t z[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) {
+        z[i >> 2] |= uint32_t((zh >> (56 - 8 * i)) & 0xff) << (8 * (i & 3));
+        z[2 + (i >> 2)] |= uint32_t((zl >> (56 - 8 * i)) & 0xff) << (8 * (i & 3));
+    }
+    return make_uint4(z[0], z[1], z[2], z[3]);
+}
+
 // XOR of four words over a wave64, valid in lane 63, by DPP moves only (no
 // LDS crossbar round trips): swap within pairs and quads, mirror 8 and 16
 // lanes (every lane then holds its row's XOR), then row_bcast:15 into rows 1

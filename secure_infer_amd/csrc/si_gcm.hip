@@ -925,6 +925,84 @@ __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ct
     }
 }
 
+// GHASH of aad || input || lengths by one workgroup: rows of SI_T blocks
+// counted from the end (thread t owns block t of each row, Horner with the
+// H^T tables in LDS), then thread t's sum times H^(T + 1 - t) from the power
+// table, XORed over the workgroup with the length block's L * H.
+__global__ __launch_bounds__(SI_T) void ghash_kernel(const GcmCtx* __restrict__ ctx, GhashJob j)
+{
+    __shared__ uint4 tbl[32 * 16];
+    __shared__ uint4 wsum[SI_T / 64];
+    __shared__ uint32_t s_ok;
+    const uint32_t t = threadIdx.x;
+    tbl[t] = ctx->gh4[t];
+    tbl[SI_T + t] = ctx->gh4[SI_T + t];
+    __syncthreads();
+    const uint64_t a = (j.aad_bytes + 15) / 16, n = (j.input_bytes + 15) / 16, m = a + n;
+    const uint64_t rows = (m + SI_T - 1) / SI_T;
+    uint32_t y[4] = {0, 0, 0, 0};
+    for (uint64_t q = 0; q < rows; ++q) {
+        if (q) gh_mul_table(tbl, y);
+        const int64_t i = int64_t(m) - int64_t(rows - q) * SI_T + int64_t(t);
+        if (i < 0) continue;
+        uint32_t x[4];
+        if (uint64_t(i) < a) {
+            const uint64_t off = uint64_t(i) * 16;
+            load_block<false>(j.aad + off, uint32_t(j.aad_bytes - off < 16 ? j.aad_bytes - off : 16), x);
+        } else {
+            const uint64_t off = (uint64_t(i) - a) * 16;
+            load_block<false>(j.input + off, uint32_t(j.input_bytes - off < 16 ? j.input_bytes - off : 16), x);
+        }
+        y[0] ^= x[0]; y[1] ^= x[1]; y[2] ^= x[2]; y[3] ^= x[3];
+    }
+    const uint4 pw = reinterpret_cast<const uint4*>(ctx + 1)[SI_T + 1 - t];
+    const uint4 z = gf_mul4(make_uint4(y[0], y[1], y[2], y[3]), pw);
+    uint32_t v[4] = {z.x, z.y, z.z, z.w};
+    wave_xor4_to63(v);
+    if ((t & 63u) == 63u) wsum[t >> 6] = make_uint4(v[0], v[1], v[2], v[3]);
+    __syncthreads();
+    if (t == 0) {
+        uint32_t g[4] = {0, 0, 0, 0};
+        for (uint32_t w = 0; w < SI_T / 64; ++w) {
+            g[0] ^= wsum[w].x; g[1] ^= wsum[w].y; g[2] ^= wsum[w].z; g[3] ^= wsum[w].w;
+        }
+        // L = [bits(aad)]_64 || [bits(input)]_64, big-endian, as memory-order words.
+        const uint64_t la = j.aad_bytes * 8, lc = j.input_bytes * 8;
+        const uint4 L = make_uint4(bswap32(uint32_t(la >> 32)), bswap32(uint32_t(la)), bswap32(uint32_t(lc >> 32)),
+                                   bswap32(uint32_t(lc)));
+        const uint4 lh = gf_mul4(L, make_uint4(ctx->h[0], ctx->h[1], ctx->h[2], ctx->h[3]));
+        g[0] ^= lh.x; g[1] ^= lh.y; g[2] ^= lh.z; g[3] ^= lh.w;
+        if (j.flags & SI_GHASH_FINALIZE_TAG) {
+            uint32_t mk[4];
+            load_block<false>(j.tag_mask, 16u, mk);
+            g[0] ^= mk[0]; g[1] ^= mk[1]; g[2] ^= mk[2]; g[3] ^= mk[3];
+        }
+        store_block<false>(j.output, 16u, g);
+        uint32_t ok = 1;
+        if (j.flags & SI_GHASH_VERIFY_TAG) {
+            uint32_t e[4];
+            load_block<false>(j.expected_tag, 16u, e);
+            ok = ((g[0] ^ e[0]) | (g[1] ^ e[1]) | (g[2] ^ e[2]) | (g[3] ^ e[3])) == 0 ? 1u : 0u;
+        }
+        s_ok = ok;
+    }
+    __syncthreads();
+    const uint32_t ok = s_ok;
+    if (j.flags & SI_GHASH_XOR_ON_SUCCESS) {
+        const uint32_t mask = 0u - ok;
+        for (uint64_t k = t; k < n; k += SI_T) {
+            const uint32_t valid = uint32_t(j.input_bytes - k * 16 < 16 ? j.input_bytes - k * 16 : 16);
+            uint32_t c[4], ks[4];
+            load_block<false>(j.input + 16 * k, valid, c);
+            load_block<false>(j.keystream + 16 * k, valid, ks);
+            const uint32_t o[4] = {(c[0] ^ ks[0]) & mask, (c[1] ^ ks[1]) & mask, (c[2] ^ ks[2]) & mask,
+                                   (c[3] ^ ks[3]) & mask};
+            store_block<false>(j.plaintext + 16 * k, valid, o);
+        }
+    }
+    if (t == 0 && j.status) *gmem(j.status) = ok;
+}
+
 __global__ void auth_gate_kernel(uint8_t* data, const uint32_t* status, uint64_t bytes)
 {
     if (*status == 1u) return;
@@ -1003,6 +1081,12 @@ hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, 
     const bool aligned = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
     hipLaunchKernelGGL(ctr_kernel, dim3(uint32_t(grid)), dim3(SI_T), 0, stream, ctx, in, out, bytes,
                        make_uint4(iv[0], iv[1], iv[2], iv[3]), aligned ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_ghash(hipStream_t stream, const GcmCtx* ctx, const GhashJob& j)
+{
+    hipLaunchKernelGGL(ghash_kernel, dim3(1), dim3(SI_T), 0, stream, ctx, j);
     return hipGetLastError();
 }
 

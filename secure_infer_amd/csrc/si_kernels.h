@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "secure_infer_gpu.h"
+
 namespace si {
 
 struct GcmCtx;
@@ -83,6 +85,27 @@ hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, 
 hipError_t launch_auth_gate(hipStream_t stream, uint8_t* data, const uint32_t* status,
                             uint64_t bytes);
 
+// One GHASH (the reference's secure_infer_ghash task, ghash.aicpu:978-1045):
+// output = GHASH_H(aad || input || lengths) (^ tag_mask with FINALIZE_TAG);
+// with VERIFY_TAG the status is 1 iff output equals expected_tag (else 1);
+// with XOR_ON_SUCCESS plaintext = (input ^ keystream) & (0 - status),
+// written after the verdict.  Any pointer may be unaligned.
+// (flags: SI_GHASH_* of secure_infer_gpu.h)
+struct GhashJob {
+    const uint8_t* input;
+    const uint8_t* aad;
+    const uint8_t* tag_mask;
+    const uint8_t* expected_tag;
+    const uint8_t* keystream;
+    uint8_t* plaintext;
+    uint32_t* status;  // may be null
+    uint8_t* output;   // 16 bytes
+    uint64_t input_bytes, aad_bytes;
+    uint32_t flags;
+};
+// ctx: a context of H (powers up to H^(SI_T + 1) at least and the tables of H^SI_T).
+hipError_t launch_ghash(hipStream_t stream, const GcmCtx* ctx, const GhashJob& j);
+
 // Codec kernels (si_codec.hip).
 struct CodecBatch {
     uint32_t nrec, n_k, bits, heads, dim, layer;
@@ -101,16 +124,22 @@ hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b);
 struct AgreeIo {
     uint8_t host_public[32];    // in
     uint8_t challenge[32];      // in
-    uint8_t seed[32];           // in: mixed with the device's clock jitter
     uint8_t device_public[32];  // out
     uint8_t proof[32];          // out: BLAKE2b-32 keyed by the key over the challenge
-    int32_t status;             // out: 0 done; 1 or 2 failed (no secret / zero shared secret)
+    int32_t status;             // out: 0 done; 1, 2 or 3 failed (the step it stopped at)
     uint32_t pad[7];
+};
+// Host seed mixed with the device's clock jitter (a kernel argument).
+struct AgreeSeed {
+    uint8_t b[32];
 };
 // Entropy pool (`pool`: SI_AGREE_POOL_WORDS u32, `counter`: one u32) and the
 // agreement; the 16-byte key is written to `key_out` (device memory only).
+// Every pointer is device memory.
 #define SI_AGREE_POOL_WORDS (512u * 256u)
-hipError_t launch_agree(hipStream_t stream, AgreeIo* io, uint8_t* key_out, uint32_t* pool, uint32_t* counter);
+hipError_t launch_agree(hipStream_t stream, const uint8_t* host_public, const uint8_t* challenge,
+                        const AgreeSeed& seed, uint32_t* pool, uint32_t* counter, uint8_t* key_out,
+                        uint8_t* device_public, uint8_t* proof, int32_t* status);
 // GcmCtx (+ npow powers) from a device-resident 16-byte key; te0 is public.
 hipError_t launch_ctx_build(hipStream_t stream, const uint8_t* key, const uint32_t* te0, GcmCtx* ctx,
                             uint32_t npow);

@@ -139,21 +139,82 @@ def gcm_encrypt_tag(plaintext, key, hash_subkey, ciphertext_out, tag_out, iv, aa
 
 def gcm_verify_only(ciphertext, key, hash_subkey, expected_tag, status_out, iv, aad=None,
                     stream=None) -> None:
-    """secure_infer_aicpu_gcm_verify_only_aad_do (launcher.asc:407-435)."""
-    a = 0 if aad is None else aad.numel()
+    """secure_infer_aicpu_gcm_verify_only[_aad]_do (launcher.asc:378-435): the
+    AAD-less launcher when aad is None."""
+    if aad is None:
+        _check(lib().secure_infer_gpu_gcm_verify_only_do(
+            _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
+            _p(status_out), ciphertext.numel(), *iv), "gcm_verify_only")
+        return
     _check(lib().secure_infer_gpu_gcm_verify_only_aad_do(
         _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
-        _p(status_out), ciphertext.numel(), *iv, _p(aad), a), "gcm_verify_only")
+        _p(status_out), ciphertext.numel(), *iv, _p(aad), aad.numel()), "gcm_verify_only")
 
 
 def gcm_verify_xor(ciphertext, key, hash_subkey, expected_tag, keystream, plaintext_out,
                    status_out, iv, aad=None, stream=None) -> None:
-    """secure_infer_aicpu_gcm_verify_xor_aad_do (launcher.asc:343-376)."""
-    a = 0 if aad is None else aad.numel()
+    """secure_infer_aicpu_gcm_verify_xor[_aad]_do (launcher.asc:312-376): the
+    AAD-less launcher when aad is None."""
+    if aad is None:
+        _check(lib().secure_infer_gpu_gcm_verify_xor_do(
+            _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
+            _p(keystream), _p(plaintext_out), _p(status_out), ciphertext.numel(), *iv),
+            "gcm_verify_xor")
+        return
     _check(lib().secure_infer_gpu_gcm_verify_xor_aad_do(
         _stream(stream), _p(ciphertext), _p(key), _p(hash_subkey), _p(expected_tag),
-        _p(keystream), _p(plaintext_out), _p(status_out), ciphertext.numel(), *iv, _p(aad), a),
-        "gcm_verify_xor")
+        _p(keystream), _p(plaintext_out), _p(status_out), ciphertext.numel(), *iv, _p(aad),
+        aad.numel()), "gcm_verify_xor")
+
+
+def _ptrs(tensors):
+    return (ct.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
+
+
+def _iv_array(ivs):
+    return (ct.c_uint32 * (4 * len(ivs)))(*[w for iv in ivs for w in iv])
+
+
+def gcm_verify_xor_batch(key, hash_subkey, ciphertexts, expected_tags, keystreams, plaintext_outs,
+                         status_outs, ivs, aads=None, stream=None) -> None:
+    """secure_infer_aicpu_gcm_verify_xor_batch_do (launcher.asc:440-486): up to
+    four same-size records under one key, each verified and released."""
+    n = ciphertexts[0].numel()
+    a = 0 if aads is None else aads[0].numel()
+    _check(lib().secure_infer_gpu_gcm_verify_xor_batch_do(
+        _stream(stream), _p(key), _p(hash_subkey), _ptrs(ciphertexts), _ptrs(expected_tags),
+        _ptrs(keystreams), _ptrs(plaintext_outs), _ptrs(status_outs),
+        None if aads is None else _ptrs(aads), n, a, _iv_array(ivs), len(ciphertexts)),
+        "gcm_verify_xor_batch")
+
+
+def keystream_batch(key, outs, ivs, stream=None) -> None:
+    """secure_infer_aicpu_keystream_batch_do (launcher.asc:184-210)."""
+    _check(lib().secure_infer_gpu_keystream_batch_do(
+        _stream(stream), _p(key), _ptrs(outs), _iv_array(ivs), outs[0].numel(), len(outs)),
+        "keystream_batch")
+
+
+GHASH_FINALIZE_TAG, GHASH_VERIFY_TAG, GHASH_XOR_ON_SUCCESS = 1, 2, 4
+
+
+def ghash(inp, hash_subkey, out, aad=None, tag_mask=None, expected_tag=None, keystream=None,
+          plaintext_out=None, status_out=None, flags=0, nbytes=None, stream=None) -> None:
+    """secure_infer_aicpu_ghash_do (launcher.asc:75-114, ghash.aicpu:978-1045)."""
+    n = inp.numel() if nbytes is None else nbytes
+    a = 0 if aad is None else aad.numel()
+    _check(lib().secure_infer_gpu_ghash_do(
+        _stream(stream), _p(inp), _p(hash_subkey), _p(out), _p(aad), _p(tag_mask), _p(expected_tag),
+        _p(keystream), _p(plaintext_out), _p(status_out), n, a, flags), "ghash")
+
+
+def key_agreement(host_public, challenge, device_key, device_public, proof, status,
+                  stream=None) -> None:
+    """secure_infer_aicpu_key_agreement_do (launcher.asc:19-32): the device half
+    of the session agreement on device buffers."""
+    _check(lib().secure_infer_gpu_key_agreement_do(
+        _stream(stream), _p(host_public), _p(challenge), _p(device_key), _p(device_public),
+        _p(proof), _p(status)), "key_agreement")
 
 
 def aes_ctr(inp, key, out, iv, stream=None) -> None:
