@@ -287,9 +287,12 @@ uint64_t secure_infer_new_transfer_ticket(void);
 int secure_infer_derive_transfer_iv(const uint8_t base_iv[16], uint64_t session_nonce,
                                     uint64_t ticket, uint64_t block_offset,
                                     uint8_t out_iv[16]);
-/* secure_infer.cpp:1066-1091 (host address ranges -> layer / kind / block). */
+/* secure_infer.cpp:1066-1091 (host address ranges -> layer / kind / block);
+ * registering an existing [base, base + bytes) again re-labels it. */
 void secure_infer_register_host_range_ex(const void* base, size_t bytes, uint32_t layer_id,
                                          uint32_t tensor_kind, size_t block_bytes);
+/* secure_infer.cpp:1093-1097: layer and kind unknown (0xffffffff), no block size. */
+void secure_infer_register_host_range(const void* base, size_t bytes);
 void secure_infer_clear_host_ranges(void);
 /* secure_infer.cpp:730-775: 64-B AAD for a registered host address.
  * Returns 1 on success, 0 on invalid arguments. */

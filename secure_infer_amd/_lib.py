@@ -67,6 +67,7 @@ SIGNATURES = {
     "secure_infer_new_transfer_ticket": ([], _u64),
     "secure_infer_derive_transfer_iv": ([_v, _u64, _u64, _u64, _v], _i),
     "secure_infer_register_host_range_ex": ([_v, _sz, _u32, _u32, _sz], None),
+    "secure_infer_register_host_range": ([_v, _sz], None),
     "secure_infer_clear_host_ranges": ([], None),
     "secure_infer_build_gcm_aad": ([_v, _sz, _u8, _u64, _u64, _u64, _v], _i),
     "secure_infer_gcm_replay_reserve": ([_u64], _i),

@@ -82,6 +82,32 @@ def test_host_iv_and_aad_match_oracle():
         si.build_gcm_aad(blk.data_ptr(), 16, 3, 1)
 
 
+def test_registering_a_range_again_relabels_it():
+    """secure_infer.cpp:1066-1091: the same [base, base + bytes) registered
+    again takes the new layer, kind and block size (no stale duplicate);
+    the two-argument form (:1093-1097) registers layer and kind unknown."""
+    import ctypes as ct
+    import torch
+    import secure_infer_amd as si
+    from oracle import oracle as O
+    from secure_infer_amd import _lib
+    pool = torch.zeros((6, 128, 2, 64), dtype=torch.bfloat16)
+    blk = pool[4]
+    nbytes = blk.numel() * 2
+    si.clear_host_ranges()
+    try:
+        si.register_host_range(pool, layer_id=9, tensor_kind=1)
+        si.register_host_range(pool, layer_id=3, tensor_kind=0)
+        assert si.build_gcm_aad(blk.data_ptr(), nbytes, 1, 77) == O.build_gcm_aad(1, 0, 3, 4, 0, nbytes, 77)
+        si.clear_host_ranges()
+        _lib.load().secure_infer_register_host_range(ct.c_void_p(pool.data_ptr()), pool.numel() * 2)
+        aad = si.build_gcm_aad(blk.data_ptr(), nbytes, 2, 78)
+        # no block size: the block id is the byte offset into the range
+        assert aad == O.build_gcm_aad(2, 0xFF, 0xFFFFFFFF, 4 * nbytes, 0, nbytes, 78)
+    finally:
+        si.clear_host_ranges()
+
+
 def test_error_returns_before_any_device_work():
     """The reference's error contract (0 / -1, launcher.asc returns -1 on null or
     zero arguments): invalid calls are rejected on the host, so they run here
