@@ -320,8 +320,9 @@ void secure_infer_get_transfer_prefetch_stats(uint64_t* ready, uint64_t* busy_fa
 /* secure_infer.cpp:5052-5070: records sealed ahead of demand and not yet consumed. */
 uint64_t secure_infer_count_ready_unconsumed_gcm_tickets(void);
 
-/* secure_infer.cpp:5883-5903: layer-group brackets (thread-local).  `expected`
- * is the group's record count.  Swaps of the group accumulate and go out as
+/* secure_infer.cpp:5883-5903: layer-group brackets (thread-local; they nest,
+ * and only the outermost end issues; an end without a begin returns -1).
+ * `expected` (of the outermost begin) is the group's record count.  Swaps of the group accumulate and go out as
  * few launches as their stream, layer and geometry allow (K swaps, then V
  * swaps, of one stream form one launch; at most SECURE_INFER_H2D_BATCH_MB of
  * records, default 64), issued at the latest by group_end, as the reference

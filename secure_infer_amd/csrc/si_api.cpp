@@ -590,6 +590,7 @@ bool replay_insert(uint64_t a, uint64_t b)
 }
 
 thread_local int64_t t_group_expected = -1;
+thread_local uint32_t t_group_depth = 0;
 
 // secure_infer_recovery_set_job_id (secure_infer.cpp:5311-5314): the job that
 // records observed from now on belong to.
@@ -1425,16 +1426,18 @@ int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket)
     return 0;
 }
 
+// Groups nest per thread (secure_infer.cpp:5883-5903): the outermost begin
+// announces the record count, the matching end issues the launch.
 int secure_infer_h2d_layer_group_begin(size_t expected)
 {
-    if (t_group_expected >= 0) return -1;
-    t_group_expected = int64_t(expected);
+    if (t_group_depth++ == 0) t_group_expected = int64_t(expected);
     return 0;
 }
 
 int secure_infer_h2d_layer_group_end(void)
 {
-    if (t_group_expected < 0) return -1;
+    if (t_group_depth == 0) return -1;
+    if (--t_group_depth != 0) return 0;
     t_group_expected = -1;
     return si_internal::flush_pending_h2d() == 0 ? 0 : -1;
 }
@@ -1547,7 +1550,7 @@ uint64_t reserve_tickets(uint32_t n)
 
 bool replay_reserve_range(uint64_t t0, uint64_t n) { return replay_insert(t0, t0 + n); }
 
-bool group_open() { return t_group_expected >= 0; }
+bool group_open() { return t_group_depth > 0; }
 
 int64_t group_expected() { return t_group_expected; }
 

@@ -141,9 +141,10 @@ def test_error_returns_before_any_device_work():
     assert L.secure_infer_d2h_batch_device_barrier() == -1
     assert L.secure_infer_d2h_batch_end() == 0
     assert L.secure_infer_d2h_swap(None, None, one, 16, 1, one, 16, 1, one, 1, 0, 0, 0, 0, 0) == -1
-    # layer-group nesting is thread-local
+    # layer groups nest (secure_infer.cpp:5883-5903) and are thread-local
     assert L.secure_infer_h2d_layer_group_begin(4) == 0
-    assert L.secure_infer_h2d_layer_group_begin(4) == -1
+    assert L.secure_infer_h2d_layer_group_begin(4) == 0
+    assert L.secure_infer_h2d_layer_group_end() == 0
     assert L.secure_infer_h2d_layer_group_end() == 0
     assert L.secure_infer_h2d_layer_group_end() == -1
     errors = []
