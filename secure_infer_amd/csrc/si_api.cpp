@@ -1287,7 +1287,8 @@ int secure_infer_gpu_ghash_do(hipStream_t stream, void* input, void* hash_subkey
         ((flags & SI_GHASH_XOR_ON_SUCCESS) && (!keystream || !plaintext_output)))
         return -1;
     std::lock_guard<std::mutex> g(g_ctx_lock);
-    DevCtx* c = ctx_for_hash_subkey(stream, hash_subkey, npow_for(input_bytes, aad_bytes));
+    // The GHASH kernel reads the powers H^0 .. H^(T + 1) only.
+    DevCtx* c = ctx_for_hash_subkey(stream, hash_subkey, SI_T + 2);
     if (!c) return -1;
     si::GhashJob j{};
     j.input = static_cast<const uint8_t*>(input);

@@ -103,7 +103,7 @@ struct GhashJob {
     uint64_t input_bytes, aad_bytes;
     uint32_t flags;
 };
-// ctx: a context of H (powers up to H^(SI_T + 1) at least and the tables of H^SI_T).
+// ctx: a context of H (the powers H^0 .. H^(SI_T + 1) and the tables of H^SI_T).
 hipError_t launch_ghash(hipStream_t stream, const GcmCtx* ctx, const GhashJob& j);
 
 // Codec kernels (si_codec.hip).
