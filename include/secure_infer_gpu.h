@@ -426,6 +426,16 @@ int64_t secure_infer_test_context_image(const uint8_t key[16], uint64_t max_reco
 int secure_infer_h2d_prefetch(si_session* session, const void* host_base, uint64_t host_block_bytes,
                               uint64_t host_nblocks, const int64_t* mapping, uint32_t n, uint32_t kind,
                               uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim);
+/* A layer group's two swaps at once (no reference counterpart; the same
+ * prefetch for the K swap of `mapping` from k_base followed by the V swap of
+ * the same mapping from v_base, tickets in that order).  The records of both
+ * halves and the group's slot ids share one pinned buffer, so a launch of
+ * exactly this group (its K swap then its V swap on one stream) goes to the
+ * device in one copy. */
+int secure_infer_h2d_prefetch_group(si_session* session, const void* k_base, const void* v_base,
+                                    uint64_t host_block_bytes, uint64_t host_nblocks, const int64_t* mapping,
+                                    uint32_t n, uint32_t layer, uint32_t codec_bits, uint32_t heads,
+                                    uint32_t head_dim);
 
 /* secure_infer.cpp:6085-6137: the H2D ledger.  With
  * SECURE_INFER_H2D_PROFILE=<path> every launch appends one CSV row (layer,

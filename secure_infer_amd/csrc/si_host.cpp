@@ -604,7 +604,12 @@ struct Prefetch {
     std::vector<int64_t> host_blocks;
     uint64_t bytes = 0, stride = 0, tag_off = 0, t0 = 0;
     uint8_t* host = nullptr;
-    size_t cap = 0;
+    size_t cap = 0;  // bytes of `host` this prefetch owns (0: a part of `owner`'s buffer)
+    std::shared_ptr<Prefetch> owner;  // the K half of a group prefetch, whose buffer this shares
+    // A group prefetch (K half): its buffer is [K records][V records][slot ids of
+    // both halves], so one DMA can carry the group's launch.
+    const uint8_t* group_ids = nullptr;
+    uint32_t group_records = 0;
     std::mutex m;
     std::condition_variable cv;
     uint32_t tasks = 0, done = 0;
@@ -633,7 +638,7 @@ size_t prefetch_budget()
 
 Prefetch::~Prefetch()
 {
-    if (!host) return;
+    if (!host || !cap) return;
     std::lock_guard<std::mutex> g(g_pf_lock);
     g_pf_free.emplace_back(host, cap);
 }
@@ -677,6 +682,73 @@ uint8_t* take_pf_buffer(size_t need, size_t& cap)
     return p;
 }
 
+double us_since(std::chrono::steady_clock::time_point t0)
+{
+    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+}
+
+void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint64_t bytes, uint64_t tag_off,
+                 uint64_t ticket, uint8_t* rec, uint32_t layer, uint32_t kind, int64_t hb, bool& ok);
+
+// A prefetch of n records of one kind sealed into `host` (tickets set by the
+// caller), not yet registered.
+std::shared_ptr<Prefetch> new_prefetch(si_session* s, const si_internal::SessionKeys& keys, const void* host_base,
+                                       uint64_t host_block_bytes, const int64_t* mapping, uint32_t n, uint32_t kind,
+                                       uint32_t layer, uint32_t codec, uint32_t heads, uint32_t dim, uint64_t bytes,
+                                       uint8_t* host)
+{
+    auto pf = std::make_shared<Prefetch>();
+    pf->session = s;
+    pf->keys = keys;
+    pf->host_base = static_cast<const uint8_t*>(host_base);
+    pf->host_block_bytes = host_block_bytes;
+    pf->kind = kind;
+    pf->layer = layer;
+    pf->codec = codec;
+    pf->heads = heads;
+    pf->dim = dim;
+    pf->n = n;
+    pf->bytes = bytes;
+    pf->stride = secure_infer_wire_stride(bytes);
+    pf->tag_off = tag_offset(bytes);
+    pf->host_blocks.resize(n);
+    for (uint32_t r = 0; r < n; ++r) pf->host_blocks[r] = mapping[2 * r];
+    pf->host = host;
+    return pf;
+}
+
+// Registers the prefetch for its swap and appends its sealing tasks, one
+// record per task (the pool balances records, not swaps).
+void queue_seals(const std::shared_ptr<Prefetch>& pf, std::vector<std::function<void()>>& tasks)
+{
+    pf->tasks = pf->n;
+    {
+        std::lock_guard<std::mutex> g(g_pf_lock);
+        g_prefetch.push_back(pf);
+    }
+    for (uint32_t r = 0; r < pf->n; ++r) {
+        tasks.emplace_back([pf, r] {
+            {
+                std::lock_guard<std::mutex> g(pf->m);
+                if (!pf->started) {
+                    pf->started = true;
+                    pf->first_start = std::chrono::steady_clock::now();
+                }
+            }
+            bool ok = true;
+            const int64_t hb = pf->host_blocks[r];
+            seal_record(pf->keys, pf->host_base + uint64_t(hb) * pf->host_block_bytes, pf->bytes, pf->tag_off,
+                        pf->t0 + r, pf->host + uint64_t(r) * pf->stride, pf->layer, pf->kind, hb, ok);
+            std::lock_guard<std::mutex> g(pf->m);
+            if (!ok) pf->failed = true;
+            if (++pf->done == pf->tasks) {
+                pf->seal_us = us_since(pf->first_start);
+                pf->cv.notify_all();
+            }
+        });
+    }
+}
+
 void wait_sealed(Prefetch& pf)
 {
     std::unique_lock<std::mutex> g(pf.m);
@@ -703,9 +775,6 @@ std::shared_ptr<Prefetch> take_prefetch(si_session* s, const void* host_base, ui
     }
     return nullptr;
 }
-
-void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint64_t bytes, uint64_t tag_off,
-                 uint64_t ticket, uint8_t* rec, uint32_t layer, uint32_t kind, int64_t hb, bool& ok);
 
 // ---------------------------------------------------------------- observed reloads
 
@@ -761,11 +830,6 @@ void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint6
     memset(rec + bytes, 0, tag_off - bytes);
     memset(rec + tag_off + 16, 0, 16);  // status slot
     if (tamper_h2d(layer, kind, hb)) rec[0] ^= 0x01;
-}
-
-double us_since(std::chrono::steady_clock::time_point t0)
-{
-    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
 }
 
 // One swap's records within a launch.
@@ -908,21 +972,39 @@ int flush_launch()
         return -1;
     };
     if (prof && hipEventRecord(sl.p_c0, L->ring->copy) != hipSuccess) return fail();
-    // One copy per run of parts whose sealed records sit back to back.
-    for (size_t i = 0; i < L->parts.size();) {
-        const uint8_t* src = L->parts[i].src;
-        const uint32_t r0 = L->parts[i].r0;
-        uint32_t rows = L->parts[i].n;
-        size_t j = i + 1;
-        for (; j < L->parts.size() && L->parts[j].src == src + size_t(rows) * L->stride; ++j) rows += L->parts[j].n;
-        if (hipMemcpyAsync(sl.dev + size_t(r0) * L->stride, src, size_t(rows) * L->stride, hipMemcpyHostToDevice,
+    // A launch of exactly one group prefetch (its K half, then its V half, as
+    // large as the launch and with one ticket run): the prefetch buffer holds
+    // the slot ids right after the records, the device layout of this
+    // launch, so one copy carries all of it.
+    const Prefetch* gk = L->parts.size() == 2 ? L->parts[0].pf.get() : nullptr;
+    const bool one_copy = gk && gk->group_records == L->n && L->cap == L->n && contiguous && L->parts[0].r0 == 0 &&
+                          L->parts[1].pf && L->parts[1].pf->owner.get() == gk &&
+                          L->parts[1].src == L->parts[0].src + size_t(L->parts[0].n) * L->stride &&
+                          memcmp(gk->group_ids, L->slot_ids.data(), size_t(L->n) * 8) == 0;
+    if (one_copy) {
+        if (hipMemcpyAsync(sl.dev, L->parts[0].src, size_t(L->n) * (L->stride + 8), hipMemcpyHostToDevice,
                            L->ring->copy) != hipSuccess)
             return fail();
-        i = j;
+    } else {
+        // One copy per run of parts whose sealed records sit back to back,
+        // then the IV words and slot ids.
+        for (size_t i = 0; i < L->parts.size();) {
+            const uint8_t* src = L->parts[i].src;
+            const uint32_t r0 = L->parts[i].r0;
+            uint32_t rows = L->parts[i].n;
+            size_t j = i + 1;
+            for (; j < L->parts.size() && L->parts[j].src == src + size_t(rows) * L->stride; ++j)
+                rows += L->parts[j].n;
+            if (hipMemcpyAsync(sl.dev + size_t(r0) * L->stride, src, size_t(rows) * L->stride,
+                               hipMemcpyHostToDevice, L->ring->copy) != hipSuccess)
+                return fail();
+            i = j;
+        }
+        if (hipMemcpyAsync(sl.dev + wire_cap, tail, iv_bytes + size_t(L->n) * 8, hipMemcpyHostToDevice,
+                           L->ring->copy) != hipSuccess)
+            return fail();
     }
-    if (hipMemcpyAsync(sl.dev + wire_cap, tail, iv_bytes + size_t(L->n) * 8, hipMemcpyHostToDevice,
-                       L->ring->copy) != hipSuccess ||
-        (prof && hipEventRecord(sl.p_c1, L->ring->copy) != hipSuccess) ||
+    if ((prof && hipEventRecord(sl.p_c1, L->ring->copy) != hipSuccess) ||
         hipEventRecord(sl.ev_a, L->ring->copy) != hipSuccess || hipStreamWaitEvent(L->stream, sl.ev_a, 0) != hipSuccess)
         return fail();
 
@@ -1633,60 +1715,59 @@ int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t hos
     if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
     for (uint32_t r = 0; r < n; ++r)
         if (mapping[2 * r] < 0 || uint64_t(mapping[2 * r]) >= host_nblocks) return -1;
-    auto pf = std::make_shared<Prefetch>();
-    pf->keys = si_internal::session_keys(s);
-    if (bytes > pf->keys.max_record_bytes) return -1;
-    pf->session = s;
-    pf->host_base = static_cast<const uint8_t*>(host_base);
-    pf->host_block_bytes = host_block_bytes;
-    pf->kind = kind;
-    pf->layer = layer;
-    pf->codec = codec_bits;
-    pf->heads = heads;
-    pf->dim = head_dim;
-    pf->n = n;
-    pf->bytes = bytes;
-    pf->stride = secure_infer_wire_stride(bytes);
-    pf->tag_off = tag_offset(bytes);
-    pf->host_blocks.resize(n);
-    for (uint32_t r = 0; r < n; ++r) pf->host_blocks[r] = mapping[2 * r];
-    const size_t need = size_t(n) * pf->stride;
-    pf->host = take_pf_buffer(need, pf->cap);
-    if (!pf->host) return -1;  // over SECURE_INFER_PREFETCH_MB: the swap seals on demand
+    const si_internal::SessionKeys keys = si_internal::session_keys(s);
+    if (bytes > keys.max_record_bytes) return -1;
+    const uint64_t stride = secure_infer_wire_stride(bytes);
+    size_t cap = 0;
+    uint8_t* buf = take_pf_buffer(size_t(n) * stride, cap);
+    if (!buf) return -1;  // over SECURE_INFER_PREFETCH_MB: the swap seals on demand
+    auto pf = new_prefetch(s, keys, host_base, host_block_bytes, mapping, n, kind, layer, codec_bits, heads,
+                           head_dim, bytes, buf);
+    pf->cap = cap;
     pf->t0 = si_internal::reserve_tickets(n);
     if (!si_internal::replay_reserve_range(pf->t0, n)) return -1;
-    const uint32_t per_task = 1;  // one record per task: the pool balances records, not swaps
-    pf->tasks = (n + per_task - 1) / per_task;
-    {
-        std::lock_guard<std::mutex> g(g_pf_lock);
-        g_prefetch.push_back(pf);
-    }
     std::vector<std::function<void()>> tasks;
-    tasks.reserve(pf->tasks);
-    for (uint32_t r0 = 0; r0 < n; r0 += per_task) {
-        const uint32_t r1 = std::min(n, r0 + per_task);
-        tasks.emplace_back([pf, r0, r1] {
-            {
-                std::lock_guard<std::mutex> g(pf->m);
-                if (!pf->started) {
-                    pf->started = true;
-                    pf->first_start = std::chrono::steady_clock::now();
-                }
-            }
-            bool ok = true;
-            for (uint32_t r = r0; r < r1 && ok; ++r) {
-                const int64_t hb = pf->host_blocks[r];
-                seal_record(pf->keys, pf->host_base + uint64_t(hb) * pf->host_block_bytes, pf->bytes, pf->tag_off,
-                            pf->t0 + r, pf->host + uint64_t(r) * pf->stride, pf->layer, pf->kind, hb, ok);
-            }
-            std::lock_guard<std::mutex> g(pf->m);
-            if (!ok) pf->failed = true;
-            if (++pf->done == pf->tasks) {
-                pf->seal_us = us_since(pf->first_start);
-                pf->cv.notify_all();
-            }
-        });
-    }
+    queue_seals(pf, tasks);
+    Pool::get().submit_all(tasks);
+    return 0;
+}
+
+int secure_infer_h2d_prefetch_group(si_session* s, const void* k_base, const void* v_base,
+                                    uint64_t host_block_bytes, uint64_t host_nblocks, const int64_t* mapping,
+                                    uint32_t n, uint32_t layer, uint32_t codec_bits, uint32_t heads,
+                                    uint32_t head_dim)
+{
+    if (!s || !k_base || !v_base || !mapping || n == 0 || host_nblocks == 0 || n > UINT32_MAX / 2) return -1;
+    uint64_t bytes = 0;
+    if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
+    for (uint32_t r = 0; r < n; ++r)
+        if (mapping[2 * r] < 0 || uint64_t(mapping[2 * r]) >= host_nblocks) return -1;
+    const si_internal::SessionKeys keys = si_internal::session_keys(s);
+    if (bytes > keys.max_record_bytes) return -1;
+    const uint64_t stride = secure_infer_wire_stride(bytes);
+    const size_t wire = size_t(2) * n * stride;
+    size_t cap = 0;
+    uint8_t* buf = take_pf_buffer(wire + size_t(2) * n * 8, cap);
+    if (!buf) return -1;
+    // The slot ids of both halves after the records: the device layout of a
+    // launch of exactly this group ([2n records][2n slot ids]).
+    for (uint32_t h = 0; h < 2; ++h)
+        for (uint32_t r = 0; r < n; ++r) memcpy(buf + wire + (size_t(h) * n + r) * 8, &mapping[2 * r + 1], 8);
+    auto pk = new_prefetch(s, keys, k_base, host_block_bytes, mapping, n, 0, layer, codec_bits, heads, head_dim,
+                           bytes, buf);
+    pk->cap = cap;
+    pk->group_ids = buf + wire;
+    pk->group_records = 2 * n;
+    auto pv = new_prefetch(s, keys, v_base, host_block_bytes, mapping, n, 1, layer, codec_bits, heads, head_dim,
+                           bytes, buf + size_t(n) * stride);
+    pv->owner = pk;
+    // K then V: the tickets a group's two swaps take in that order.
+    pk->t0 = si_internal::reserve_tickets(2 * n);
+    pv->t0 = pk->t0 + n;
+    if (!si_internal::replay_reserve_range(pk->t0, 2 * uint64_t(n))) return -1;
+    std::vector<std::function<void()>> tasks;
+    queue_seals(pk, tasks);
+    queue_seals(pv, tasks);
     Pool::get().submit_all(tasks);
     return 0;
 }

@@ -644,12 +644,24 @@ class NativeTransfer:
         for kind in (0, 1):
             src = self._host_pool(host[kind])
             pools.append((ct.c_void_p(src.data_ptr()), src.stride(0) * src.element_size(), src.shape[0]))
-        prefetch, h = lib().secure_infer_h2d_prefetch, self.session._h
+        L, h = lib(), self.session._h
+        prefetch = L.secure_infer_h2d_prefetch
+        heads, dim = self.shape.heads, self.shape.head_dim
+        # One stream and K / V pools of one geometry: a group's K and V swaps
+        # are sealed together into one buffer, which the group's launch
+        # copies in one DMA (same tickets as two prefetches: K, then V).
+        paired = len(self.streams) == 1 and pools[0][1:] == pools[1][1:]
         for _, parts in self._plan(mapping):
+            if paired:
+                (_, _, part), _ = parts
+                sp, sbb, sn = pools[0]
+                ok &= L.secure_infer_h2d_prefetch_group(h, sp, pools[1][0], sbb, sn, ct.c_void_p(part.data_ptr()),
+                                                        part.shape[0], layer, bits, heads, dim) == 0
+                continue
             for kind, _, part in parts:
                 sp, sbb, sn = pools[kind]
                 ok &= prefetch(h, sp, sbb, sn, ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer, bits,
-                               self.shape.heads, self.shape.head_dim) == 0
+                               heads, dim) == 0
         self._prefetched.add(layer)
         return ok
 

@@ -525,6 +525,88 @@ def test_group_launch_mixes_sources_and_ticket_runs():
         si.clear_host_ranges()
 
 
+@pytest.mark.parametrize("same_slots", [True, False], ids=["one_copy", "slots_differ"])
+def test_group_prefetch_serves_the_group_launch(same_slots):
+    """secure_infer_h2d_prefetch_group seals a group's K and V records (and its
+    slot ids) into one buffer under tickets K then V.  The group's launch
+    takes them in one copy when its slots are the prefetched ones, and falls
+    back to separate record and slot-id copies when they are not; either way
+    both swaps are served by the prefetch and the caches end bit-exact."""
+    rng = np.random.default_rng(145)
+    heads, dim, ncpu, nslots, layer = 2, 128, 9, 16, 4
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 6, max_record_bytes=shape.record_bytes)
+    L = _lib.load()
+    si.clear_host_ranges()
+    try:
+        hk, hv = pools(rng, ncpu, heads, dim)
+        si.register_host_range(hk, layer, 0)
+        si.register_host_range(hv, layer, 1)
+        ck, cv = caches(nslots, heads, dim)
+        cpu_ids = np.array([8, 1, 4, 0, 6])
+        slot_ids = np.array([3, 15, 0, 9, 7])
+        pre_slots = slot_ids if same_slots else slot_ids[::-1].copy()
+        m = torch.from_numpy(np.stack([cpu_ids, slot_ids], 1).astype(np.int64)).contiguous()
+        mp = torch.from_numpy(np.stack([cpu_ids, pre_slots], 1).astype(np.int64)).contiguous()
+        stream = torch.cuda.current_stream().cuda_stream
+        bb = hk[0].numel() * 2
+        t0 = si.new_transfer_ticket()
+        assert L.secure_infer_h2d_prefetch_group(sess._h, ct.c_void_p(hk.data_ptr()), ct.c_void_p(hv.data_ptr()),
+                                                 bb, ncpu, ct.c_void_p(mp.data_ptr()), len(cpu_ids), layer, 0,
+                                                 heads, dim) == 0
+        assert si.new_transfer_ticket() == t0 + 2 * len(cpu_ids) + 1  # K then V tickets, one run
+        before = si.transfer_prefetch_stats()
+
+        def swap(pool, cache, kind):
+            return L.secure_infer_h2d_swap(ct.c_void_p(stream), sess._h, ct.c_void_p(pool.data_ptr()), bb, ncpu,
+                                           ct.c_void_p(cache.data_ptr()), bb, nslots, ct.c_void_p(m.data_ptr()),
+                                           len(cpu_ids), kind, layer, 0, heads, dim, None)
+
+        assert L.secure_infer_h2d_layer_group_begin(2 * len(cpu_ids)) == 0
+        assert swap(hk, ck, 0) == 0 and swap(hv, cv, 1) == 0
+        assert L.secure_infer_h2d_layer_group_end() == 0
+        assert si.NativeTransfer(sess, shape).wait_layer(layer) == 0
+        after = si.transfer_prefetch_stats()
+        assert after["ready"] + after["busy_fallback"] - before["ready"] - before["busy_fallback"] == 2
+        assert after["missing_fallback"] == before["missing_fallback"]
+        idx = torch.from_numpy(slot_ids.astype(np.int64)).to(DEV)
+        cid = torch.from_numpy(cpu_ids.astype(np.int64))
+        assert torch.equal(ck.index_select(0, idx).cpu(), hk.index_select(0, cid))
+        assert torch.equal(cv.index_select(0, idx).cpu(), hv.index_select(0, cid))
+        untouched = np.setdiff1d(np.arange(nslots), slot_ids)
+        assert (host(ck)[untouched].view(np.uint8) == 0x3C).all()
+    finally:
+        si.inject_h2d_tamper(shots=0)
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()
+
+
+def test_group_prefetch_tamper_is_retried():
+    """A record of a group prefetch corrupted after sealing fails once and is
+    re-sealed from its host block; the layer authenticates."""
+    rng = np.random.default_rng(146)
+    heads, dim, ncpu, nslots, layer = 2, 128, 6, 12, 5
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 7, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        hk, hv = pools(rng, ncpu, heads, dim)
+        si.register_host_range(hk, layer, 0)
+        si.register_host_range(hv, layer, 1)
+        ck, cv = caches(nslots, heads, dim)
+        mapping = torch.tensor([[5, 2], [0, 11], [3, 7]], dtype=torch.int64)
+        si.inject_h2d_tamper(layer=layer, kind=0, host_block=0, shots=1)
+        nt = si.NativeTransfer(sess, shape)  # one stream: group prefetches
+        nt.layer = layer
+        nt.single_layer_kv_transfer(((hk, hv), mapping), (ck, cv))
+        assert nt.wait_layer(layer) == 0
+        for c, sl in mapping.tolist():
+            assert torch.equal(ck[sl].cpu(), hk[c]) and torch.equal(cv[sl].cpu(), hv[c])
+    finally:
+        si.inject_h2d_tamper(shots=0)
+        si.clear_host_ranges()
+
+
 def test_job_authentication_spans_layers():
     """secure_infer_recovery_wait_job_authentication (secure_infer.cpp:7336-7372):
     every record of the job on every layer, no retry; 1 / 0 / -1."""

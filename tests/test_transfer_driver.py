@@ -64,6 +64,15 @@ class Recorder:
         self.calls.append(("prefetch", kind, layer, bits, [(arr[2 * i], arr[2 * i + 1]) for i in range(n)]))
         return 0
 
+    def secure_infer_h2d_prefetch_group(self, sess, k_base, v_base, host_block_bytes, host_nblocks, mapping_ptr, n,
+                                        layer, bits, heads, dim):
+        # the K swap's prefetch, then the V swap's (the tickets' order)
+        self.secure_infer_h2d_prefetch(sess, k_base, host_block_bytes, host_nblocks, mapping_ptr, n, 0, layer,
+                                       bits, heads, dim)
+        self.calls.append(("prefetch_group_pairs_with_previous",))
+        return self.secure_infer_h2d_prefetch(sess, v_base, host_block_bytes, host_nblocks, mapping_ptr, n, 1,
+                                              layer, bits, heads, dim)
+
 
 def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False,
                  pipeline_seal=True):
@@ -83,7 +92,7 @@ def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep
          mock.patch.object(gcm.torch.cuda, "current_stream", return_value=parent):
         nt.single_layer_kv_transfer((host, mapping), dest, None, False, 2, True, False)
     if not keep_prefetch:
-        rec.calls = [c for c in rec.calls if c[0] != "prefetch"]
+        rec.calls = [c for c in rec.calls if not c[0].startswith("prefetch")]
     return nt, rec, parent
 
 
@@ -175,6 +184,8 @@ def test_layer_seals_are_queued_in_swap_order():
     pre = [(c[1], c[2], c[4]) for c in rec.calls if c[0] == "prefetch"]
     swaps = [(c[2], c[3], c[5]) for c in rec.calls if c[0] == "swap"]
     assert pre == swaps and len(pre) == 6
+    # one stream: each group's K and V are sealed as one group prefetch
+    assert len([c for c in rec.calls if c[0] == "prefetch_group_pairs_with_previous"]) == 3
     first_swap = next(i for i, c in enumerate(rec.calls) if c[0] == "swap")
     last_prefetch = max(i for i, c in enumerate(rec.calls) if c[0] == "prefetch")
     assert last_prefetch < first_swap
