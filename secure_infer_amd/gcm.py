@@ -550,24 +550,26 @@ class NativeTransfer:
         self._prefetched = set()
 
     def _plan(self, mapping: torch.Tensor):
-        """Groups of (kind, slice index, mapping part) in submission order:
-        causal groups of ``causal_group_blocks`` from the tail, then K / V,
-        then the slice streams' stripes."""
+        """Groups of (kind, slice index, address of the mapping part, rows) in
+        submission order: causal groups of ``causal_group_blocks`` from the
+        tail, then K / V, then the slice streams' stripes.  A part is a row
+        range of the contiguous [N, 2] int64 mapping, passed by address (a
+        torch slice and copy per part cost ~25 us per layer in Python)."""
         n = int(mapping.shape[0])
+        base = mapping.data_ptr()
         group = self.causal_group_blocks
         g = group if group and n > group else n
         nsl = len(self.streams)
         plan, end = [], n
         while end > 0:
             start = max(0, end - g)
-            m = mapping[start:end]
             k = end - start
             parts = []
             for kind in (0, 1):
                 for j in range(nsl):
-                    part = m[k * j // nsl:k * (j + 1) // nsl].contiguous()
-                    if part.shape[0]:
-                        parts.append((kind, j, part))
+                    r0, r1 = start + k * j // nsl, start + k * (j + 1) // nsl
+                    if r1 > r0:
+                        parts.append((kind, j, ct.c_void_p(base + 16 * r0), r1 - r0))
             plan.append((k, parts))
             end = start
         return plan
@@ -619,10 +621,10 @@ class NativeTransfer:
         for k, parts in plan:
             _check(L.secure_infer_h2d_layer_group_begin(2 * k), "h2d_layer_group_begin")
             try:
-                for kind, j, part in parts:
+                for kind, j, part, rows in parts:
                     sp, sbb, sn, dp, dbb, dn = pools[kind]
-                    _check(swap(handles[j], h, sp, sbb, sn, dp, dbb, dn, ct.c_void_p(part.data_ptr()),
-                                part.shape[0], kind, layer, bits, heads, dim, None), "h2d_swap")
+                    _check(swap(handles[j], h, sp, sbb, sn, dp, dbb, dn, part, rows, kind, layer, bits, heads,
+                                dim, None), "h2d_swap")
             finally:
                 _check(L.secure_infer_h2d_layer_group_end(), "h2d_layer_group_end")
         for st in streams:
@@ -653,15 +655,14 @@ class NativeTransfer:
         paired = len(self.streams) == 1 and pools[0][1:] == pools[1][1:]
         for _, parts in self._plan(mapping):
             if paired:
-                (_, _, part), _ = parts
+                (_, _, part, rows), _ = parts
                 sp, sbb, sn = pools[0]
-                ok &= L.secure_infer_h2d_prefetch_group(h, sp, pools[1][0], sbb, sn, ct.c_void_p(part.data_ptr()),
-                                                        part.shape[0], layer, bits, heads, dim) == 0
+                ok &= L.secure_infer_h2d_prefetch_group(h, sp, pools[1][0], sbb, sn, part, rows, layer, bits, heads,
+                                                        dim) == 0
                 continue
-            for kind, _, part in parts:
+            for kind, _, part, rows in parts:
                 sp, sbb, sn = pools[kind]
-                ok &= prefetch(h, sp, sbb, sn, ct.c_void_p(part.data_ptr()), part.shape[0], kind, layer, bits,
-                               heads, dim) == 0
+                ok &= prefetch(h, sp, sbb, sn, part, rows, kind, layer, bits, heads, dim) == 0
         self._prefetched.add(layer)
         return ok
 
