@@ -10,8 +10,10 @@ launch takes only appear at these sizes), checked record by record:
 * int4 Llama-3-70B writeback: 256 blocks -> 512 packets of 81,936 B (pairs of
   whole records per workgroup).
 
-Reload ciphertext comes from OpenSSL (the reference's host AES-128-GCM) over
-the oracle's packets; outputs must equal the input blocks (bf16) or the
+The bf16 and int4 reload layers also run end to end through the host
+pipeline (host pools, NativeTransfer with 16-block causal groups, group
+prefetch).  Reload ciphertext comes from OpenSSL (the reference's host
+AES-128-GCM) over the oracle's packets; outputs must equal the input blocks (bf16) or the
 oracle decode of the packets, bit for bit, and every record's status must be
 1 except the tampered ones (0, slot zeroed on the device).  Writeback
 ciphertext and tags must equal OpenSSL's over the oracle's packets.
@@ -128,3 +130,46 @@ def test_full_size_writeback_layer_int4_llama3_70b():
         c, tag = O.ossl_gcm_encrypt(KEY, O.iv12_from_words(W.record_iv(SALT, t0 + r)), aad, pkt)
         assert np.array_equal(ww[r, :n], c), f"record {r} ciphertext"
         assert ww[r, toff:toff + 16].tobytes() == tag, f"record {r} tag"
+
+
+@pytest.mark.parametrize("bits,heads,nb", [(0, 8, 48), (4, 4, 64)], ids=["bf16_llama3_8b", "int4_qwen2_5_7b"])
+def test_full_size_layer_through_the_host_pipeline(bits, heads, nb):
+    """A full-size layer end to end: host pools -> NativeTransfer with the
+    reference's 16-block causal groups (host OpenSSL seals, group prefetch,
+    one DMA per group launch) -> fused reload into a 512-slot cache; every
+    slot equals its host block (bf16) or the oracle decode of its packet, and
+    the other slots are untouched."""
+    rng = np.random.default_rng(2000 + bits)
+    dim, nslots, layer = 128, 512, 9
+    shape = si.LayerShape(heads, dim, bits)
+    sess = si.GcmSession(KEY, SALT, 31, max_record_bytes=shape.record_bytes)
+    blocks = [W.bf16_blocks(rng, nb, heads, dim) for _ in range(2)]
+    if bits:
+        host = [torch.from_numpy(np.stack([O.codec_encode(blocks[k][i], bits, k, layer) for i in range(nb)]))
+                for k in range(2)]
+    else:
+        host = [torch.from_numpy(np.stack(blocks[k]).view(np.int16)).contiguous() for k in range(2)]
+    slots = rng.permutation(nslots)[:nb]
+    mapping = torch.from_numpy(np.stack([np.arange(nb), slots], 1).astype(np.int64))
+    caches = [torch.zeros((nslots, 128, heads, dim), dtype=torch.int16, device=DEV) for _ in range(2)]
+    for c in caches:
+        c.view(torch.uint8).fill_(0x3C)
+    si.clear_host_ranges()
+    try:
+        si.register_host_range(host[0], layer, 0)
+        si.register_host_range(host[1], layer, 1)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16)
+        nt.layer = layer
+        nt.single_layer_kv_transfer((host, mapping), caches)
+        assert nt.wait_layer(layer) == 0
+        torch.cuda.synchronize()
+        idx = torch.from_numpy(slots.astype(np.int64)).to(DEV)
+        for k in range(2):
+            got = caches[k].index_select(0, idx).cpu().numpy().view(np.uint16)
+            want = np.stack(blocks[k]) if not bits else np.stack(
+                [O.codec_decode(host[k][i].numpy(), heads, dim, bits, k) for i in range(nb)])
+            assert np.array_equal(got, want)
+            rest = torch.from_numpy(np.setdiff1d(np.arange(nslots), slots).astype(np.int64)).to(DEV)
+            assert bool((caches[k].index_select(0, rest).view(torch.uint8) == 0x3C).all())
+    finally:
+        si.clear_host_ranges()
