@@ -12,7 +12,7 @@ launch takes only appear at these sizes), checked record by record:
 
 The bf16 and int4 reload layers also run end to end through the host
 pipeline (host pools, NativeTransfer with 16-block causal groups, group
-prefetch).  Reload ciphertext comes from OpenSSL (the reference's host
+prefetch), and the 70B layer through the D2H store into host packet pools.  Reload ciphertext comes from OpenSSL (the reference's host
 AES-128-GCM) over the oracle's packets; outputs must equal the input blocks (bf16) or the
 oracle decode of the packets, bit for bit, and every record's status must be
 1 except the tampered ones (0, slot zeroed on the device).  Writeback
@@ -173,3 +173,25 @@ def test_full_size_layer_through_the_host_pipeline(bits, heads, nb):
             assert bool((caches[k].index_select(0, rest).view(torch.uint8) == 0x3C).all())
     finally:
         si.clear_host_ranges()
+
+
+def test_full_size_writeback_through_the_host_pipeline():
+    """One 70B int4 layer stored end to end: 256 blocks x K/V gathered from a
+    512-slot cache, quantised, sealed on the device, copied down and
+    authenticated by OpenSSL into host packet pools (D2HTransfer, 16-block
+    groups); every packet equals the oracle's encoding of its block."""
+    rng = np.random.default_rng(3004)
+    heads, dim, nslots, nb, layer = 8, 128, 512, 256, 61
+    shape = si.LayerShape(heads, dim, 4)
+    sess = si.GcmSession(KEY, SALT, 32, max_record_bytes=shape.record_bytes)
+    blocks = [W.bf16_blocks(rng, nslots, heads, dim) for _ in range(2)]
+    src = [tuple(dev(blocks[k].view(np.int16)) for k in range(2))]
+    slots = rng.permutation(nslots)[:nb]
+    width = shape.record_bytes
+    pools = [(torch.zeros((nb, width), dtype=torch.uint8), torch.zeros((nb, width), dtype=torch.uint8))]
+    mapping = torch.from_numpy(np.stack([slots, np.arange(nb)], 1).astype(np.int64))
+    si.D2HTransfer(sess, shape, group_blocks=16).store(src, pools, mapping, layers=[layer])
+    for k in range(2):
+        got = pools[0][k].numpy()
+        for i in range(nb):
+            assert np.array_equal(got[i], O.codec_encode(blocks[k][slots[i]], 4, k, layer)), (k, i)
