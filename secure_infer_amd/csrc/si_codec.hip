@@ -181,11 +181,10 @@ __device__ __forceinline__ float quant_scale(float lo, float hi, float qmax)
 
 // RN((x - lo) / s) rounded half-to-even, clamped to [0, qmax] and inserted
 // as byte K of acc.
-template <int K>
-__device__ __forceinline__ uint32_t quant_byte(float x, float lo, float s, float y, uint32_t bits,
-                                               uint32_t acc)
+template <int K, uint32_t kBits>
+__device__ __forceinline__ uint32_t quant_byte(float x, float lo, float s, float y, uint32_t acc)
 {
-    return insert_q<K>(div_rn(__fsub_rn(x, lo), s, y), bits, acc);
+    return insert_q<K>(div_rn(__fsub_rn(x, lo), s, y), kBits, acc);
 }
 
 __device__ __forceinline__ void unpack8(uint4 w, float x[8])
@@ -201,20 +200,20 @@ __device__ __forceinline__ void unpack8(uint4 w, float x[8])
 // 8 consecutive elements -> int8 bytes (2 dwords) or int4 nibbles (1 dword,
 // element 2i in the low nibble).  Column-dependent parameters come in
 // lo[k] / s[k] / y[k] with stride `ps` (1: per element, 0: shared).
-template <int PS>
+template <int PS, uint32_t kBits>
 __device__ __forceinline__ void quant8(const float x[8], const float* lo, const float* s, const float* y,
-                                       uint32_t bits, uint32_t out[2])
+                                       uint32_t out[2])
 {
     uint32_t d0 = 0, d1 = 0;
-    d0 = quant_byte<0>(x[0], lo[0], s[0], y[0], bits, d0);
-    d0 = quant_byte<1>(x[1], lo[PS], s[PS], y[PS], bits, d0);
-    d0 = quant_byte<2>(x[2], lo[2 * PS], s[2 * PS], y[2 * PS], bits, d0);
-    d0 = quant_byte<3>(x[3], lo[3 * PS], s[3 * PS], y[3 * PS], bits, d0);
-    d1 = quant_byte<0>(x[4], lo[4 * PS], s[4 * PS], y[4 * PS], bits, d1);
-    d1 = quant_byte<1>(x[5], lo[5 * PS], s[5 * PS], y[5 * PS], bits, d1);
-    d1 = quant_byte<2>(x[6], lo[6 * PS], s[6 * PS], y[6 * PS], bits, d1);
-    d1 = quant_byte<3>(x[7], lo[7 * PS], s[7 * PS], y[7 * PS], bits, d1);
-    if (bits == 8) {
+    d0 = quant_byte<0, kBits>(x[0], lo[0], s[0], y[0], d0);
+    d0 = quant_byte<1, kBits>(x[1], lo[PS], s[PS], y[PS], d0);
+    d0 = quant_byte<2, kBits>(x[2], lo[2 * PS], s[2 * PS], y[2 * PS], d0);
+    d0 = quant_byte<3, kBits>(x[3], lo[3 * PS], s[3 * PS], y[3 * PS], d0);
+    d1 = quant_byte<0, kBits>(x[4], lo[4 * PS], s[4 * PS], y[4 * PS], d1);
+    d1 = quant_byte<1, kBits>(x[5], lo[5 * PS], s[5 * PS], y[5 * PS], d1);
+    d1 = quant_byte<2, kBits>(x[6], lo[6 * PS], s[6 * PS], y[6 * PS], d1);
+    d1 = quant_byte<3, kBits>(x[7], lo[7 * PS], s[7 * PS], y[7 * PS], d1);
+    if (kBits == 8) {
         out[0] = d0;
         out[1] = d1;
     } else {
@@ -225,9 +224,10 @@ __device__ __forceinline__ void quant8(const float x[8], const float* lo, const 
     }
 }
 
-__device__ __forceinline__ void store_q8(uint8_t* pkt, uint32_t e, uint32_t bits, const uint32_t w[2])
+template <uint32_t kBits>
+__device__ __forceinline__ void store_q8(uint8_t* pkt, uint32_t e, const uint32_t w[2])
 {
-    if (bits == 8) *reinterpret_cast<uint2*>(pkt + e) = make_uint2(w[0], w[1]);
+    if (kBits == 8) *reinterpret_cast<uint2*>(pkt + e) = make_uint2(w[0], w[1]);
     else *reinterpret_cast<uint32_t*>(pkt + e / 2u) = w[0];
 }
 
@@ -241,6 +241,7 @@ __device__ __forceinline__ void store_header(const CodecBatch& b, uint8_t* pkt, 
 // K: eight lanes per (token group of 64, 8 consecutive columns), each lane 8
 // tokens held in registers; the column min / max is reduced across the eight
 // lanes, so the slot is read once.  Workgroup bx of K record r.
+template <uint32_t kBits>
 __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, uint32_t bx)
 {
     const uint32_t hd = b.heads * b.dim;
@@ -255,7 +256,7 @@ __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, u
     const uint32_t l8 = idx & 7u, cg = idx >> 3;
     const uint32_t g = cg >= nch ? 1u : 0u;
     const uint32_t col = (cg - g * nch) * 8u;
-    const float qmax = float((1u << b.bits) - 1u);
+    const float qmax = float((1u << kBits) - 1u);
     const uint8_t* slot = b.cache[0] + uint64_t(bad ? 0 : sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
     if (idx == 0) store_header(b, pkt, 0u);
@@ -313,8 +314,8 @@ __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, u
         float x[8];
         unpack8(raw[tt], x);
         uint32_t w[2];
-        quant8<1>(x, lo, sc, rc, b.bits, w);
-        store_q8(pkt, (t0 + tt) * hd + col, b.bits, w);
+        quant8<1, kBits>(x, lo, sc, rc, w);
+        store_q8<kBits>(pkt, (t0 + tt) * hd + col, w);
     }
 }
 
@@ -322,6 +323,7 @@ __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, u
 // V: two lanes per (token, head, dim group of 64), 32 consecutive elements
 // each; the group's min / max meets in one DPP swap, and the group's scale
 // and reciprocal are formed once per 32 elements.  Workgroup bx of V record r.
+template <uint32_t kBits>
 __device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, uint32_t bx)
 {
     const uint32_t hd = b.heads * b.dim;
@@ -333,7 +335,7 @@ __device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, u
     const int64_t sid = b.slots[r];
     const bool bad = sid < 0 || sid >= b.nslots;  // encode zeros, as in quant_k_block
     const uint32_t gi = idx >> 1, half = idx & 1u;
-    const float qmax = float((1u << b.bits) - 1u);
+    const float qmax = float((1u << kBits) - 1u);
     const uint8_t* slot = b.cache[1] + uint64_t(bad ? 0 : sid) * b.slot_bytes;
     uint8_t* pkt = b.staging + uint64_t(r) * b.staging_stride;
     if (idx == 0) store_header(b, pkt, 1u);
@@ -360,11 +362,11 @@ __device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, u
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         uint32_t p2[2];
-        quant8<0>(x + 8 * k, &lo, &s, &y, b.bits, p2);
+        quant8<0, kBits>(x + 8 * k, &lo, &s, &y, p2);
         w[2 * k] = p2[0];
         w[2 * k + 1] = p2[1];
     }
-    if (b.bits == 8) {
+    if (kBits == 8) {
         uint4* dst = reinterpret_cast<uint4*>(pkt + e);
         dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
         dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
@@ -378,14 +380,15 @@ __device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, u
 // token rows per lane), the V blocks stream; in one grid the V blocks fill
 // the machine while the K blocks drain (MI355X, Llama-3-70B int4 layer: 22.7
 // + 18.8 us as two launches, 6.5 us less per layer as one).
+template <uint32_t kBits>
 __global__ __launch_bounds__(256) void quant_kernel(CodecBatch b, uint32_t kx, uint32_t vx)
 {
     const uint32_t nkb = kx * b.n_k;
     if (blockIdx.x < nkb) {
-        quant_k_block(b, blockIdx.x / kx, blockIdx.x % kx);
+        quant_k_block<kBits>(b, blockIdx.x / kx, blockIdx.x % kx);
     } else {
         const uint32_t v = blockIdx.x - nkb;
-        quant_v_block(b, b.n_k + v / vx, v % vx);
+        quant_v_block<kBits>(b, b.n_k + v / vx, v % vx);
     }
 }
 
@@ -409,8 +412,11 @@ hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b)
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nv = b.nrec - b.n_k;
     const uint32_t kx = (2u * hd + 255u) / 256u, vx = (4u * hd + 255u) / 256u;
-    if (b.n_k + nv)
-        hipLaunchKernelGGL(quant_kernel, dim3(kx * b.n_k + vx * nv), dim3(256), 0, stream, b, kx, vx);
+    if (b.n_k + nv) {
+        const dim3 grid(kx * b.n_k + vx * nv);
+        if (b.bits == 8) hipLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, b, kx, vx);
+        else hipLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, b, kx, vx);
+    }
     return hipGetLastError();
 }
 
