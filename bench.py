@@ -236,7 +236,8 @@ def ledger_split(path: Path, steps: int) -> dict:
     return out
 
 
-def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer, steps, truth):
+def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer, steps, truth,
+               slice_streams=1, stripe=False):
     """The same layers through the host-memory path: reload = host OpenSSL seal
     into the pinned ring, H2D on the library's copy stream, fused kernel;
     writeback = fused kernel, D2H, host authentication into host pools.  Wall
@@ -267,7 +268,14 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
     out = {"host_threads": int(si._lib.load().secure_infer_host_threads())}
     if op == "reload":
         cache.zero_()
-        nt = si.NativeTransfer(sess, shape, causal_group_blocks=LOAD_CHUNK_BLOCKS)
+        # Slice streams as the reference's PIPE_GCM_H2D_SLICE_STREAMS (npu_predict.py:130-155):
+        # 1 = the caller's stream only; more, with `stripe`, stripe each
+        # group's swaps over side streams that the caller's stream joins.
+        streams = [torch.cuda.Stream() for _ in range(slice_streams)] if slice_streams > 1 else None
+        nt = si.NativeTransfer(sess, shape, streams=streams, causal_group_blocks=LOAD_CHUNK_BLOCKS,
+                               stripe=stripe)
+        out["slice_streams"] = slice_streams
+        out["stripe"] = bool(stripe)
         lib = si._lib.load()
 
         def step(ahead):
@@ -353,6 +361,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=3,
                     help="steps of the host-memory path (host seal + pinned ring + PCIe); 0 = skip")
+    ap.add_argument("--slice-streams", type=int, default=1,
+                    help="slice streams of the end-to-end reload (the reference's PIPE_GCM_H2D_SLICE_STREAMS, default 1)")
+    ap.add_argument("--stripe", action="store_true",
+                    help="stripe each causal group over the slice streams as the reference does")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC byte calibration)")
     args = ap.parse_args()
@@ -567,7 +579,8 @@ def main():
             import tempfile
             os.environ["SECURE_INFER_H2D_PROFILE"] = os.path.join(tempfile.mkdtemp(), "h2d_ledger.csv")
         res["end_to_end"] = end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer,
-                                       args.e2e_steps, truth if (op == "reload" and bits == 0) else None)
+                                       args.e2e_steps, truth if (op == "reload" and bits == 0) else None,
+                                       max(1, min(args.slice_streams, 8)), args.stripe)
     print(json.dumps(res), flush=True)
 
 

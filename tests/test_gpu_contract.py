@@ -367,10 +367,11 @@ def test_reference_ticket_order_layer_authenticates(ranges):
     assert torch.equal(cv.index_select(0, idx), want[nb:])
 
 
-@pytest.mark.parametrize("slices", [1, 2])
-def test_causal_groups_through_the_host_pipeline(ranges, slices):
+@pytest.mark.parametrize("slices,stripe", [(1, False), (2, True), (2, False)])
+def test_causal_groups_through_the_host_pipeline(ranges, slices, stripe):
     """NativeTransfer with 16-block causal groups over 41 host blocks, on one
-    stream or striped over two slice streams (native_layerwise.py:113-129):
+    stream, striped over two slice streams (native_layerwise.py:113-129) or
+    given two slice streams without striping:
     every block lands bit-exactly and tickets advance by one per record, plus
     one for a V record sealed with a one-shot fault and sealed again by the
     strict retry."""
@@ -385,7 +386,7 @@ def test_causal_groups_through_the_host_pipeline(ranges, slices):
     slot_ids = rng.permutation(nslots)[:ncpu]
     mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
     streams = None if slices == 1 else [torch.cuda.current_stream(), torch.cuda.Stream()]
-    nt = si.NativeTransfer(sess, shape, streams=streams, causal_group_blocks=16)
+    nt = si.NativeTransfer(sess, shape, streams=streams, causal_group_blocks=16, stripe=stripe)
     nt.layer = layer
     si.inject_h2d_tamper(layer=layer, kind=1, host_block=30, shots=1)
     t_before = si.new_transfer_ticket()

@@ -75,14 +75,14 @@ class Recorder:
 
 
 def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False,
-                 pipeline_seal=True):
+                 pipeline_seal=True, stripe=False):
     rec = Recorder()
     parent = FakeStream("parent")
     shape = shape or si.LayerShape(2, 64)
     sess = mock.Mock()
     sess._h = None
     nt = si.NativeTransfer(sess, shape, streams=streams or None, causal_group_blocks=group,
-                           pipeline_seal=pipeline_seal)
+                           pipeline_seal=pipeline_seal, stripe=stripe)
     nt.layer = layer
     host = [torch.zeros((nblocks, 4), dtype=torch.int16), torch.zeros((nblocks, 4), dtype=torch.int16)]
     dest = [torch.zeros((nslots or nblocks + 100, 4), dtype=torch.int16) for _ in range(2)]
@@ -129,12 +129,28 @@ def test_record_order_is_layer_group_kind_block():
 
 def test_slice_streams_stripe_rows_and_join():
     s1, s2 = FakeStream("s1"), FakeStream("s2")
-    _, rec, parent = run_transfer(10, 0, [s1, s2])
+    _, rec, parent = run_transfer(10, 0, [s1, s2], stripe=True)
     swaps = [c for c in rec.calls if c[0] == "swap"]
     assert [(c[1], c[2], len(c[5])) for c in swaps] == [
         (s1.cuda_stream, 0, 5), (s2.cuda_stream, 0, 5), (s1.cuda_stream, 1, 5), (s2.cuda_stream, 1, 5)]
     assert s1.waits == ["parent"] and s2.waits == ["parent"]
     assert parent.waits == ["s1", "s2"]
+
+
+def test_unstriped_slice_streams_keep_the_striped_ticket_order():
+    """Without striping, every row goes to the first slice stream, K then V, in
+    the order the stripes would take their tickets; the group is one launch
+    and only the stream that carries it is joined."""
+    s1, s2 = FakeStream("s1"), FakeStream("s2")
+    _, rec_s, _ = run_transfer(10, 0, [s1, s2], stripe=True)
+    t1, t2 = FakeStream("s1"), FakeStream("s2")
+    _, rec, parent = run_transfer(10, 0, [t1, t2])
+    swaps = [c for c in rec.calls if c[0] == "swap"]
+    assert [(c[1], c[2], len(c[5])) for c in swaps] == [(t1.cuda_stream, 0, 10), (t1.cuda_stream, 1, 10)]
+    order = [(c[2], h) for c in swaps for h, _ in c[5]]
+    striped = [(c[2], h) for c in rec_s.calls if c[0] == "swap" for h, _ in c[5]]
+    assert order == striped
+    assert t1.waits == ["parent"] and t2.waits == [] and parent.waits == ["s1"]
 
 
 def test_swap_carries_pool_sizes():
