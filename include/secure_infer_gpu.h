@@ -234,16 +234,38 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* session,
  * packet staging) lives in one 64 MiB device array per GPU
  * (SI_NOALLOC_SCRATCH_BYTES below, held until the process ends) instead of
  * per-stream workspaces and the caller's staging buffer: desc->staging must
- * be NULL.  Limits: at most 8192 records, and 256 KiB of accumulators +
- * pair parking (12 KiB per workgroup when the records outnumber the CUs) +
- * nrec * align32(bytes) of staging (codec only) within the 64 MiB; a larger
- * request returns -1 with a message on stderr.  The first call on a GPU
- * clears the accumulators on `stream` and waits for it (unless the stream
- * is capturing).  Every call on one GPU shares that GPU's array: calls whose
- * work overlaps on one GPU (other streams, or other threads) race and must
- * be serialised by the caller. */
+ * be NULL.  Limits: at most 8192 records, and 256 B of control words +
+ * 256 KiB of accumulators + pair parking (12 KiB per workgroup when the
+ * records outnumber the CUs) + nrec * align32(bytes) of staging (codec only)
+ * within the 64 MiB; a larger request returns -1 with a message on stderr.
+ * The first call on a GPU clears the control words and accumulators on
+ * `stream` and waits for it (a capturing stream skips the clear: the array
+ * is zero when the library loads).
+ * Every call on one GPU shares that GPU's array, so each call first takes it
+ * for itself with a one-thread device kernel (compare-and-swap of an owner
+ * word with a fresh token; the token is written into bytes 4..7 of record
+ * 0's status slot, which must therefore be writable) and returns it with a
+ * last kernel.  A call whose work overlaps another's on the same GPU (other
+ * streams, other threads) and finds the array taken does not wait: it
+ * touches no scratch and fails closed -- every record gets status 0 (wire
+ * record and status_out), its output extent is zeroed (bf16 payload, or the
+ * whole bf16 block of a codec record; slots out of range are not touched)
+ * and fail_count grows by nrec.  So overlapping calls never mix their
+ * scratch, and no record keeps unverified plaintext without being counted
+ * as failed.  Callers that need every call to verify serialise them. */
 int secure_infer_gpu_reload_layer_noalloc(hipStream_t stream, si_session* session,
                                           const si_reload_desc* desc);
+
+/* Kernel timing of the calling thread's next layer call (one shot; no
+ * reference counterpart -- the reference's per-copy profile rows,
+ * secure_infer.cpp:1826-1951, time its AICPU tasks): the next
+ * secure_infer_gpu_reload_layer, _reload_layer_noalloc or _writeback_layer
+ * launches its first kernel with `start` and its last kernel with `stop` as
+ * hipExtLaunchKernel events, which take the kernels' own dispatch start and
+ * end times (an event recorded between kernels also times the launch gap).
+ * Either may be NULL; both must have been created by the caller.  0, or -1
+ * if both are NULL. */
+int secure_infer_gpu_time_next_layer(hipEvent_t start, hipEvent_t stop);
 
 /* One layer of writeback: record r gathers cache[kind] + slots[r]*slot_bytes,
  * optionally quantises it with the transport codec, encrypts it and writes the
@@ -407,6 +429,11 @@ int secure_infer_test_tamper_d2h(uint32_t shots);
  * proof as it reaches the host, mode 2 sends the all-zero (low-order) public
  * value to the device; either makes the agreement return -1.  0 disarms. */
 int secure_infer_test_tamper_agree(uint32_t mode);
+/* Test-only (no reference counterpart): holds (hold != 0) or releases the
+ * current GPU's allocation-free scratch with a token no call receives, on
+ * `stream`, so a test can make secure_infer_gpu_reload_layer_noalloc find it
+ * taken.  0 or -1.  Production code never calls it. */
+int secure_infer_test_noalloc_hold(hipStream_t stream, int hold);
 int secure_infer_test_x25519(const uint8_t scalar[32], const uint8_t u[32], uint8_t out[32]);
 int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_t* msg, uint64_t msg_len,
                               uint8_t* out, uint32_t out_len);
@@ -479,7 +506,14 @@ int secure_infer_d2h_batch_end(void);
  * thread hands each launch to the pool once its copy is done.  At most 6
  * launches and SECURE_INFER_D2H_INFLIGHT_MB (128) of buffers are in flight
  * per device; an issue beyond that waits.  A failed record is zeroed in the
- * host pool and makes batch_end return -1 (the reference zeroes and aborts). */
+ * host pool and makes batch_end return -1 (the reference zeroes and aborts).
+ * Stream order of the source reads: the device reads a swap's slots when its
+ * launch is issued, which can be as late as batch_device_barrier (the
+ * reference enqueues each swap's read at the call).  So work the caller
+ * queues on `stream` after a swap must not write that swap's source slots
+ * until batch_device_barrier has returned; work queued after the barrier is
+ * ordered behind every read of the batch.  The reference's own D2H driver
+ * calls the barrier right after its last group (npu_predict.py:874-916). */
 int secure_infer_d2h_swap(hipStream_t stream, si_session* session, const void* dev_cache,
                           uint64_t slot_bytes, uint64_t nslots, void* host_base,
                           uint64_t host_block_bytes, uint64_t host_nblocks, const int64_t* mapping,

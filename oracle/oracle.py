@@ -266,9 +266,9 @@ def np_codec_encode(block_bf16: np.ndarray, bits: int, kind: int, layer: int) ->
         scale = np.maximum(scale, np.float32(1e-12))
         q = np.rint(((g - low) / scale).astype(np.float32))
     q = np.clip(q, 0, (1 << bits) - 1).reshape(-1)
+    if bits == 4:  # packed in float: a NaN in either element makes the byte NaN
+        q = q[0::2] + np.float32(16) * q[1::2]
     q = np.where(np.isnan(q), 0, q)  # torch's NaN -> uint8 cast gives 0 on x86
-    if bits == 4:
-        q = q[0::2] + 16 * q[1::2]
     q = q.astype(np.uint8)
     qb, sb = q.size, scale.size * 4
     width = (qb + 2 * sb + 16 + 15) // 16 * 16

@@ -378,7 +378,10 @@ void si_or_codec_encode(const uint16_t* block_bf16, uint32_t heads, uint32_t dim
         volatile float s = diff / qmax;
         scale[p] = s < floor_scale ? floor_scale : s;
     }
-    /* q = ((x-low)/scale).round().clamp(0, 2^bits-1), flattened (t, h, d) */
+    /* q = ((x-low)/scale).round().clamp(0, 2^bits-1), flattened (t, h, d);
+     * int4 then packs q[2j] + 16*q[2j+1] in float (a NaN in either element
+     * makes the byte's value NaN) before the uint8 cast. */
+    float qpair = 0.0f;
     for (uint64_t e = 0; e < n; ++e) {
         uint32_t t = (uint32_t)(e / hd);
         uint32_t hh = (uint32_t)((e % hd) / dim);
@@ -392,13 +395,13 @@ void si_or_codec_encode(const uint16_t* block_bf16, uint32_t heads, uint32_t dim
         if (q > qmax) q = qmax;
         /* round().clamp() keeps NaN; torch's float -> uint8 cast then gives 0
          * (the x86 conversion yields 0x80000000, whose low byte is 0). */
-        uint32_t qi = isnan(q) ? 0u : (uint32_t)q;
         if (bits == 8) {
-            packet[e] = (uint8_t)qi;
+            packet[e] = isnan(q) ? 0u : (uint8_t)(uint32_t)q;
+        } else if ((e & 1) == 0) {
+            qpair = q;
         } else {
-            /* byte j = q[2j] + 16*q[2j+1] */
-            if (e & 1) packet[e >> 1] |= (uint8_t)(qi << 4);
-            else packet[e >> 1] |= (uint8_t)qi;
+            volatile float v = qpair + 16.0f * q;
+            packet[e >> 1] = isnan(v) ? 0u : (uint8_t)(uint32_t)v;
         }
     }
     memcpy(packet + qb, scale, (size_t)sb);

@@ -62,6 +62,7 @@ SIGNATURES = {
     "secure_infer_gpu_reload_layer": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),
     "secure_infer_gpu_reload_layer_noalloc": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),
     "secure_infer_gpu_writeback_layer": ([_v, _v, ct.POINTER(SiWritebackDesc)], _i),
+    "secure_infer_gpu_time_next_layer": ([_v, _v], _i),
     "secure_infer_codec_width": ([_u32, _u32, _u32], _u64),
     "secure_infer_wire_stride": ([_u64], _u64),
     "secure_infer_new_transfer_ticket": ([], _u64),
@@ -81,6 +82,7 @@ SIGNATURES = {
     "secure_infer_test_tamper_h2d": ([ct.c_int32, ct.c_int32, ct.c_int64, _u32], _i),
     "secure_infer_test_tamper_d2h": ([_u32], _i),
     "secure_infer_test_tamper_agree": ([_u32], _i),
+    "secure_infer_test_noalloc_hold": ([_v, _i], _i),
     "secure_infer_retire_transfer_prefetches": ([], None),
     "secure_infer_invalidate_transfer_prefetches": ([], None),
     "secure_infer_get_transfer_prefetch_stats": ([ct.POINTER(_u64)] * 3, None),

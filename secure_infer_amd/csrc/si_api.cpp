@@ -185,6 +185,16 @@ struct DevCtx {
     uint32_t npow = 0;
     uint8_t key[16];
     uint8_t h[16];
+    // L * H of the last few record shapes (L = the length block): it reveals
+    // H, so it lives and dies with the context rather than in a launch cache.
+    struct Lh {
+        uint64_t bytes, aad_bytes;
+        uint32_t w[4];
+    };
+    std::mutex lh_m;
+    Lh lh[4]{};
+    int lh_used = 0, lh_next = 0;
+    void lh_of(uint64_t bytes, uint64_t aad_bytes, uint32_t out[4]);
     ~DevCtx()
     {
         if (dev) {
@@ -193,8 +203,33 @@ struct DevCtx {
         }
         OPENSSL_cleanse(key, sizeof(key));
         OPENSSL_cleanse(h, sizeof(h));
+        OPENSSL_cleanse(lh, sizeof(lh));
     }
 };
+
+void DevCtx::lh_of(uint64_t bytes, uint64_t aad_bytes, uint32_t out[4])
+{
+    std::lock_guard<std::mutex> g(lh_m);
+    for (int i = 0; i < lh_used; ++i)
+        if (lh[i].bytes == bytes && lh[i].aad_bytes == aad_bytes) {
+            memcpy(out, lh[i].w, 16);
+            return;
+        }
+    Blk len{}, hb;
+    put_be64(len.b, aad_bytes * 8u);
+    put_be64(len.b + 8, bytes * 8u);
+    memcpy(hb.b, h, 16);
+    Blk r = gf_mul(len, hb);
+    Lh& e = lh[lh_next];
+    e.bytes = bytes;
+    e.aad_bytes = aad_bytes;
+    for (int k = 0; k < 4; ++k) e.w[k] = le32(r.b + 4 * k);
+    memcpy(out, e.w, 16);
+    OPENSSL_cleanse(hb.b, 16);
+    OPENSSL_cleanse(r.b, 16);
+    lh_next = (lh_next + 1) % 4;
+    if (lh_used < 4) ++lh_used;
+}
 
 // Te0 of the record kernels' T-table AES (public: S-box column 2, 1, 1, 3).
 void te0_table(uint32_t te0[256])
@@ -309,7 +344,7 @@ uint32_t cu_count()
 // The rows cover AAD || C; the length block L, the last block of the GHASH
 // input, adds L * H to every record's sum (the same for the whole batch), and
 // the kernel's placement exponents count one more for it.
-static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, const uint8_t h[16])
+static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
 {
     si::Sched s{};
     s.nrec = nrec;
@@ -322,14 +357,6 @@ static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad
     {
         const uint64_t pad = uint64_t(s.rows) * SI_T - m;  // blocks of row 0 before X
         s.ek_row0 = (s.a >= 1 && s.n >= 1 && pad + s.a <= SI_T - 1) ? 1u : 0u;
-    }
-    {
-        Blk len{}, hb;
-        put_be64(len.b, aad_bytes * 8u);
-        put_be64(len.b + 8, bytes * 8u);
-        memcpy(hb.b, h, 16);
-        const Blk lh = gf_mul(len, hb);
-        for (int k = 0; k < 4; ++k) s.lh[k] = le32(lh.b + 4 * k);
     }
     // W workgroups, one per CU, none with fewer than g_min_rows rows, and at
     // least nrec of them (rounded to whole rounds of one per CU) so that no
@@ -397,17 +424,17 @@ static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad
     return s;
 }
 
-// A layer's schedule depends only on its shape, H, the layout knobs and the
+// A layer's schedule depends only on its shape, the layout knobs and the
 // device's CU count; a serving loop launches the same few shapes every layer,
-// so each thread keeps its last few schedules (the layout search and the
-// software GF multiply take 2.3 us per int4 Qwen2.5-7B layer launch and
-// 3.1 us per bf16 Llama-3-8B one on an x86 host core; a cached one, 0.13 us).
-si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, const uint8_t h[16])
+// so each thread keeps its last few layouts (the layout search takes ~2 us
+// per int4 Qwen2.5-7B layer launch and ~3 us per bf16 Llama-3-8B one on an
+// x86 host core; a cached one, 0.13 us).  The cache holds no key material:
+// the length block's term L * H comes from the context (DevCtx::lh_of).
+si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, DevCtx& c)
 {
     struct Key {
         uint64_t bytes, aad_bytes;
         uint32_t nrec, cus, min_rows, straddle, fixed, pair;
-        uint8_t h[16];
     };
     struct Entry {
         Key k;
@@ -426,15 +453,21 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, const ui
     k.straddle = g_straddle_rows;
     k.fixed = g_wg_fixed_rows;
     k.pair = g_pair_records ? 1u : 0u;
-    memcpy(k.h, h, 16);
     if (!cache) cache.reset(new Entry[kEntries]);
-    for (int i = 0; i < used; ++i)
-        if (!memcmp(&cache[i].k, &k, sizeof(k))) return cache[i].s;
-    const si::Sched s = make_sched_uncached(nrec, bytes, aad_bytes, h);
-    cache[next].k = k;
-    cache[next].s = s;
-    next = (next + 1) % kEntries;
-    if (used < kEntries) ++used;
+    si::Sched s;
+    int hit = -1;
+    for (int i = 0; i < used && hit < 0; ++i)
+        if (!memcmp(&cache[i].k, &k, sizeof(k))) hit = i;
+    if (hit >= 0) {
+        s = cache[hit].s;
+    } else {
+        s = make_sched_uncached(nrec, bytes, aad_bytes);
+        cache[next].k = k;
+        cache[next].s = s;
+        next = (next + 1) % kEntries;
+        if (used < kEntries) ++used;
+    }
+    c.lh_of(bytes, aad_bytes, s.lh);
     return s;
 }
 
@@ -569,7 +602,7 @@ int run_single_ctx(int mode, hipStream_t stream, DevCtx* c, void* src, void* tag
     b.status = static_cast<uint32_t*>(status);
     b.ks = static_cast<const uint8_t*>(ks);
     for (int k = 0; k < 4; ++k) b.iv[k] = iv[k];
-    const si::Sched s = make_sched(1, bytes, aad_bytes, c->h);
+    const si::Sched s = make_sched(1, bytes, aad_bytes, *c);
     const bool al = aligned16(src) && (!dst || aligned16(dst)) && (!ks || aligned16(ks));
     return si::launch_gcm(mode, stream, c->dev, b, s, acc, al) == hipSuccess ? 0 : -1;
 }
@@ -655,6 +688,7 @@ struct si_session {
     uint32_t salt_word;
     uint64_t session_nonce;
     uint64_t max_record_bytes;
+    std::atomic<uint32_t> holds{0};  // pending launches / jobs naming it (si_host.cpp)
 };
 
 extern "C" {
@@ -925,7 +959,11 @@ int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_
 int secure_infer_gpu_session_destroy(si_session* s)
 {
     if (!s) return -1;
-    si_internal::forget_session(s);
+    if (!si_internal::forget_session(s)) {
+        fprintf(stderr, "[secure_infer] session_destroy: another thread still has swaps of this session "
+                        "that were not issued (an open layer group or D2H batch); end them first\n");
+        return -1;
+    }
     (void)hipDeviceSynchronize();
     delete s;
     return 0;
@@ -994,11 +1032,22 @@ static int reload_checks(const si_session* s, const si_reload_desc* d, const voi
     return 0;
 }
 
+// Events armed by secure_infer_gpu_time_next_layer for the calling thread's
+// next layer launch (one shot).
+thread_local si::LaunchEvents t_layer_events;
+
+static si::LaunchEvents take_layer_events()
+{
+    const si::LaunchEvents ev = t_layer_events;
+    t_layer_events = si::LaunchEvents();
+    return ev;
+}
+
 // The verify / decrypt launch and, with a codec, the dequantise-scatter
 // launch of one reload layer, given its accumulators, schedule (with its
 // parking area) and staging.
 static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc* d, si::RecAcc* acc,
-                         const si::Sched& sc, uint8_t* staging)
+                         const si::Sched& sc, uint8_t* staging, const uint32_t* gate = nullptr)
 {
     si::RecBatch b{};
     b.single = 0;
@@ -1024,7 +1073,15 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
     si::Sched sc2 = sc;
     sc2.status_out = d->status_out;
-    if (si::launch_gcm(0, stream, s->ctx->dev, b, sc2, acc, al) != hipSuccess) return -1;
+    sc2.gate = gate;
+    // A timed layer: start at the record kernel, stop at the layer's last kernel.
+    const si::LaunchEvents ev = take_layer_events();
+    si::LaunchEvents ev_rec = ev, ev_dq;
+    if (codec) {
+        ev_rec.stop = nullptr;
+        ev_dq.stop = ev.stop;
+    }
+    if (si::launch_gcm(0, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) return -1;
     if (codec) {
         si::CodecBatch cb{};
         cb.nrec = d->nrec;
@@ -1043,7 +1100,8 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
         cb.qbytes = 128ull * d->heads * d->head_dim * d->codec_bits / 8;
         cb.sbytes = 2ull * d->heads * d->head_dim * 4;
         cb.width = d->bytes;
-        if (si::launch_dequant_scatter(stream, cb) != hipSuccess) return -1;
+        cb.gate = gate;
+        if (si::launch_dequant_scatter(stream, cb, ev_dq) != hipSuccess) return -1;
     }
     return 0;
 }
@@ -1056,7 +1114,7 @@ int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* s, const si_re
     std::lock_guard<std::mutex> g(ws->m);
     si::RecAcc* acc = workspace(*ws, stream, d->nrec);
     if (!acc) return -1;
-    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, *s->ctx);
     if (sc.pairs && !(sc.park = park_area(*ws, stream, sc.nwg))) return -1;
     return reload_launch(stream, s, d, acc, sc, static_cast<uint8_t*>(d->staging));
 }
@@ -1073,25 +1131,67 @@ int secure_infer_gpu_reload_layer_noalloc(hipStream_t stream, si_session* s, con
     // layer_common wants a staging pointer for a codec; the scratch's is
     // only known once the request fits, so check with a stand-in first.
     if (reload_checks(s, d, codec ? reinterpret_cast<const void*>(uintptr_t(256)) : nullptr)) return -1;
-    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, *s->ctx);
     const uint64_t park_bytes = sc.pairs ? (uint64_t(sc.nwg) * SI_NT * sizeof(uint4) + 255) / 256 * 256 : 0;
     const uint64_t stage_bytes = codec ? uint64_t(d->nrec) * ((d->bytes + 31) & ~uint64_t(31)) : 0;
-    if (d->nrec > SI_NOALLOC_MAX_RECORDS ||
-        SI_NOALLOC_ACC_BYTES + park_bytes + stage_bytes > SI_NOALLOC_SCRATCH_BYTES) {
+    const uint64_t need = SI_NOALLOC_CTRL_BYTES + SI_NOALLOC_ACC_BYTES + park_bytes + stage_bytes;
+    if (d->nrec > SI_NOALLOC_MAX_RECORDS || need > SI_NOALLOC_SCRATCH_BYTES) {
         fprintf(stderr,
                 "[secure_infer] reload_layer_noalloc: %u records of %llu B need %llu B of scratch "
                 "(at most %u records and %llu B); use secure_infer_gpu_reload_layer\n",
-                d->nrec, static_cast<unsigned long long>(d->bytes),
-                static_cast<unsigned long long>(SI_NOALLOC_ACC_BYTES + park_bytes + stage_bytes),
+                d->nrec, static_cast<unsigned long long>(d->bytes), static_cast<unsigned long long>(need),
                 SI_NOALLOC_MAX_RECORDS, static_cast<unsigned long long>(SI_NOALLOC_SCRATCH_BYTES));
         return -1;
     }
     uint8_t* base = si::noalloc_scratch(stream);
     if (!base) return -1;
-    si::RecAcc* acc = reinterpret_cast<si::RecAcc*>(base);
-    if (sc.pairs) sc.park = reinterpret_cast<uint4*>(base + SI_NOALLOC_ACC_BYTES);
-    uint8_t* staging = codec ? base + SI_NOALLOC_ACC_BYTES + park_bytes : nullptr;
-    return reload_launch(stream, s, d, acc, sc, staging);
+    uint32_t* ctrl = reinterpret_cast<uint32_t*>(base);
+    si::RecAcc* acc = reinterpret_cast<si::RecAcc*>(base + SI_NOALLOC_CTRL_BYTES);
+    uint8_t* after_acc = base + SI_NOALLOC_CTRL_BYTES + SI_NOALLOC_ACC_BYTES;
+    if (sc.pairs) sc.park = reinterpret_cast<uint4*>(after_acc);
+    uint8_t* staging = codec ? after_acc + park_bytes : nullptr;
+    // The call's lock cell: bytes 4..7 of record 0's status slot (its own
+    // memory; the kernels write only the status word, bytes 0..3).
+    uint8_t* wire = static_cast<uint8_t*>(const_cast<void*>(d->wire));
+    const uint64_t status_off = ((d->bytes + 31) & ~uint64_t(31)) + 16;
+    uint32_t* cell = reinterpret_cast<uint32_t*>(wire + status_off + 4);
+    if (si::launch_noalloc_acquire(stream, ctrl, cell) != hipSuccess) return -1;
+    const int rc = reload_launch(stream, s, d, acc, sc, staging, cell);
+    // The finishing kernel runs even after a failed launch: it returns the
+    // owner word (or fails the records closed), so no call keeps the scratch.
+    si::NoallocFinish f{};
+    f.ctrl = ctrl;
+    f.cell = cell;
+    f.wire = wire;
+    f.wire_stride = d->wire_stride;
+    f.status_off = status_off;
+    f.cache[0] = static_cast<uint8_t*>(d->cache_k);
+    f.cache[1] = static_cast<uint8_t*>(d->cache_v);
+    f.slot_bytes = d->slot_bytes;
+    f.out_bytes = codec ? 128ull * d->heads * d->head_dim * 2 : d->bytes;
+    f.slots = d->slots;
+    f.nslots = int64_t(d->nslots);
+    f.nrec = d->nrec;
+    f.n_k = d->n_k;
+    f.status_out = d->status_out;
+    f.fail_count = d->fail_count;
+    if (si::launch_noalloc_finish(stream, f) != hipSuccess) return -1;
+    return rc;
+}
+
+int secure_infer_gpu_time_next_layer(hipEvent_t start, hipEvent_t stop)
+{
+    if (!start && !stop) return -1;
+    t_layer_events.start = start;
+    t_layer_events.stop = stop;
+    return 0;
+}
+
+int secure_infer_test_noalloc_hold(hipStream_t stream, int hold)
+{
+    uint8_t* base = si::noalloc_scratch(stream);
+    if (!base) return -1;
+    return si::launch_noalloc_test_hold(stream, reinterpret_cast<uint32_t*>(base), hold) == hipSuccess ? 0 : -1;
 }
 
 int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si_writeback_desc* d)
@@ -1125,6 +1225,13 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
     b.n_k = d->n_k;
     b.fail_count = d->fail_count;
     fill_layer_ivs(s, b, d->iv_words, d->ticket_base);
+    // A timed layer: start at the layer's first kernel, stop at the record kernel.
+    const si::LaunchEvents ev = take_layer_events();
+    si::LaunchEvents ev_q, ev_rec = ev;
+    if (codec) {
+        ev_q.start = ev.start;
+        ev_rec.start = nullptr;
+    }
     if (codec) {
         b.staging = static_cast<uint8_t*>(d->staging);
         b.staging_stride = (d->bytes + 31) & ~uint64_t(31);
@@ -1145,12 +1252,12 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
         cb.qbytes = 128ull * d->heads * d->head_dim * d->codec_bits / 8;
         cb.sbytes = 2ull * d->heads * d->head_dim * 4;
         cb.width = d->bytes;
-        if (si::launch_gather_quant(stream, cb) != hipSuccess) return -1;
+        if (si::launch_gather_quant(stream, cb, ev_q) != hipSuccess) return -1;
     }
-    si::Sched sc = make_sched(d->nrec, d->bytes, 64, s->ctx->h);
+    si::Sched sc = make_sched(d->nrec, d->bytes, 64, *s->ctx);
     if (sc.pairs && !(sc.park = park_area(*ws, stream, sc.nwg))) return -1;
     const bool al = aligned16(d->cache_k) && aligned16(d->cache_v) && (d->slot_bytes % 16 == 0);
-    return si::launch_gcm(1, stream, s->ctx->dev, b, sc, acc, al) == hipSuccess ? 0 : -1;
+    return si::launch_gcm(1, stream, s->ctx->dev, b, sc, acc, al, ev_rec) == hipSuccess ? 0 : -1;
 }
 
 // ---------------------------------------------------------------- kernel-level mirrors
@@ -1569,6 +1676,12 @@ int secure_infer_gpu_set_straddle_rows(int rows)
 }  // extern "C"
 
 namespace si_internal {
+
+void session_hold(si_session* s) { s->holds.fetch_add(1, std::memory_order_acq_rel); }
+
+void session_release(si_session* s) { s->holds.fetch_sub(1, std::memory_order_acq_rel); }
+
+uint32_t session_holds(const si_session* s) { return s->holds.load(std::memory_order_acquire); }
 
 SessionKeys session_keys(const si_session* s)
 {

@@ -13,8 +13,10 @@
 // with fl(a/scale) formed from the correctly rounded reciprocal of the
 // group's scale and one FMA correction (bit-identical to IEEE division).
 // Non-finite KV follows torch: x.amin / x.amax propagate NaN, so a group with
-// a NaN gets NaN scale and low and quantises to 0; decoding a NaN gives the
-// bf16 NaN 0x7fc0.  The bit patterns of NaN parameters are not specified.
+// a NaN gets NaN scale and low and quantises to 0; an int4 byte whose pair
+// holds a NaN quotient is 0 (packed in float, then cast); decoding a NaN
+// gives the bf16 NaN 0x7fc0.  The bit patterns of NaN parameters are not
+// specified.
 #include "si_codec_math.h"
 #include "si_kernels.h"
 
@@ -66,6 +68,10 @@ __device__ __forceinline__ float nonfinite(float x)
 // wave covers 1 KiB of consecutive packet columns.
 __global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint32_t tpt)
 {
+    // An allocation-free call that does not own the GPU's scratch (whose
+    // staging this reads) touches nothing; its records are failed closed
+    // by the call's finishing kernel.
+    if (b.gate && *b.gate == 0u) return;
     const uint32_t r = blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nc = hd / 16u;  // column chunks per token
@@ -224,6 +230,31 @@ __device__ __forceinline__ void quant8(const float x[8], const float* lo, const 
     }
 }
 
+// Byte mask (0xff per byte to keep) of 8 consecutive int4 K elements packed
+// by quant8, for a lane whose column groups are not all finite.  The
+// reference packs q[2i] + 16 q[2i+1] in float before its uint8 cast
+// (transport_codec.py:33-34), so a NaN quotient in either element zeroes the
+// whole byte.  quant8's nibbles already equal the reference's (its
+// reciprocal form may turn finite / inf into NaN where IEEE division gives
+// 0, and both cast to 0); only the whole-byte rule is added here.  The IEEE
+// quotient (x - lo) / s is NaN iff x - lo or s is NaN, or both are infinite
+// (with finite parameters it is never NaN).
+__device__ __forceinline__ uint32_t int4_nan_pairs_keep(const float x[8], const float* lo, const float* s)
+{
+    uint32_t keep = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        bool nan = false;
+#pragma unroll
+        for (int j = 2 * i; j < 2 * i + 2; ++j) {
+            const float a = __fsub_rn(x[j], lo[j]);
+            nan = nan || __builtin_isnan(a) || __builtin_isnan(s[j]) || (__builtin_isinf(a) && __builtin_isinf(s[j]));
+        }
+        keep |= (nan ? 0u : 0xffu) << (8 * i);
+    }
+    return keep;
+}
+
 template <uint32_t kBits>
 __device__ __forceinline__ void store_q8(uint8_t* pkt, uint32_t e, const uint32_t w[2])
 {
@@ -317,6 +348,31 @@ __device__ __forceinline__ void quant_k_block(const CodecBatch& b, uint32_t r, u
         quant8<1, kBits>(x, lo, sc, rc, w);
         store_q8<kBits>(pkt, (t0 + tt) * hd + col, w);
     }
+    // int4 pairs two columns of different groups in one byte: a lane with a
+    // non-finite group (the only way to a NaN quotient) stores its bytes
+    // again under the pairwise rule (a second pass, so the common path keeps
+    // its registers).
+    if (kBits == 4) {
+        bool finite = true;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) finite = finite && __builtin_isfinite(lo[k]) && __builtin_isfinite(sc[k]);
+        if (!finite) {
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                // read again (a rare path: keeping raw[] live would cost the
+                // common path a wave per SIMD)
+                uint32_t off = ((t0 + tt) * hd + col) * 2u;
+                asm volatile("" : "+v"(off));  // a fresh load, not raw[tt] kept alive
+                const uint4 rw = bad ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(slot + off);
+                float x[8];
+                unpack8(rw, x);
+                uint32_t w[2];
+                quant8<1, kBits>(x, lo, sc, rc, w);
+                w[0] &= int4_nan_pairs_keep(x, lo, sc);
+                store_q8<kBits>(pkt, (t0 + tt) * hd + col, w);
+            }
+        }
+    }
 }
 
 
@@ -392,7 +448,7 @@ __global__ __launch_bounds__(256) void quant_kernel(CodecBatch b, uint32_t kx, u
     }
 }
 
-hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b)
+hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev)
 {
     // Tokens per thread: the most that still leaves >= 1024 workgroups (four
     // per CU), so K parameters are re-read as little as the chip's width
@@ -403,19 +459,31 @@ hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b)
     uint32_t tpt = 8;
     while (tpt > 1 && wg1 / tpt < 1024u) tpt >>= 1;
     const uint32_t per_rec = (128u / tpt) * (b.heads * b.dim / 16u);
-    hipLaunchKernelGGL(dequant_scatter_kernel, dim3((per_rec + 255u) / 256u, b.nrec), dim3(256), 0, stream, b, tpt);
+    const dim3 grid((per_rec + 255u) / 256u, b.nrec);
+    if (ev.start || ev.stop)
+        hipExtLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, b, tpt);
+    else
+        hipLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, b, tpt);
     return hipGetLastError();
 }
 
-hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b)
+hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev)
 {
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nv = b.nrec - b.n_k;
     const uint32_t kx = (2u * hd + 255u) / 256u, vx = (4u * hd + 255u) / 256u;
     if (b.n_k + nv) {
         const dim3 grid(kx * b.n_k + vx * nv);
-        if (b.bits == 8) hipLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, b, kx, vx);
-        else hipLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, b, kx, vx);
+        if (ev.start || ev.stop) {
+            if (b.bits == 8)
+                hipExtLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, b, kx, vx);
+            else
+                hipExtLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, b, kx, vx);
+        } else if (b.bits == 8) {
+            hipLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, b, kx, vx);
+        } else {
+            hipLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, b, kx, vx);
+        }
     }
     return hipGetLastError();
 }

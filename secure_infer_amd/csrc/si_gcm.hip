@@ -651,6 +651,9 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     uint4* const xs0 = s_lds + 1024;     // after the rows: a pair's segment-0 products
 
     constexpr bool kNeedRelease = (kMode == MODE_DECRYPT || kMode == MODE_VERIFY_XOR) && !kWT;
+    // An allocation-free call that does not own the GPU's scratch touches
+    // nothing; its finishing kernel fails every record closed.
+    if (sch.gate && *gmem(sch.gate) == 0u) return;
     const uint32_t tid = threadIdx.x;
     // Unit index: uniform over a wave (SI_T is a multiple of 64).
     const uint32_t u = __builtin_amdgcn_readfirstlane(tid / SI_T), t = tid % SI_T;
@@ -1028,46 +1031,126 @@ uint8_t* noalloc_scratch(hipStream_t stream)
     if (it != ptrs.end()) return it->second;
     void* ptr = nullptr;
     if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-    // The record kernel's accumulators must start at zero; the workgroup
-    // that finalises a record returns its accumulator to zero, so this clear
-    // is needed once per device.  A fill kernel, not a memset node, in case
-    // the stream is being captured.
-    const uint64_t words = SI_NOALLOC_ACC_BYTES / 16u;
-    hipLaunchKernelGGL(zero_words_kernel, dim3(uint32_t((words + 255) / 256)), dim3(256), 0, stream,
-                       static_cast<uint4*>(ptr), words);
-    if (hipGetLastError() != hipSuccess) return nullptr;
+    // The owner word and the record kernel's accumulators must start at zero
+    // (the workgroup that finalises a record returns its accumulator to
+    // zero, and a finishing kernel returns the owner word to zero).  The
+    // array is zero when the code object loads; this clear runs once per
+    // device, before any call can hold the scratch (the lock is held until
+    // it completes).  Under capture it is skipped: a clear recorded into a
+    // graph would run again at every replay, under other calls' feet.
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return nullptr;
-    if (cs == hipStreamCaptureStatusNone && hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    if (cs == hipStreamCaptureStatusNone) {
+        const uint64_t words = (SI_NOALLOC_CTRL_BYTES + SI_NOALLOC_ACC_BYTES) / 16u;
+        hipLaunchKernelGGL(zero_words_kernel, dim3(uint32_t((words + 255) / 256)), dim3(256), 0, stream,
+                           static_cast<uint4*>(ptr), words);
+        if (hipGetLastError() != hipSuccess) return nullptr;
+        if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    }
     ptrs[dev] = static_cast<uint8_t*>(ptr);
     return ptrs[dev];
 }
 
+// Control word 0: the owner token; word 1: the token sequence.
+__global__ void noalloc_acquire_kernel(uint32_t* ctrl, uint32_t* cell)
+{
+    uint32_t tok;
+    do {
+        tok = __hip_atomic_fetch_add(&ctrl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    } while (tok == 0u || tok == SI_NOALLOC_TEST_TOKEN);
+    uint32_t expected = 0u;
+    const bool won = __hip_atomic_compare_exchange_strong(&ctrl[0], &expected, tok, __ATOMIC_ACQ_REL,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *gmem(cell) = won ? tok : 0u;
+}
+
+// One workgroup per record (grid nrec): release the owner word, or fail the
+// denied call's records closed.
+__global__ __launch_bounds__(256) void noalloc_finish_kernel(NoallocFinish f)
+{
+    const uint32_t tok = *gmem(f.cell);
+    const uint32_t r = blockIdx.x;
+    if (tok != 0u) {
+        if (r == 0 && threadIdx.x == 0) {
+            uint32_t expected = tok;
+            __hip_atomic_compare_exchange_strong(&f.ctrl[0], &expected, 0u, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    if (threadIdx.x == 0) {
+        *gmem(reinterpret_cast<uint32_t*>(f.wire + uint64_t(r) * f.wire_stride + f.status_off)) = 0u;
+        if (f.status_out) gmem(f.status_out)[r] = 0u;
+        if (r == 0 && f.fail_count) atomicAdd(f.fail_count, f.nrec);
+    }
+    const int64_t sid = f.slots[r];
+    if (sid < 0 || sid >= f.nslots) return;  // a bad slot id touches no cache memory
+    uint8_t* dst = f.cache[r < f.n_k ? 0 : 1] + uint64_t(sid) * f.slot_bytes;
+    zero_bytes(dst, f.out_bytes, threadIdx.x, blockDim.x);
+}
+
+__global__ void noalloc_test_hold_kernel(uint32_t* ctrl, int hold)
+{
+    uint32_t expected = hold ? 0u : SI_NOALLOC_TEST_TOKEN;
+    __hip_atomic_compare_exchange_strong(&ctrl[0], &expected, hold ? SI_NOALLOC_TEST_TOKEN : 0u, __ATOMIC_ACQ_REL,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+hipError_t launch_noalloc_acquire(hipStream_t stream, uint32_t* ctrl, uint32_t* cell)
+{
+    hipLaunchKernelGGL(noalloc_acquire_kernel, dim3(1), dim3(1), 0, stream, ctrl, cell);
+    return hipGetLastError();
+}
+
+hipError_t launch_noalloc_finish(hipStream_t stream, const NoallocFinish& f)
+{
+    if (f.nrec == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(noalloc_finish_kernel, dim3(f.nrec), dim3(256), 0, stream, f);
+    return hipGetLastError();
+}
+
+hipError_t launch_noalloc_test_hold(hipStream_t stream, uint32_t* ctrl, int hold)
+{
+    hipLaunchKernelGGL(noalloc_test_hold_kernel, dim3(1), dim3(1), 0, stream, ctrl, hold);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- launches
+
+template <int kMode, bool kAligned, bool kWT>
+static void launch_records(dim3 grid, dim3 block, hipStream_t stream, const LaunchEvents& ev, const GcmCtx* ctx,
+                           const RecBatch& b, const Sched& s, RecAcc* acc)
+{
+    if (ev.start || ev.stop)
+        hipExtLaunchKernelGGL((gcm_records_kernel<kMode, kAligned, kWT>), grid, block, 0, stream, ev.start, ev.stop,
+                              0, ctx, b, s, acc);
+    else
+        hipLaunchKernelGGL((gcm_records_kernel<kMode, kAligned, kWT>), grid, block, 0, stream, ctx, b, s, acc);
+}
 
 template <int kMode>
 static hipError_t launch_mode(hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
-                              const Sched& s, RecAcc* acc, bool aligned)
+                              const Sched& s, RecAcc* acc, bool aligned, const LaunchEvents& ev)
 {
     if (s.nwg == 0) return hipSuccess;
     const dim3 grid(s.nwg), block(SI_NT);
     if (aligned && s.bytes % 16 == 0)
-        hipLaunchKernelGGL((gcm_records_kernel<kMode, true, true>), grid, block, 0, stream, ctx, b, s, acc);
+        launch_records<kMode, true, true>(grid, block, stream, ev, ctx, b, s, acc);
     else if (aligned)
-        hipLaunchKernelGGL((gcm_records_kernel<kMode, true, false>), grid, block, 0, stream, ctx, b, s, acc);
+        launch_records<kMode, true, false>(grid, block, stream, ev, ctx, b, s, acc);
     else
-        hipLaunchKernelGGL((gcm_records_kernel<kMode, false, false>), grid, block, 0, stream, ctx, b, s, acc);
+        launch_records<kMode, false, false>(grid, block, stream, ev, ctx, b, s, acc);
     return hipGetLastError();
 }
 
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
-                      const Sched& s, RecAcc* acc, bool aligned)
+                      const Sched& s, RecAcc* acc, bool aligned, const LaunchEvents& ev)
 {
     switch (mode) {
-    case MODE_DECRYPT: return launch_mode<MODE_DECRYPT>(stream, ctx, b, s, acc, aligned);
-    case MODE_ENCRYPT: return launch_mode<MODE_ENCRYPT>(stream, ctx, b, s, acc, aligned);
-    case MODE_VERIFY: return launch_mode<MODE_VERIFY>(stream, ctx, b, s, acc, aligned);
-    case MODE_VERIFY_XOR: return launch_mode<MODE_VERIFY_XOR>(stream, ctx, b, s, acc, aligned);
+    case MODE_DECRYPT: return launch_mode<MODE_DECRYPT>(stream, ctx, b, s, acc, aligned, ev);
+    case MODE_ENCRYPT: return launch_mode<MODE_ENCRYPT>(stream, ctx, b, s, acc, aligned, ev);
+    case MODE_VERIFY: return launch_mode<MODE_VERIFY>(stream, ctx, b, s, acc, aligned, ev);
+    case MODE_VERIFY_XOR: return launch_mode<MODE_VERIFY_XOR>(stream, ctx, b, s, acc, aligned, ev);
     default: return hipErrorInvalidValue;
     }
 }

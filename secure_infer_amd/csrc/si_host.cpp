@@ -814,6 +814,24 @@ struct Observed {
 std::mutex g_obs_lock;
 std::multimap<uint32_t, std::shared_ptr<Observed>>& g_observed = *new std::multimap<uint32_t, std::shared_ptr<Observed>>();
 
+// Observed swaps that nobody waits for would hold their status buffers
+// forever: past kObservedSweep entries, swaps whose kernel has completed and
+// whose every record authenticated are dropped (a wait would find nothing to
+// report for them); failed and unfinished ones stay until waited for.
+constexpr size_t kObservedSweep = 4096;
+
+void sweep_observed_locked()
+{
+    if (g_observed.size() < kObservedSweep) return;
+    for (auto it = g_observed.begin(); it != g_observed.end();) {
+        const Observed& ob = *it->second;
+        bool drop = hipEventQuery(ob.status->ready) == hipSuccess;
+        for (uint32_t r = 0, n = uint32_t(ob.mapping.size() / 2); drop && r < n; ++r)
+            drop = ob.status_of(r) == 1u;
+        it = drop ? g_observed.erase(it) : std::next(it);
+    }
+}
+
 // ---------------------------------------------------------------- H2D
 
 void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint64_t bytes, uint64_t tag_off,
@@ -855,6 +873,7 @@ struct H2DPart {
 struct H2DLaunch {
     hipStream_t stream = nullptr;
     si_session* s = nullptr;
+    si_internal::SessionHold hold;  // until the launch is issued or dropped
     si_internal::SessionKeys keys{};
     DeviceState* ds = nullptr;
     StreamRing* ring = nullptr;
@@ -1050,6 +1069,7 @@ int flush_launch()
     release_slot(L->ring, L->slot, true);
     if (L->observe) {
         std::lock_guard<std::mutex> go(g_obs_lock);
+        sweep_observed_locked();
         for (H2DPart& p : L->parts) g_observed.emplace(L->layer, std::move(p.ob));
     }
     return 0;
@@ -1122,6 +1142,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
         }
         nl->stream = stream;
         nl->s = s;
+        nl->hold.take(s);
         nl->keys = keys;
         nl->ds = ds;
         nl->layer = layer;
@@ -1223,6 +1244,7 @@ struct D2HJob {
     std::unique_ptr<Mirror> buf;
     hipStream_t stream = nullptr;
     si_session* s = nullptr;
+    si_internal::SessionHold hold;  // until the job is issued (or dropped)
     si_internal::SessionKeys keys{};
     uint32_t layer = 0, codec = 0, heads = 0, dim = 0;
     uint64_t bytes = 0, stride = 0, tag_off = 0, slot_bytes = 0, nslots = 0;
@@ -1539,6 +1561,7 @@ int d2h_issue(D2HBatch* b)
     w.staging = job->buf->stage;
     w.fail_count = reinterpret_cast<uint32_t*>(d + job->fail_off);
     if (secure_infer_gpu_writeback_layer(job->stream, job->s, &w) != 0) return fail();
+    job->hold.reset();  // the session is not used past the launch
     if (hipEventRecord(job->buf->ev_a, job->stream) != hipSuccess ||
         hipStreamWaitEvent(ds->d2h, job->buf->ev_a, 0) != hipSuccess ||
         hipMemcpyAsync(h, d, wire, hipMemcpyDeviceToHost, ds->d2h) != hipSuccess ||
@@ -1636,12 +1659,13 @@ int wait_observed_layer(uint32_t layer, bool* found)
     }
 }
 
-void forget_session(const si_session* s)
+bool forget_session(si_session* s)
 {
     // The calling thread's pending launches may name the session: issue them.
     (void)flush_launch();
     if (D2HBatch* b = t_batch.get())
         if (b->pending && b->pending->s == s) (void)d2h_issue(b);
+    if (session_holds(s) != 0) return false;
     std::vector<std::shared_ptr<Prefetch>> drop;
     {
         std::lock_guard<std::mutex> g(g_pf_lock);
@@ -1658,6 +1682,7 @@ void forget_session(const si_session* s)
     std::lock_guard<std::mutex> g(g_obs_lock);
     for (auto& e : g_observed)
         if (e.second->session == s) e.second->session = nullptr;
+    return true;
 }
 
 int wait_observed_job(uint64_t job_id, bool* found)
@@ -1701,9 +1726,13 @@ int secure_infer_h2d_swap(hipStream_t stream, si_session* s, const void* host_ba
                           uint32_t kind, uint32_t layer, uint32_t codec_bits, uint32_t heads,
                           uint32_t head_dim, uint32_t* fail_count)
 {
+    // Every swap is observed, inside a layer group or not, as the reference
+    // observes its unbatched copies too (secure_infer.cpp:7036-7052): a
+    // failed record reaches wait_layer_authentication whether or not the
+    // caller passed a fail counter.
     return h2d_swap_impl(stream, s, host_base, host_block_bytes, host_nblocks, dev_cache, slot_bytes, nslots,
-                         mapping, n, kind, layer, codec_bits, heads, head_dim, fail_count,
-                         si_internal::group_open(), si_internal::group_open());
+                         mapping, n, kind, layer, codec_bits, heads, head_dim, fail_count, true,
+                         si_internal::group_open());
 }
 
 int secure_infer_h2d_prefetch(si_session* s, const void* host_base, uint64_t host_block_bytes, uint64_t host_nblocks,
@@ -1877,6 +1906,7 @@ int secure_infer_d2h_swap(hipStream_t stream, si_session* s, const void* dev_cac
         J->ds = b->ds;
         J->stream = stream;
         J->s = s;
+        J->hold.take(s);
         J->keys = keys;
         J->layer = layer;
         J->codec = codec_bits;

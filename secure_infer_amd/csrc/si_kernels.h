@@ -6,6 +6,8 @@
 
 #include "secure_infer_gpu.h"
 
+#include <hip/hip_ext.h>
+
 namespace si {
 
 struct GcmCtx;
@@ -66,20 +68,66 @@ struct Sched {
     uint32_t* status_out;  // layer form, optional: record r's status also at
                            // status_out[r] (one contiguous array, device or
                            // mapped pinned host memory)
+    const uint32_t* gate;  // optional: when *gate == 0 every workgroup returns
+                           // at once (an allocation-free call that does not own
+                           // the GPU's scratch; see noalloc_finish)
 };
 // Scratch of the allocation-free reload (secure_infer_gpu_reload_layer_noalloc):
-// one device array per GPU, [accumulators of up to SI_NOALLOC_MAX_RECORDS
-// records][parking area of pairs][codec staging].
+// one device array per GPU, [control words][accumulators of up to
+// SI_NOALLOC_MAX_RECORDS records][parking area of pairs][codec staging].
+// Control word 0 is the owner token (0 = free), word 1 the token sequence.
 #define SI_NOALLOC_SCRATCH_BYTES (64ull << 20)
 #define SI_NOALLOC_MAX_RECORDS 8192u
+#define SI_NOALLOC_CTRL_BYTES 256u
 #define SI_NOALLOC_ACC_BYTES (uint64_t(SI_NOALLOC_MAX_RECORDS) * 32u)
+// Token the test hook holds the scratch with (never handed to a call).
+#define SI_NOALLOC_TEST_TOKEN 0xffffffffu
 // Device address of the current GPU's scratch; on a device's first call its
-// accumulator region is zeroed on `stream` (and, unless the stream is
-// capturing, waited for).  nullptr on failure.
+// control words and accumulators are zeroed on `stream` and waited for
+// (a capturing stream skips this: the array is zero when the module loads).
+// nullptr on failure.
 uint8_t* noalloc_scratch(hipStream_t stream);
 
+// Exclusive use of the scratch by one allocation-free call, without any
+// wait on the device (a wave that spun for another stream's release could
+// hold a hardware queue the release is queued behind):
+//   acquire: one thread draws a token (never 0 or the test token) and
+//            compare-and-swaps the owner word from 0 to it; `cell` (4 bytes
+//            of the call's own memory) receives the token, or 0 when the
+//            scratch is held by another call;
+//   the call's kernels run with gate = cell and return at once on 0;
+//   finish:  owner -> 0 if the call held it; a call that did not hold it
+//            fails every record closed instead: its output extent zeroed
+//            (bf16 payload, or the whole bf16 block of a codec record),
+//            status 0 in the wire record and status_out, fail_count += nrec.
+struct NoallocFinish {
+    uint32_t* ctrl;
+    const uint32_t* cell;
+    uint8_t* wire;
+    uint64_t wire_stride, status_off;
+    uint8_t* cache[2];
+    uint64_t slot_bytes, out_bytes;
+    const int64_t* slots;
+    int64_t nslots;
+    uint32_t nrec, n_k;
+    uint32_t* status_out;
+    uint32_t* fail_count;
+};
+hipError_t launch_noalloc_acquire(hipStream_t stream, uint32_t* ctrl, uint32_t* cell);
+hipError_t launch_noalloc_finish(hipStream_t stream, const NoallocFinish& f);
+// Test hook: hold (1) or release (0) the scratch with SI_NOALLOC_TEST_TOKEN.
+hipError_t launch_noalloc_test_hold(hipStream_t stream, uint32_t* ctrl, int hold);
+
+// Events a timed launch records at its kernel's dispatch start and end
+// (hipExtLaunchKernel: the interval a kernel trace reports, without the
+// launch gaps an event recorded between kernels adds).  Null: a plain launch.
+struct LaunchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
-                      const Sched& s, RecAcc* acc, bool aligned);
+                      const Sched& s, RecAcc* acc, bool aligned, const LaunchEvents& ev = LaunchEvents());
 hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, uint8_t* out,
                       uint64_t bytes, const uint32_t iv[4]);
 hipError_t launch_auth_gate(hipStream_t stream, uint8_t* data, const uint32_t* status,
@@ -116,9 +164,10 @@ struct CodecBatch {
     uint8_t* staging;       // packets, one per record
     uint64_t staging_stride;
     uint64_t qbytes, sbytes, width;
+    const uint32_t* gate;   // as Sched::gate (dequantiser only)
 };
-hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b);
-hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b);
+hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev = LaunchEvents());
+hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev = LaunchEvents());
 
 // Session key agreement and device-side context set-up (si_agree.hip).
 struct AgreeIo {

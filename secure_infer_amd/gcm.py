@@ -342,8 +342,11 @@ class GcmSession:
         return self
 
     def close(self) -> None:
+        """Destroys the session; raises (and keeps it) while another thread
+        still has swaps of it that were not issued (an open layer group or
+        D2H batch)."""
         if self._h:
-            lib().secure_infer_gpu_session_destroy(self._h)
+            _check(lib().secure_infer_gpu_session_destroy(self._h), "session_destroy (session still in use)")
             self._h = ct.c_void_p()
 
     def __del__(self):

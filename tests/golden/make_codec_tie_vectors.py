@@ -18,7 +18,14 @@ the quantiser's hard cases occur many times:
 
 Counts of each case are stored with the vectors; tests/test_codec_ties.py
 asserts them and checks the oracle encoders (C and NumPy) and the GPU
-quantiser against the packets.  Run: python tests/golden/make_codec_tie_vectors.py
+quantiser against the packets.
+
+A second file, codec_nonfinite_vectors.npz, holds blocks whose groups carry
+NaN, +inf, -inf or a range that overflows float32 (hi - lo = inf), next to
+finite groups: for K the two nibbles of an int4 byte belong to different
+column groups, so torch's packing in float (q[0::2] + 16 q[1::2], then the
+uint8 cast) decides whether a NaN quotient zeroes its finite partner.
+Run: python tests/golden/make_codec_tie_vectors.py
 """
 from __future__ import annotations
 
@@ -28,6 +35,7 @@ import numpy as np
 import torch
 
 OUT = Path(__file__).resolve().parent / "codec_tie_vectors.npz"
+OUT_NONFINITE = Path(__file__).resolve().parent / "codec_nonfinite_vectors.npz"
 HEADS, DIM, LAYER = 2, 64, 9
 
 
@@ -161,6 +169,70 @@ def census(x: np.ndarray, bits: int, kind: int) -> tuple[int, int]:
     return ties, int((np.round(quo) != np.round(naive)).sum())
 
 
+def nonfinite_block(rng, kind: int) -> np.ndarray:
+    """[128, HEADS, DIM] float32 (bf16-exact) with non-finite groups next to
+    finite ones.  K: per (token group, column) patterns cycling over the
+    columns, so even and odd columns (the two nibbles of an int4 byte) mix a
+    NaN / +inf / -inf / overflowing group with a finite one.  V: every
+    fourth (token, head, 64-dim group) gets one such pattern."""
+    x = round_bf16(rng.standard_normal((128, HEADS, DIM)).astype(np.float32))
+    big = np.float32(3.0e38)  # bf16-exact after rounding; big - (-big) overflows
+
+    def put(g: np.ndarray, pat: int) -> None:
+        n = g.size
+        i, j = rng.integers(0, n, 2)
+        if pat == 0:
+            g[i] = np.nan
+        elif pat == 1:
+            g[i] = np.inf
+        elif pat == 2:
+            g[i] = -np.inf
+        elif pat == 3:
+            g[i], g[(i + 1) % n] = np.inf, -np.inf
+        elif pat == 4:
+            g[i], g[(i + 1) % n] = round_bf16(big), round_bf16(-big)
+        elif pat == 5:
+            g[i], g[j] = np.inf, np.nan
+
+    if kind == 0:
+        for tg in range(2):
+            for h in range(HEADS):
+                for d in range(DIM):
+                    pat = (d + 3 * tg + 5 * h) % 9  # 6..8: finite groups
+                    if pat < 6:
+                        col = x[64 * tg:64 * tg + 64, h, d].copy()
+                        put(col, pat)
+                        x[64 * tg:64 * tg + 64, h, d] = col
+    else:
+        for t in range(128):
+            for h in range(HEADS):
+                for dg in range(DIM // 64):
+                    pat = (t + h + dg) % 8
+                    if pat < 6 and t % 4 == 0:
+                        seg = x[t, h, 64 * dg:64 * dg + 64].copy()
+                        put(seg, pat)
+                        x[t, h, 64 * dg:64 * dg + 64] = seg
+    return x
+
+
+def make_nonfinite(rng) -> None:
+    blocks, bits_l, kinds, packets = [], [], [], []
+    for bits in (8, 4):
+        for kind in (0, 1):
+            x = nonfinite_block(rng, kind)
+            u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+            blk = (u >> 16).astype(np.uint16)  # NaN / inf keep their bf16 patterns
+            blocks.append(blk)
+            bits_l.append(bits)
+            kinds.append(kind)
+            packets.append(torch_encode(blk, bits, kind, LAYER))
+    np.savez_compressed(OUT_NONFINITE, blocks=np.stack(blocks), bits=np.array(bits_l, np.int32),
+                        kinds=np.array(kinds, np.int32), layer=np.int32(LAYER),
+                        torch_version=np.array(torch.__version__),
+                        **{f"packet_{i}": pk for i, pk in enumerate(packets)})
+    print(f"wrote {OUT_NONFINITE}: {len(blocks)} blocks")
+
+
 def main():
     rng = np.random.default_rng(20261202)
     blocks, bits_l, kinds, packets, ties, recips = [], [], [], [], [], []
@@ -184,6 +256,7 @@ def main():
                         ties=np.array(ties, np.int64), recip_differs=np.array(recips, np.int64),
                         torch_version=np.array(torch.__version__), **packed)
     print(f"wrote {OUT}: {len(blocks)} blocks, ties {ties}, reciprocal-form differs {recips}")
+    make_nonfinite(np.random.default_rng(20261203))
 
 
 if __name__ == "__main__":

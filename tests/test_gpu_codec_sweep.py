@@ -7,8 +7,12 @@ transport_codec.py:22-42), sealed by OpenSSL, verified / decrypted /
 dequantised on the device and compared with the oracle's decode
 (optimized_decode.py:5-26), one tampered V record zeroed.  Writeback: KV
 blocks quantised and sealed on the device, compared with OpenSSL over the
-oracle's packets of the same blocks.  Bit-exact throughout.
+oracle's packets of the same blocks.  Bit-exact throughout.  The reference's
+own decode_into output at 1, 4 and 8 heads (tests/golden/codec_decode_vectors.npz)
+is reloaded through the device as well.
 """
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -109,3 +113,30 @@ def test_codec_writeback_shapes(bits):
             o = r * st
             assert np.array_equal(ww[o:o + n], expect[o:o + n]), (heads, dim, r, "ciphertext")
             assert np.array_equal(ww[o + toff:o + toff + 16], expect[o + toff:o + toff + 16]), (heads, dim, r, "tag")
+
+
+@pytest.mark.parametrize("heads", [1, 4, 8])
+def test_reload_matches_reference_decode_fixture(heads):
+    """The fixture's packets (int8 / int4, K and V) sealed with OpenSSL and
+    reloaded into a paged cache: every slot equals decode_into's output."""
+    z = np.load(Path(__file__).resolve().parent / "golden" / "codec_decode_vectors.npz", allow_pickle=False)
+    pre = "" if heads == 1 else f"h{heads}_"
+    dim, layer, nslots = 128, 3, 6
+    for bits in (8, 4):
+        print(f"int{bits} decode fixture {heads} heads", flush=True)
+        packets = [z[f"{pre}packet_b{bits}_k0"], z[f"{pre}packet_b{bits}_k1"]]
+        want = [z[f"{pre}decoded_b{bits}_k0"], z[f"{pre}decoded_b{bits}_k1"]]
+        n = packets[0].size
+        ticket = 500 + 10 * heads + bits
+        wire = W.build_wire(KEY, SALT, packets, [0, 1], layer, [0, 0], ticket)
+        ck, cv = _caches(nslots, heads, dim)
+        sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+        staging = torch.zeros(2 * W.align32(n), dtype=torch.uint8, device=DEV)
+        fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+        sess.reload_layer(_dev(wire), n, 2, 1, ck, cv, _dev(np.array([4, 4], np.int64)), ticket_base=ticket,
+                          codec_bits=bits, heads=heads, head_dim=dim, layer=layer, staging=staging,
+                          fail_count=fail)
+        kk, vv = _host(ck), _host(cv)
+        assert int(_host(fail)[0]) == 0
+        assert np.array_equal(kk[4].view(np.uint16), want[0]), (heads, bits, "K")
+        assert np.array_equal(vv[4].view(np.uint16), want[1]), (heads, bits, "V")

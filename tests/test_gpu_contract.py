@@ -396,3 +396,106 @@ def test_causal_groups_through_the_host_pipeline(ranges, slices, stripe):
     assert si.new_transfer_ticket() - t_before == 2 * ncpu + 1 + 1
     idx = dev(slot_ids.astype(np.int64))
     assert torch.equal(ck.index_select(0, idx).cpu(), hk) and torch.equal(cv.index_select(0, idx).cpu(), hv)
+
+
+@pytest.mark.parametrize("shots,rc_want", [(1, 0), (2, -1)], ids=["one_shot", "persistent"])
+def test_ungrouped_swaps_are_observed(ranges, shots, rc_want):
+    """Swaps issued outside a layer group, with no fail counter, are observed
+    like grouped ones (the reference observes its unbatched copies too,
+    secure_infer.cpp:7036-7052): a record corrupted once is re-sealed and the
+    layer authenticates; corrupted on the retry too, the layer's wait returns
+    -1 and the slot reads as zeros."""
+    import ctypes as ct
+
+    from secure_infer_amd import _lib
+    rng = np.random.default_rng(331 + shots)
+    heads, dim, ncpu, nslots, layer = 2, 128, 8, 16, 7
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 21, max_record_bytes=shape.record_bytes)
+    hk, hv = pools(rng, ncpu, heads, dim)
+    si.register_host_range(hk, layer, 0)
+    si.register_host_range(hv, layer, 1)
+    ck, cv = caches(nslots, heads, dim)
+    cpu_ids = rng.permutation(ncpu)[:5]
+    slot_ids = rng.permutation(nslots)[:5]
+    mapping = torch.from_numpy(np.stack([cpu_ids, slot_ids], 1).astype(np.int64))
+    target = int(cpu_ids[3])
+    si.inject_h2d_tamper(layer=layer, kind=0, host_block=target, shots=shots)
+    L = _lib.load()
+    stream = ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+    bb = hk[0].numel() * 2
+    for pool, cache, kind in ((hk, ck, 0), (hv, cv, 1)):
+        assert L.secure_infer_h2d_swap(stream, sess._h, ct.c_void_p(pool.data_ptr()), bb, ncpu,
+                                       ct.c_void_p(cache.data_ptr()), bb, nslots,
+                                       ct.c_void_p(mapping.data_ptr()), 5, kind, layer, 0, heads, dim, None) == 0
+    assert si.NativeTransfer(sess, shape).wait_layer(layer) == rc_want
+    torch.cuda.synchronize()
+    for c, s in zip(cpu_ids, slot_ids):
+        assert torch.equal(cv[s].cpu(), hv[c])
+        if c == target and rc_want == -1:
+            assert zero_on_device(ck[s])
+        else:
+            assert torch.equal(ck[s].cpu(), hk[c])
+
+
+def test_session_destroy_refuses_while_another_thread_holds_it(ranges):
+    """A thread's layer group (an H2D launch not yet issued) or D2H batch (a
+    job not yet issued) names its session: destroying the session from
+    another thread returns -1 and leaves it usable; once the work is issued,
+    destroy succeeds."""
+    import ctypes as ct
+    import threading
+
+    from secure_infer_amd import _lib
+    rng = np.random.default_rng(341)
+    heads, dim, ncpu, nslots, layer = 2, 128, 6, 12, 3
+    shape = si.LayerShape(heads, dim)
+    L = _lib.load()
+    bb = 128 * heads * dim * 2
+    hk, hv = pools(rng, ncpu, heads, dim)
+    si.register_host_range(hk, layer, 0)
+    si.register_host_range(hv, layer, 1)
+    ck, cv = caches(nslots, heads, dim)
+    mapping = torch.from_numpy(np.stack([np.arange(4), rng.permutation(nslots)[:4]], 1).astype(np.int64))
+    back = torch.stack([mapping[:, 1], mapping[:, 0]], 1).contiguous()
+    for direction in ("h2d", "d2h"):
+        sess = si.GcmSession(KEY, SALT, 40, max_record_bytes=shape.record_bytes)
+        opened, release, closed = threading.Event(), threading.Event(), threading.Event()
+        rcs = []
+
+        def holder():
+            stream = ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+            if direction == "h2d":
+                rcs.append(L.secure_infer_h2d_layer_group_begin(8))
+                rcs.append(L.secure_infer_h2d_swap(stream, sess._h, ct.c_void_p(hk.data_ptr()), bb, ncpu,
+                                                   ct.c_void_p(ck.data_ptr()), bb, nslots,
+                                                   ct.c_void_p(mapping.data_ptr()), 4, 0, layer, 0, heads, dim,
+                                                   None))
+                opened.set()
+                release.wait(60)
+                rcs.append(L.secure_infer_h2d_layer_group_end())
+                rcs.append(L.secure_infer_recovery_wait_layer_authentication(layer))
+            else:
+                rcs.append(L.secure_infer_d2h_batch_begin(4) - 1)
+                rcs.append(L.secure_infer_d2h_group_begin(4) - 1)
+                rcs.append(L.secure_infer_d2h_swap(stream, sess._h, ct.c_void_p(ck.data_ptr()), bb, nslots,
+                                                   ct.c_void_p(hv.data_ptr()), bb, ncpu,
+                                                   ct.c_void_p(back.data_ptr()), 4, 0, layer, 0, heads, dim))
+                rcs.append(L.secure_infer_d2h_group_end())
+                opened.set()
+                release.wait(60)
+                rcs.append(L.secure_infer_d2h_batch_device_barrier())
+                rcs.append(L.secure_infer_d2h_batch_end())
+            torch.cuda.synchronize()
+            closed.set()
+
+        t = threading.Thread(target=holder)
+        t.start()
+        assert opened.wait(60)
+        assert L.secure_infer_gpu_session_destroy(sess._h) == -1, direction  # still held
+        release.set()
+        assert closed.wait(60)
+        t.join(60)
+        assert rcs == [0] * len(rcs), (direction, rcs)
+        assert L.secure_infer_gpu_session_destroy(sess._h) == 0, direction
+        sess._h = ct.c_void_p()  # destroyed here, not by the wrapper

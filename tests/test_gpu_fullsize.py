@@ -8,7 +8,10 @@ launch takes only appear at these sizes), checked record by record:
 * int4 Qwen2.5-7B reload: 64 blocks -> 128 packets of 40,976 B (4 kv heads),
   two seeded records with one seeded ciphertext byte flipped;
 * int4 Llama-3-70B writeback: 256 blocks -> 512 packets of 81,936 B (pairs of
-  whole records per workgroup).
+  whole records per workgroup);
+* one tensor-parallel rank of Llama-3-70B at TP = 8 (1 kv head x 128 per
+  rank): 256 blocks -> 512 bf16 records of 32,768 B reloaded, and 512 int4
+  packets of 10,256 B written back (small records: several rounds of pairs).
 
 The bf16 and int4 reload layers also run end to end through the host
 pipeline (host pools, NativeTransfer with 16-block causal groups, group
@@ -42,8 +45,8 @@ def statuses(ww: np.ndarray, n: int, nrec: int) -> np.ndarray:
     return ww.reshape(nrec, st)[:, toff + 16:toff + 20].copy().view(np.uint32).ravel()
 
 
-@pytest.mark.parametrize("bits,heads,nb", [(0, 8, 48), (8, 8, 64), (4, 4, 64)],
-                         ids=["bf16_llama3_8b", "int8_llama3_8b", "int4_qwen2_5_7b"])
+@pytest.mark.parametrize("bits,heads,nb", [(0, 8, 48), (8, 8, 64), (4, 4, 64), (0, 1, 256)],
+                         ids=["bf16_llama3_8b", "int8_llama3_8b", "int4_qwen2_5_7b", "bf16_llama3_70b_tp8_rank"])
 def test_full_size_reload_layer(bits, heads, nb):
     rng = np.random.default_rng(1000 + bits)
     dim, nslots, layer, t0 = 128, 512, 17, 123456
@@ -99,9 +102,10 @@ def test_full_size_reload_layer(bits, heads, nb):
         assert bool((c[untouched].view(torch.uint8) == 0x3C).all())
 
 
-def test_full_size_writeback_layer_int4_llama3_70b():
-    rng = np.random.default_rng(1070)
-    heads, dim, nb, nslots, layer, bits, t0 = 8, 128, 256, 512, 61, 4, 777000
+@pytest.mark.parametrize("heads", [8, 1], ids=["llama3_70b", "llama3_70b_tp8_rank"])
+def test_full_size_writeback_layer_int4_llama3_70b(heads):
+    rng = np.random.default_rng(1070 + heads)
+    dim, nb, nslots, layer, bits, t0 = 128, 256, 512, 61, 4, 777000
     nrec = 2 * nb
     kinds = [0] * nb + [1] * nb
     slot_ids = rng.permutation(nslots)[:nb].astype(np.int64)

@@ -415,3 +415,66 @@ def test_native_transfer_wait_layer():
     kk = host(ck)
     assert not kk[5].any()  # layer 1 record 0 (K block -> slot 5) withheld
     assert np.array_equal(kk[2].view(np.uint16), tickets[1][1])
+
+
+@pytest.mark.parametrize("bits", [0, 4])
+def test_timed_layer_launch(bits):
+    """secure_infer_gpu_time_next_layer: the next layer call (reload, then
+    writeback) launches its first and last kernels with the caller's events;
+    the interval is positive and within the host's wall time around the call,
+    the results are unchanged (bit-exact, statuses 1), and the arming is one
+    shot (the following call leaves the events alone)."""
+    import time
+    rng = np.random.default_rng(61 + bits)
+    heads, dim, nb, nslots, layer, t0 = 4, 128, 6, 16, 2, 30000 + bits
+    blocks = W.bf16_blocks(rng, 2 * nb, heads, dim)
+    kinds = [0] * nb + [1] * nb
+    if bits:
+        payloads = [O.codec_encode(blocks[r], bits, kinds[r], layer) for r in range(2 * nb)]
+        want = np.stack([O.codec_decode(payloads[r], heads, dim, bits, kinds[r]) for r in range(2 * nb)])
+    else:
+        payloads = [blocks[r].view(np.uint8).reshape(-1) for r in range(2 * nb)]
+        want = blocks
+    n = payloads[0].size
+    wire = dev(W.build_wire(KEY, SALT, payloads, kinds, layer, list(range(nb)) * 2, t0))
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    ck, cv = make_caches(nslots, heads, dim)
+    slot_ids = rng.permutation(nslots)[:nb].astype(np.int64)
+    slots = dev(np.concatenate([slot_ids, slot_ids]))
+    staging = torch.zeros(2 * nb * W.align32(n), dtype=torch.uint8, device=DEV) if bits else None
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    L = si._lib.load()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    b.record()
+    torch.cuda.synchronize()
+    assert L.secure_infer_gpu_time_next_layer(None, None) == -1
+    assert L.secure_infer_gpu_time_next_layer(a.cuda_event, b.cuda_event) == 0
+    w0 = time.perf_counter()
+    sess.reload_layer(wire, n, 2 * nb, nb, ck, cv, slots, ticket_base=t0, codec_bits=bits, heads=heads,
+                      head_dim=dim, layer=layer, staging=staging, fail_count=fail)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - w0) * 1e3
+    ms = a.elapsed_time(b)
+    assert 0 < ms <= wall_ms
+    assert int(fail.item()) == 0
+    idx = dev(slot_ids)
+    assert torch.equal(ck.index_select(0, idx), dev(want[:nb].view(np.int16)))
+    assert torch.equal(cv.index_select(0, idx), dev(want[nb:].view(np.int16)))
+    # one shot: the next (unarmed) call does not move the events
+    sess.reload_layer(wire, n, 2 * nb, nb, ck, cv, slots, ticket_base=t0, codec_bits=bits, heads=heads,
+                      head_dim=dim, layer=layer, staging=staging, fail_count=fail)
+    torch.cuda.synchronize()
+    assert a.elapsed_time(b) == ms
+    # writeback, timed the same way, seals what OpenSSL seals
+    wb = dev(W.wire_aads(KEY, SALT, n, kinds, layer, list(range(nb)) * 2, t0 + 100))
+    assert L.secure_infer_gpu_time_next_layer(a.cuda_event, b.cuda_event) == 0
+    sess.writeback_layer(wb, n, 2 * nb, nb, ck, cv, slots, ticket_base=t0 + 100, codec_bits=bits, heads=heads,
+                         head_dim=dim, layer=layer, staging=staging)
+    torch.cuda.synchronize()
+    assert a.elapsed_time(b) > 0
+    expect = W.build_wire(KEY, SALT, payloads, kinds, layer, list(range(nb)) * 2, t0 + 100, direction=2)
+    got = host(wb).reshape(2 * nb, W.stride(n))
+    ex = expect.reshape(2 * nb, W.stride(n))
+    toff = W.align32(n)
+    assert np.array_equal(got[:, :n], ex[:, :n]) and np.array_equal(got[:, toff:toff + 16], ex[:, toff:toff + 16])

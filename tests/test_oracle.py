@@ -189,12 +189,18 @@ def test_aad_layout():
 CODEC = np.load(GOLD / "codec_decode_vectors.npz")
 
 
+@pytest.mark.parametrize("heads", [1, 4, 8])
 @pytest.mark.parametrize("bits,kind", [(8, 0), (8, 1), (4, 0), (4, 1)])
-def test_codec_decode_matches_reference_fixture(bits, kind):
-    pkt = CODEC[f"packet_b{bits}_k{kind}"]
-    expect = CODEC[f"decoded_b{bits}_k{kind}"]
-    assert np.array_equal(O.codec_decode(pkt, 1, 128, bits, kind), expect)
-    assert np.array_equal(O.np_codec_decode(pkt, 1, 128, bits, kind), expect)
+def test_codec_decode_matches_reference_fixture(heads, bits, kind):
+    """decode_into's own output (optimized_decode.py:5-26) at 1, 4 and 8 kv
+    heads x 128: the K (2, h, d) and V (128, h, d/64) parameter layouts are
+    pinned where the head axis is not trivial."""
+    pre = "" if heads == 1 else f"h{heads}_"
+    pkt = CODEC[f"{pre}packet_b{bits}_k{kind}"]
+    expect = CODEC[f"{pre}decoded_b{bits}_k{kind}"]
+    assert expect.shape == (128, heads, 128)
+    assert np.array_equal(O.codec_decode(pkt, heads, 128, bits, kind), expect)
+    assert np.array_equal(O.np_codec_decode(pkt, heads, 128, bits, kind), expect)
 
 
 @pytest.mark.parametrize("bits,kind", [(8, 0), (8, 1), (4, 0), (4, 1)])
