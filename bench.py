@@ -376,6 +376,8 @@ def main():
                     help="slice streams of the end-to-end reload (the reference's PIPE_GCM_H2D_SLICE_STREAMS, default 1)")
     ap.add_argument("--stripe", action="store_true",
                     help="stripe each causal group over the slice streams as the reference does")
+    ap.add_argument("--verify-before-release", action="store_true",
+                    help="reload with SI_RELOAD_VERIFY_BEFORE_RELEASE (tags checked before any plaintext is written)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC byte calibration)")
     args = ap.parse_args()
@@ -461,7 +463,8 @@ def main():
     rl_prep = [sess.prepare_reload_layer(wire[layer], nbytes, nrec, n_k, cache[layer, 0], cache[layer, 1],
                                          slots2[layer], iv_words_dev=ivw[layer], codec_bits=bits, heads=H,
                                          head_dim=D, layer=layer, staging=staging,
-                                         fail_count=fails[layer:layer + 1]) for layer in range(L)]
+                                         fail_count=fails[layer:layer + 1],
+                                         verify_before_release=args.verify_before_release) for layer in range(L)]
 
     def writeback_layer(layer):
         wb_prep[layer].launch(launch_stream)
@@ -575,7 +578,8 @@ def main():
         "config": {"workload": args.config, "direction": op, "layers": L, "kv_heads": H, "head_dim": D,
                    "tokens": NB * 128, "blocks": NB, "records_per_layer": nrec,
                    "record_bytes": nbytes, "cache_slots": NS, "codec_bits": bits,
-                   "tampered_records": len(tampered), "algorithmic_bytes_per_layer": algo_layer},
+                   "tampered_records": len(tampered), "algorithmic_bytes_per_layer": algo_layer,
+                   **({"verify_before_release": True} if args.verify_before_release else {})},
         "us_per_layer": round(us_launch, 3),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "failed_records_per_step": nfail // max(args.steps, 1),

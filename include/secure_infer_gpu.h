@@ -221,7 +221,18 @@ typedef struct si_reload_desc {
     uint32_t* status_out;     /* optional: nrec u32, record r's status (1 / 0)
                                  also at status_out[r]; device memory or
                                  mapped pinned host memory; NULL ok          */
+    uint32_t flags;           /* SI_RELOAD_* below; 0 = the fused default       */
 } si_reload_desc;
+
+/* si_reload_desc.flags.  SI_RELOAD_VERIFY_BEFORE_RELEASE: the reference's
+ * order (ghash.aicpu:623-648, direct verified release secure_infer.cpp:
+ * 5522-5538) -- a first launch computes every record's tag and status and
+ * writes nothing else; a second decrypts each record into its slot (or the
+ * codec staging) only if its status is 1 and writes zeros otherwise.  No
+ * unverified byte ever reaches the cache, at the price of reading the
+ * ciphertext twice.  The default (0) decrypts and hashes in one pass and
+ * zeroes a failed record's slot before the launch sequence ends. */
+enum { SI_RELOAD_VERIFY_BEFORE_RELEASE = 1u };
 
 int secure_infer_gpu_reload_layer(hipStream_t stream, si_session* session,
                                   const si_reload_desc* desc);
@@ -434,6 +445,11 @@ int secure_infer_test_tamper_agree(uint32_t mode);
  * `stream`, so a test can make secure_infer_gpu_reload_layer_noalloc find it
  * taken.  0 or -1.  Production code never calls it. */
 int secure_infer_test_noalloc_hold(hipStream_t stream, int hold);
+/* Test-only (no reference counterpart): the calling thread's next
+ * verify-before-release reload stops after its first n launches (1: the
+ * verification alone, so a test can see that it writes nothing but
+ * statuses); 0 disarms.  0 or -1.  Production code never calls it. */
+int secure_infer_test_strict_phases(int n);
 int secure_infer_test_x25519(const uint8_t scalar[32], const uint8_t u[32], uint8_t out[32]);
 int secure_infer_test_blake2b(const uint8_t* key, uint32_t key_len, const uint8_t* msg, uint64_t msg_len,
                               uint8_t* out, uint32_t out_len);

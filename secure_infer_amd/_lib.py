@@ -21,7 +21,7 @@ class SiReloadDesc(ct.Structure):
         ("iv_words", _v), ("ticket_base", _u64), ("cache_k", _v), ("cache_v", _v),
         ("slot_bytes", _u64), ("nslots", _u64), ("slots", _v), ("codec_bits", _u32),
         ("heads", _u32), ("head_dim", _u32), ("layer", _u32), ("staging", _v),
-        ("fail_count", _v), ("status_out", _v),
+        ("fail_count", _v), ("status_out", _v), ("flags", _u32),
     ]
 
 
@@ -83,6 +83,7 @@ SIGNATURES = {
     "secure_infer_test_tamper_d2h": ([_u32], _i),
     "secure_infer_test_tamper_agree": ([_u32], _i),
     "secure_infer_test_noalloc_hold": ([_v, _i], _i),
+    "secure_infer_test_strict_phases": ([_i], _i),
     "secure_infer_retire_transfer_prefetches": ([], None),
     "secure_infer_invalidate_transfer_prefetches": ([], None),
     "secure_infer_get_transfer_prefetch_stats": ([ct.POINTER(_u64)] * 3, None),

@@ -1029,6 +1029,7 @@ static int reload_checks(const si_session* s, const si_reload_desc* d, const voi
     if (!d->cache_k && d->n_k) return -1;
     if (!d->cache_v && d->n_k < d->nrec) return -1;
     if (!d->iv_words && d->ticket_base == 0) return -1;
+    if (d->flags & ~uint32_t(SI_RELOAD_VERIFY_BEFORE_RELEASE)) return -1;
     return 0;
 }
 
@@ -1041,6 +1042,17 @@ static si::LaunchEvents take_layer_events()
     const si::LaunchEvents ev = t_layer_events;
     t_layer_events = si::LaunchEvents();
     return ev;
+}
+
+// Test hook (secure_infer_test_strict_phases): the calling thread's next
+// verify-before-release reload stops after its first `n` launches (0: all).
+thread_local int t_strict_phases = 0;
+
+static int take_strict_phases()
+{
+    const int n = t_strict_phases;
+    t_strict_phases = 0;
+    return n;
 }
 
 // The verify / decrypt launch and, with a codec, the dequantise-scatter
@@ -1074,14 +1086,27 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
     si::Sched sc2 = sc;
     sc2.status_out = d->status_out;
     sc2.gate = gate;
-    // A timed layer: start at the record kernel, stop at the layer's last kernel.
+    const bool strict = (d->flags & SI_RELOAD_VERIFY_BEFORE_RELEASE) != 0;
+    const int phases = take_strict_phases();
+    // A timed layer: start at the first kernel, stop at the layer's last kernel.
     const si::LaunchEvents ev = take_layer_events();
-    si::LaunchEvents ev_rec = ev, ev_dq;
-    if (codec) {
+    si::LaunchEvents ev_rec = ev, ev_rel, ev_dq;
+    if (strict) {
         ev_rec.stop = nullptr;
-        ev_dq.stop = ev.stop;
+        ev_rel.stop = codec ? nullptr : ev.stop;
+    } else if (codec) {
+        ev_rec.stop = nullptr;
     }
-    if (si::launch_gcm(0, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) return -1;
+    if (codec) ev_dq.stop = ev.stop;
+    if (strict) {
+        // Tags and statuses first (nothing else written), then the release.
+        if (si::launch_gcm(2, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) return -1;
+        if (phases == 1) return 0;
+        if (si::launch_release(stream, s->ctx->dev, b, d->nrec, d->bytes, al || codec, gate, ev_rel) != hipSuccess)
+            return -1;
+    } else if (si::launch_gcm(0, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) {
+        return -1;
+    }
     if (codec) {
         si::CodecBatch cb{};
         cb.nrec = d->nrec;
@@ -1184,6 +1209,13 @@ int secure_infer_gpu_time_next_layer(hipEvent_t start, hipEvent_t stop)
     if (!start && !stop) return -1;
     t_layer_events.start = start;
     t_layer_events.stop = stop;
+    return 0;
+}
+
+int secure_infer_test_strict_phases(int n)
+{
+    if (n < 0) return -1;
+    t_strict_phases = n;
     return 0;
 }
 

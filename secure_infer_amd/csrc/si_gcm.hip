@@ -898,6 +898,65 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     }
 }
 
+// Verify-before-release, second launch: record r (grid y) was verified by a
+// MODE_VERIFY launch that wrote its status word; workgroup x decrypts blocks
+// [x*chunk, (x+1)*chunk) of it into its destination (slot, or the codec
+// staging row) only if that status is 1, and writes zeros there otherwise:
+// the reference's order, tag first, then masked output
+// (ghash.aicpu:623-648), so no unverified byte reaches the destination.
+// A slot id out of range with no staging touches nothing.  Threads take
+// blocks 256 apart, so the counter-mode cache of rounds 1-2 applies while
+// counter bytes 12..13 stay fixed over the workgroup's range.
+__global__ __launch_bounds__(SI_RELEASE_THREADS) void release_kernel(const GcmCtx* __restrict__ ctx, RecBatch b,
+                                                                     uint64_t bytes, uint32_t chunk, int aligned,
+                                                                     const uint32_t* gate)
+{
+    __shared__ uint32_t s_aes[256 * 64];
+    if (gate && *gmem(gate) == 0u) return;
+    const uint32_t tid = threadIdx.x, r = blockIdx.y;
+    const RecView v = view_of(b, r);
+    if (v.skip) return;
+    const uint64_t nb = (bytes + 15) / 16;
+    const uint64_t k0 = uint64_t(blockIdx.x) * chunk;
+    if (k0 >= nb) return;
+    const uint64_t k1 = k0 + chunk < nb ? k0 + chunk : nb;
+    const uint32_t ok = (*gmem(v.status) == 1u && !v.bad) ? 1u : 0u;
+    if (!ok) {
+        const uint64_t e = 16 * k1 < bytes ? 16 * k1 : bytes;
+        zero_bytes(v.dst + 16 * k0, e - 16 * k0, tid, SI_RELEASE_THREADS);
+        return;
+    }
+    if (tid < 256) aes_fill_lds(s_aes, ctx->te0, tid);
+    AesKeys keys;
+    load_keys(ctx, keys);
+    __syncthreads();
+    const AesLane lane = aes_lane(tid & 63u);
+    const uint32_t n0 = bswap32(v.iv[0]) ^ ctx->rk[0];
+    const uint32_t n1 = bswap32(v.iv[1]) ^ ctx->rk[1];
+    const uint32_t n2 = bswap32(v.iv[2]) ^ ctx->rk[2];
+    const uint32_t clo = v.iv[3] + uint32_t(k0), chi = v.iv[3] + uint32_t(k1 - 1);
+    const bool cached = chi >= clo && (clo >> 16) == (chi >> 16);  // uniform over the workgroup
+    const bool fast = aligned && (bytes & 15) == 0;
+    CtrCache cc{};
+    if (cached) cc = ctr_cache(s_aes, lane, ctx, n0, n1, n2, bswap32(v.iv[3] + uint32_t(k0 + tid)) ^ keys.rk3);
+    for (uint64_t k = k0 + tid; k < k1; k += SI_RELEASE_THREADS) {
+        uint32_t ks[4];
+        if (cached) aes_ctr_block_cached(s_aes, lane, keys, cc, v.iv[3] + uint32_t(k), ks);
+        else aes_ctr_block(s_aes, lane, keys, n0, n1, n2, v.iv[3] + uint32_t(k), ks);
+        if (fast) {
+            const uint4 c = gload4(v.src + 16 * k);
+            gstore4(v.dst + 16 * k, make_uint4(c.x ^ ks[0], c.y ^ ks[1], c.z ^ ks[2], c.w ^ ks[3]));
+        } else {
+            const uint32_t valid = k == nb - 1 ? uint32_t(bytes - 16 * k) : 16u;
+            uint32_t c[4];
+            load_block<true>(v.src + 16 * k, valid, c);  // wire records are 16-byte aligned
+            const uint32_t o[4] = {c[0] ^ ks[0], c[1] ^ ks[1], c[2] ^ ks[2], c[3] ^ ks[3]};
+            if (aligned) store_block<true>(v.dst + 16 * k, valid, o);
+            else store_block<false>(v.dst + 16 * k, valid, o);
+        }
+    }
+}
+
 __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ctx,
                                                    const uint8_t* __restrict__ in,
                                                    uint8_t* __restrict__ out, uint64_t bytes,
@@ -1153,6 +1212,23 @@ hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const Rec
     case MODE_VERIFY_XOR: return launch_mode<MODE_VERIFY_XOR>(stream, ctx, b, s, acc, aligned, ev);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_release(hipStream_t stream, const GcmCtx* ctx, const RecBatch& b, uint32_t nrec, uint64_t bytes,
+                          bool aligned, const uint32_t* gate, const LaunchEvents& ev)
+{
+    if (nrec == 0) return hipSuccess;
+    // Blocks per workgroup: a multiple of the block stride (the counter-mode
+    // cache needs each thread's blocks 256 apart), at least 8 per thread.
+    const uint64_t nb = (bytes + 15) / 16;
+    const uint32_t chunk = 8u * SI_RELEASE_THREADS;
+    const dim3 grid(uint32_t((nb + chunk - 1) / chunk), nrec), block(SI_RELEASE_THREADS);
+    if (ev.start || ev.stop)
+        hipExtLaunchKernelGGL(release_kernel, grid, block, 0, stream, ev.start, ev.stop, 0, ctx, b, bytes, chunk,
+                              aligned ? 1 : 0, gate);
+    else
+        hipLaunchKernelGGL(release_kernel, grid, block, 0, stream, ctx, b, bytes, chunk, aligned ? 1 : 0, gate);
+    return hipGetLastError();
 }
 
 hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, uint8_t* out,

@@ -25,6 +25,7 @@ from . import _lib
 
 AAD_BYTES = 64
 SI_CODEC_NONE, SI_CODEC_INT8, SI_CODEC_INT4 = 0, 8, 4
+SI_RELOAD_VERIFY_BEFORE_RELEASE = 1  # si_reload_desc.flags (include/secure_infer_gpu.h)
 
 
 def lib():
@@ -366,10 +367,13 @@ class GcmSession:
                              ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
                              codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
                              layer: int = 0, staging: torch.Tensor | None = None,
-                             fail_count: torch.Tensor | None = None) -> "PreparedLayer":
+                             fail_count: torch.Tensor | None = None,
+                             verify_before_release: bool = False) -> "PreparedLayer":
         """The checked descriptor of one reload layer, launched by
         ``.launch(stream)`` as often as needed (buffers with fixed addresses, as
-        a serving loop keeps them); the tensors are kept alive with it."""
+        a serving loop keeps them); the tensors are kept alive with it.
+        ``verify_before_release`` selects SI_RELOAD_VERIFY_BEFORE_RELEASE: every
+        tag is checked before any plaintext reaches the cache (two launches)."""
         for t, name in ((wire, "wire"), (cache_k, "cache_k"), (cache_v, "cache_v"),
                         (slots, "slots")):
             _dev(t, name)
@@ -389,7 +393,8 @@ class GcmSession:
             nslots=min(cache_k.shape[0], cache_v.shape[0]), slots=slots.data_ptr(),
             codec_bits=codec_bits, heads=heads, head_dim=head_dim, layer=layer,
             staging=None if staging is None else staging.data_ptr(),
-            fail_count=None if fail_count is None else fail_count.data_ptr())
+            fail_count=None if fail_count is None else fail_count.data_ptr(),
+            flags=SI_RELOAD_VERIFY_BEFORE_RELEASE if verify_before_release else 0)
         return PreparedLayer(lib().secure_infer_gpu_reload_layer, self, d,
                              (wire, cache_k, cache_v, slots, iv_words_dev, staging, fail_count), "reload_layer")
 
@@ -398,11 +403,13 @@ class GcmSession:
                      ticket_base: int = 0, iv_words_dev: torch.Tensor | None = None,
                      codec_bits: int = SI_CODEC_NONE, heads: int = 0, head_dim: int = 0,
                      layer: int = 0, staging: torch.Tensor | None = None,
-                     fail_count: torch.Tensor | None = None, stream=None) -> None:
+                     fail_count: torch.Tensor | None = None, stream=None,
+                     verify_before_release: bool = False) -> None:
         """One layer of authenticated reload of device-resident wire records
         (secure_infer_gpu_reload_layer); arguments as prepare_reload_layer."""
         self.prepare_reload_layer(wire, nbytes, nrec, n_k, cache_k, cache_v, slots, ticket_base, iv_words_dev,
-                                  codec_bits, heads, head_dim, layer, staging, fail_count).launch(stream)
+                                  codec_bits, heads, head_dim, layer, staging, fail_count,
+                                  verify_before_release).launch(stream)
 
     def prepare_writeback_layer(self, wire: torch.Tensor, nbytes: int, nrec: int, n_k: int,
                                 cache_k: torch.Tensor, cache_v: torch.Tensor, slots: torch.Tensor,
