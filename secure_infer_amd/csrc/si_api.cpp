@@ -16,7 +16,7 @@
 #include <unordered_set>
 #include <vector>
 
-#include "si_device.h"
+#include "si_layout.h"
 #include "si_host.h"
 #include "si_kernels.h"
 
