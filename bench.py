@@ -361,54 +361,13 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
     return out
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
-    ap.add_argument("--chunk-rows", type=int, default=0)
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--e2e-steps", type=int, default=3,
-                    help="steps of the host-memory path (host seal + pinned ring + PCIe); 0 = skip")
-    ap.add_argument("--slice-streams", type=int, default=1,
-                    help="slice streams of the end-to-end reload (the reference's PIPE_GCM_H2D_SLICE_STREAMS, default 1)")
-    ap.add_argument("--stripe", action="store_true",
-                    help="stripe each causal group over the slice streams as the reference does")
-    ap.add_argument("--verify-before-release", action="store_true",
-                    help="reload with SI_RELOAD_VERIFY_BEFORE_RELEASE (tags checked before any plaintext is written)")
-    ap.add_argument("--copy-mb", type=int, default=0,
-                    help="only run a plain device copy of this many MiB (PMC byte calibration)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: records are independent and need no exchange; "
-              "run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-    import secure_infer_amd as si
-
-    if args.copy_mb:
-        n = args.copy_mb << 20
-        src = torch.ones(n, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        dst.copy_(src)  # warm-up: page-table entries of both buffers
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(4):
-            dst.copy_(src)
-        t1.record()
-        torch.cuda.synchronize()
-        dt = t0.elapsed_time(t1) * 1e-3 / 4
-        # read + write bytes per copy over its time: the device's practical
-        # streaming rate, the ceiling of the memory-bound codec kernels
-        print(json.dumps({"copy_bytes": n, "launches": 5,
-                          "copy_read_plus_write_GB_s": round(2 * n / dt / 1e9, 1)}), flush=True)
-        return
-
-    cfg = CONFIGS[args.config]
+def run_workload(name: str, args, torch, si, steps: int, warmup: int, with_cpu: bool, cpu_budget: float,
+                 e2e_steps: int) -> dict:
+    """One workload: set-up (wire records made on the device), `warmup`
+    untimed steps, `steps` timed steps of one launch sequence per layer, the
+    per-launch kernel pass, correctness, and optionally the CPU leg (oracle
+    check of sampled layers + OpenSSL baseline) and the end-to-end leg."""
+    cfg = CONFIGS[name]
     op = cfg["op"]
     L, H, D, NB, NS, bits = cfg["layers"], cfg["heads"], cfg["dim"], cfg["blocks"], cfg["slots"], cfg["bits"]
     if args.chunk_rows:
@@ -498,7 +457,7 @@ def main():
         step = writeback_layer
     torch.cuda.synchronize()
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         for layer in range(L):
             step(layer)
     torch.cuda.synchronize()
@@ -509,14 +468,14 @@ def main():
     t_start, t_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         for layer in range(L):
             step(layer)
     t_stop.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_stop)
-    ms_per_step = total_ms / args.steps
-    us_launch = total_ms * 1e3 / (args.steps * L)
+    ms_per_step = total_ms / steps
+    us_launch = total_ms * 1e3 / (steps * L)
 
     # correctness of what was timed: every layer on the device (bf16 reload),
     # sampled layers against the oracle (every workload)
@@ -533,7 +492,7 @@ def main():
     tamper_ok = None
     if op == "reload" and tampered:
         zeroed = all(bool((cache[l, r // NB, slots[l, r % NB]] == 0).all()) for l, r in tampered)
-        tamper_ok = nfail == len(tampered) * args.steps and zeroed
+        tamper_ok = nfail == len(tampered) * steps and zeroed
 
     # The kernel time per launch, measured in this run: one more pass of the
     # same prepared launches after the timed region (same results: reloads
@@ -567,22 +526,22 @@ def main():
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic (seeded torch.randn bf16 KV, seeded key/salt; ciphertext produced on device)",
-        "config": {"workload": args.config, "direction": op, "layers": L, "kv_heads": H, "head_dim": D,
+        "config": {"workload": name, "direction": op, "layers": L, "kv_heads": H, "head_dim": D,
                    "tokens": NB * 128, "blocks": NB, "records_per_layer": nrec,
                    "record_bytes": nbytes, "cache_slots": NS, "codec_bits": bits,
                    "tampered_records": len(tampered), "algorithmic_bytes_per_layer": algo_layer,
                    **({"verify_before_release": True} if args.verify_before_release else {})},
         "us_per_layer": round(us_launch, 3),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "failed_records_per_step": nfail // max(args.steps, 1),
+        "failed_records_per_step": nfail // max(steps, 1),
         "bit_exact": exact,
         "bit_exact_checked": ("every layer on the device + " if (op == "reload" and bits == 0) else "") +
                              f"layers {sample_layers} against the oracle in the CPU leg" +
@@ -593,16 +552,16 @@ def main():
         "tamper_fail_closed": tamper_ok,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic(args.config),
+                     "traffic": load_traffic(name),
                      "kernel_us": round(kernel_us, 3),
                      "kernel_us_range": [round(float(per_launch_us.min()), 3), round(float(per_launch_us.max()), 3)],
                      "kernel_us_source": (f"median over {L} layers of one pass after the timed region: HIP events "
                                           "at the dispatch start of each layer's first kernel and the end of its "
                                           "last (hipExtLaunchKernel)"),
                      "region_us_per_launch": round(us_launch, 3)},
-        "issue": load_issue(args.config),
+        "issue": load_issue(name),
     }
-    if not args.no_cpu:
+    if with_cpu:
         # The CPU leg: the oracle checks the timed work on sampled layers, then
         # OpenSSL on the host cores is timed on one layer.
         res["bit_exact"] = exact and cpu_check_sampled_layers(
@@ -617,15 +576,90 @@ def main():
         if op == "writeback":
             wh.reshape(nrec, stride)[:, :tag_off + 16] = 0  # the host recomputes ciphertext and tags
         res["cpu_baseline"] = cpu_baseline(op, wh, stride, nbytes, nrec, n_k, key, ivs, H, D, bits, layer,
-                                           args.cpu_budget, algo_layer, planes, gw)
-    if args.e2e_steps > 0:
+                                           cpu_budget, algo_layer, planes, gw)
+    if e2e_steps > 0:
         if op == "reload" and "SECURE_INFER_H2D_PROFILE" not in os.environ:
             # read by the library at the first H2D swap, which comes later
             import tempfile
             os.environ["SECURE_INFER_H2D_PROFILE"] = os.path.join(tempfile.mkdtemp(), "h2d_ledger.csv")
         res["end_to_end"] = end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer,
-                                       args.e2e_steps, truth if (op == "reload" and bits == 0) else None,
+                                       e2e_steps, truth if (op == "reload" and bits == 0) else None,
                                        max(1, min(args.slice_streams, 8)), args.stripe)
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
+    ap.add_argument("--chunk-rows", type=int, default=0)
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--e2e-steps", type=int, default=3,
+                    help="steps of the host-memory path (host seal + pinned ring + PCIe); 0 = skip")
+    ap.add_argument("--slice-streams", type=int, default=1,
+                    help="slice streams of the end-to-end reload (the reference's PIPE_GCM_H2D_SLICE_STREAMS, default 1)")
+    ap.add_argument("--stripe", action="store_true",
+                    help="stripe each causal group over the slice streams as the reference does")
+    ap.add_argument("--verify-before-release", action="store_true",
+                    help="reload with SI_RELOAD_VERIFY_BEFORE_RELEASE (tags checked before any plaintext is written)")
+    ap.add_argument("--single", action="store_true",
+                    help="the headline workload only (by default its run also times every other workload)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (PMC byte calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: records are independent and need no exchange; "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import secure_infer_amd as si
+
+    if args.copy_mb:
+        n = args.copy_mb << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # warm-up: page-table entries of both buffers
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(4):
+            dst.copy_(src)
+        t1.record()
+        torch.cuda.synchronize()
+        dt = t0.elapsed_time(t1) * 1e-3 / 4
+        # read + write bytes per copy over its time: the device's practical
+        # streaming rate, the ceiling of the memory-bound codec kernels
+        print(json.dumps({"copy_bytes": n, "launches": 5,
+                          "copy_read_plus_write_GB_s": round(2 * n / dt / 1e9, 1)}), flush=True)
+        return
+
+    res = run_workload(args.config, args, torch, si, args.steps, args.warmup, not args.no_cpu, args.cpu_budget,
+                       args.e2e_steps)
+    if args.config == DEFAULT and not args.single:
+        # The other workloads in the same run, so one driver run times all of
+        # them: same device measurement and checks, a short CPU leg, no
+        # end-to-end leg.  `value` and `config` stay the headline's.
+        others = {}
+        for name in sorted(CONFIGS):
+            if name == DEFAULT:
+                continue
+            r = run_workload(name, args, torch, si, min(args.steps, 10), min(args.warmup, 2), not args.no_cpu,
+                             min(args.cpu_budget, 2.0), 0)
+            others[name] = {k: r[k] for k in ("us_per_layer", "value", "hbm_frac", "ms_per_step", "steps", "warmup",
+                                              "bit_exact", "bit_exact_checked", "tamper_fail_closed",
+                                              "failed_records_per_step")}
+            others[name]["GB_s"] = others[name].pop("value")
+            others[name]["config"] = r["config"]
+            others[name]["roofline"] = {k: r["roofline"][k] for k in ("achieved", "frac", "kernel_us", "traffic")}
+            if "cpu_baseline" in r:
+                others[name]["cpu_baseline"] = {k: r["cpu_baseline"][k] for k in ("value", "unit", "cores",
+                                                                                  "us_per_layer", "matches_gpu")}
+            torch.cuda.empty_cache()
+        res["other_workloads"] = others
     print(json.dumps(res), flush=True)
 
 

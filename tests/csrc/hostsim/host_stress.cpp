@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -49,6 +50,17 @@ std::atomic<int> g_failures{0};
             g_failures.fetch_add(1);                       \
         }                                                  \
     } while (0)
+
+// Where each scenario thread is (a watchdog prints them if a round stalls).
+constexpr int kSlots = 16;
+std::atomic<const char*> g_stage[kSlots];
+std::atomic<uint32_t> g_stage_layer[kSlots];
+
+void stage(int slot, const char* what, uint32_t layer = 0)
+{
+    g_stage_layer[slot].store(layer);
+    g_stage[slot].store(what);
+}
 
 const uint8_t kKey[16] = {0x10, 0x21, 0x32, 0x43, 0x54, 0x65, 0x76, 0x87,
                           0x98, 0xa9, 0xba, 0xcb, 0xdc, 0xed, 0xfe, 0x0f};
@@ -118,7 +130,8 @@ std::vector<uint8_t>& kept(std::vector<uint8_t> v)
 // tamper: this thread (alone) arms the H2D fault injection for its own
 // layers (it matches layer, kind and host block, so no other thread's
 // records are hit).
-void reload_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint32_t bits, uint32_t seed, bool tamper)
+void reload_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t layers, uint32_t bits, uint32_t seed,
+                   bool tamper)
 {
     std::mt19937 rng(seed);
     hipStream_t stream;
@@ -144,18 +157,24 @@ void reload_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint
         const int64_t victim = map[2 * 3];
         const int mode = tamper ? int(l % 4) : 0;  // 1: corrupted once, 2: corrupted twice
         if (mode == 1 || mode == 2) secure_infer_test_tamper_h2d(int32_t(layer), 1, victim, uint32_t(mode));
+        stage(slot, "reload: prefetch", layer);
         if (l % 2 == 1)
             CHECK(secure_infer_h2d_prefetch_group(sess, pools[0].data(), pools[1].data(), rb, nhost, map.data(),
                                                   uint32_t(n), layer, bits, kHeads, kDim) == 0,
                   "prefetch_group layer %u", layer);
+        stage(slot, "reload: swaps", layer);
         CHECK(secure_infer_h2d_layer_group_begin(2 * n) == 0, "group_begin");
         for (uint32_t kind = 0; kind < 2; ++kind)
             CHECK(secure_infer_h2d_swap(stream, sess, pools[kind].data(), rb, nhost, cache[kind].data(), kBlock, nslots,
                                         map.data(), uint32_t(n), kind, layer, bits, kHeads, kDim, nullptr) == 0,
                   "h2d_swap layer %u kind %u", layer, kind);
+        stage(slot, "reload: group_end", layer);
         CHECK(secure_infer_h2d_layer_group_end() == 0, "group_end");
+        stage(slot, "reload: wait_layer", layer);
         const int rc = secure_infer_recovery_wait_layer_authentication(layer);
+        stage(slot, "reload: stream sync", layer);
         hipStreamSynchronize(stream);
+        stage(slot, "reload: check", layer);
         CHECK(rc == (mode == 2 ? -1 : 0), "layer %u mode %d wait rc %d", layer, mode, rc);
         for (uint32_t kind = 0; kind < 2; ++kind)
             for (size_t i = 0; i < n; ++i) {
@@ -171,12 +190,14 @@ void reload_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint
             }
         if (tamper) secure_infer_test_tamper_h2d(-1, -1, -1, 0);
     }
+    stage(slot, "reload: stream destroy");
     hipStreamDestroy(stream);
+    stage(slot, "reload: done");
 }
 
 // ---------------------------------------------------------------- store
 
-void store_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint32_t bits, uint32_t seed,
+void store_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t layers, uint32_t bits, uint32_t seed,
                   bool tamper)
 {
     std::mt19937 rng(seed);
@@ -191,6 +212,7 @@ void store_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint3
     };
     std::vector<Layer> ls(layers);
     if (tamper) secure_infer_test_tamper_d2h(1);
+    stage(slot, "store: swaps", first_layer);
     CHECK(secure_infer_d2h_batch_begin(2 * n * layers) == 1, "batch_begin");
     for (uint32_t l = 0; l < layers; ++l) {
         Layer& L = ls[l];
@@ -213,8 +235,11 @@ void store_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint3
             CHECK(secure_infer_d2h_group_end() == 0, "d2h group_end");
         }
     }
+    stage(slot, "store: device barrier", first_layer);
     CHECK(secure_infer_d2h_batch_device_barrier() == 0, "device barrier");
+    stage(slot, "store: batch_end", first_layer);
     const int rc = secure_infer_d2h_batch_end();
+    stage(slot, "store: check", first_layer);
     CHECK(rc == (tamper ? -1 : 0), "batch_end rc %d (tamper %d)", rc, int(tamper));
     size_t zeroed = 0;
     for (uint32_t l = 0; l < layers; ++l) {
@@ -235,15 +260,18 @@ void store_thread(si_session* sess, uint32_t first_layer, uint32_t layers, uint3
     }
     CHECK(zeroed == (tamper ? 1u : 0u), "%zu zeroed blocks (tamper %d)", zeroed, int(tamper));
     secure_infer_test_tamper_d2h(0);
+    stage(slot, "store: stream destroy", first_layer);
     hipStreamDestroy(stream);
+    stage(slot, "store: done");
 }
 
 // ---------------------------------------------------------------- exits
 
 // A thread ends inside a layer group with a swap queued: its ring slot and
 // session hold go with it; nothing was issued.
-void exit_inside_group(si_session* sess, uint32_t layer, uint32_t seed)
+void exit_inside_group(int slot, si_session* sess, uint32_t layer, uint32_t seed)
 {
+    stage(slot, "exit_inside_group: start", layer);
     std::mt19937 rng(seed);
     hipStream_t stream;
     hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
@@ -256,11 +284,13 @@ void exit_inside_group(si_session* sess, uint32_t layer, uint32_t seed)
                                 kHeads, kDim, nullptr) == 0,
           "swap");
     // no group_end: the thread ends here (its stream outlives it)
+    stage(slot, "exit_inside_group: thread exit", layer);
 }
 
 // A thread ends inside a D2H batch: its issued launches finish first.
-void exit_inside_batch(si_session* sess, uint32_t layer, uint32_t seed)
+void exit_inside_batch(int slot, si_session* sess, uint32_t layer, uint32_t seed)
 {
+    stage(slot, "exit_inside_batch: start", layer);
     std::mt19937 rng(seed);
     static hipStream_t stream = [] {
         hipStream_t s;
@@ -281,12 +311,14 @@ void exit_inside_batch(si_session* sess, uint32_t layer, uint32_t seed)
     CHECK(secure_infer_d2h_group_end() == 0, "group_end");
     CHECK(secure_infer_d2h_batch_device_barrier() == 0, "barrier");  // issues the launch
     // no batch_end: the thread's batch waits for its launch as the thread ends
+    stage(slot, "exit_inside_batch: thread exit", layer);
 }
 
 // ---------------------------------------------------------------- sessions
 
-void destroy_during_prefetch(uint32_t layer, uint32_t seed)
+void destroy_during_prefetch(int slot, uint32_t layer, uint32_t seed)
 {
+    stage(slot, "destroy_during_prefetch: prefetch", layer);
     std::mt19937 rng(seed);
     si_session* s = new_session(900 + seed);
     const size_t nhost = 16, n = 16;
@@ -303,7 +335,9 @@ void destroy_during_prefetch(uint32_t layer, uint32_t seed)
         CHECK(secure_infer_h2d_prefetch_group(s, k.data(), v.data(), kBlock, nhost, map.data(), uint32_t(n), layer, 0,
                                               kHeads, kDim) == 0,
               "prefetch");
+    stage(slot, "destroy_during_prefetch: destroy", layer);
     CHECK(secure_infer_gpu_session_destroy(s) == 0, "destroy with prefetches sealing");
+    stage(slot, "destroy_during_prefetch: done", layer);
 }
 
 void destroy_refused_while_held(uint32_t layer, uint32_t seed)
@@ -341,35 +375,69 @@ void destroy_refused_while_held(uint32_t layer, uint32_t seed)
 
 }  // namespace
 
+// Prints every thread's stage and aborts when a round makes no progress for
+// `limit` seconds (a hang in the library or the stand-in shows where).
+std::atomic<int> g_round_done{-1};
+
+void watchdog(int rounds, int limit)
+{
+    int last = -1;
+    auto since = std::chrono::steady_clock::now();
+    while (g_round_done.load() < rounds - 1) {
+        std::this_thread::sleep_for(std::chrono::milliseconds(200));
+        const int now = g_round_done.load();
+        if (now != last) {
+            last = now;
+            since = std::chrono::steady_clock::now();
+        } else if (std::chrono::steady_clock::now() - since > std::chrono::seconds(limit)) {
+            fprintf(stderr, "[host_stress] WATCHDOG: round %d stalled for %d s\n", now + 1, limit);
+            for (int i = 0; i < kSlots; ++i) {
+                const char* st = g_stage[i].load();
+                if (st) fprintf(stderr, "  thread slot %d: %s (layer %u)\n", i, st, g_stage_layer[i].load());
+            }
+            fflush(stderr);
+            abort();
+        }
+    }
+}
+
 int main(int argc, char** argv)
 {
     const int rounds = argc > 1 ? atoi(argv[1]) : 2;
+    const int limit = argc > 2 ? atoi(argv[2]) : 60;
+    std::thread dog(watchdog, rounds, limit);
     si_session* sess = new_session(77);
     for (int round = 0; round < rounds; ++round) {
         const uint32_t base = 1000u * uint32_t(round + 1);
+        for (int i = 0; i < kSlots; ++i) g_stage[i].store(nullptr);
         std::vector<std::thread> ts;
-        ts.emplace_back(reload_thread, sess, base + 0, 8, 0u, 11u + round, true);
-        ts.emplace_back(reload_thread, sess, base + 100, 8, 4u, 12u + round, false);
-        ts.emplace_back(reload_thread, sess, base + 200, 6, 0u, 13u + round, false);
-        ts.emplace_back(store_thread, sess, base + 300, 5, 0u, 14u + round, false);
-        ts.emplace_back(store_thread, sess, base + 400, 4, 8u, 15u + round, false);
-        ts.emplace_back(exit_inside_group, sess, base + 600, 17u + round);
-        ts.emplace_back(exit_inside_batch, sess, base + 700, 18u + round);
-        ts.emplace_back(destroy_during_prefetch, base + 800, 19u + round);
+        ts.emplace_back(reload_thread, 0, sess, base + 0, 8, 0u, 11u + round, true);
+        ts.emplace_back(reload_thread, 1, sess, base + 100, 8, 4u, 12u + round, false);
+        ts.emplace_back(reload_thread, 2, sess, base + 200, 6, 0u, 13u + round, false);
+        ts.emplace_back(store_thread, 3, sess, base + 300, 5, 0u, 14u + round, false);
+        ts.emplace_back(store_thread, 4, sess, base + 400, 4, 8u, 15u + round, false);
+        ts.emplace_back(exit_inside_group, 5, sess, base + 600, 17u + round);
+        ts.emplace_back(exit_inside_batch, 6, sess, base + 700, 18u + round);
+        ts.emplace_back(destroy_during_prefetch, 7, base + 800, 19u + round);
         for (auto& t : ts) t.join();
         // The D2H fault injection hits any record: the tampered store runs
         // with no other store in flight, beside more reloads.
-        std::thread tr(reload_thread, sess, base + 250, 4, 4u, 21u + round, false);
-        store_thread(sess, base + 500, 3, 0u, 16u + round, true);
+        stage(10, "main: tampered store phase");
+        std::thread tr(reload_thread, 8, sess, base + 250, 4, 4u, 21u + round, false);
+        store_thread(9, sess, base + 500, 3, 0u, 16u + round, true);
         tr.join();
+        stage(10, "main: destroy_refused_while_held");
         destroy_refused_while_held(base + 900, 20u + round);
+        stage(10, "main: round end");
         secure_infer_clear_host_ranges();
         {
             std::lock_guard<std::mutex> g(g_keep_m);
             g_keep.clear();
         }
         fprintf(stderr, "[host_stress] round %d done, %d failures\n", round, g_failures.load());
+        g_round_done.store(round);
     }
+    dog.join();
     CHECK(secure_infer_gpu_session_destroy(sess) == 0, "final destroy");
     hipDeviceSynchronize();
     if (g_failures.load()) {

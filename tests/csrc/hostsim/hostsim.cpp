@@ -30,7 +30,6 @@
 #include <map>
 #include <memory>
 #include <mutex>
-#include <set>
 #include <thread>
 #include <vector>
 
@@ -96,17 +95,24 @@ struct ihipStream_t {
 
 namespace {
 
+// Live streams, shared: a hipDeviceSynchronize on one thread may still be
+// syncing a stream that another thread is destroying (HIP allows both), so
+// the object goes when its last holder lets go.
 std::mutex g_streams_m;
-std::set<ihipStream_t*>& g_streams = *new std::set<ihipStream_t*>();
+std::map<ihipStream_t*, std::shared_ptr<ihipStream_t>>& g_streams =
+    *new std::map<ihipStream_t*, std::shared_ptr<ihipStream_t>>();
+
+ihipStream_t* new_stream()
+{
+    auto p = std::make_shared<ihipStream_t>();
+    std::lock_guard<std::mutex> g(g_streams_m);
+    g_streams[p.get()] = p;
+    return p.get();
+}
 
 ihipStream_t* default_stream()
 {
-    static ihipStream_t* s = [] {
-        auto* p = new ihipStream_t();
-        std::lock_guard<std::mutex> g(g_streams_m);
-        g_streams.insert(p);
-        return p;
-    }();
+    static ihipStream_t* s = new_stream();
     return s;
 }
 
@@ -160,12 +166,12 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int)
 
 hipError_t hipDeviceSynchronize(void)
 {
-    std::vector<ihipStream_t*> all;
+    std::vector<std::shared_ptr<ihipStream_t>> all;
     {
         std::lock_guard<std::mutex> g(g_streams_m);
-        all.assign(g_streams.begin(), g_streams.end());
+        for (auto& e : g_streams) all.push_back(e.second);
     }
-    for (auto* s : all) s->sync();
+    for (auto& s : all) s->sync();
     return hipSuccess;
 }
 
@@ -231,21 +237,22 @@ hipError_t hipMemcpy2DAsync(void* dst, size_t dpitch, const void* src, size_t sp
 
 hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned int)
 {
-    *s = new ihipStream_t();
-    std::lock_guard<std::mutex> g(g_streams_m);
-    g_streams.insert(*s);
+    *s = new_stream();
     return hipSuccess;
 }
 
 hipError_t hipStreamDestroy(hipStream_t s)
 {
     if (!s) return hipErrorInvalidValue;
-    s->sync();
+    std::shared_ptr<ihipStream_t> p;
     {
         std::lock_guard<std::mutex> g(g_streams_m);
-        g_streams.erase(s);
+        auto it = g_streams.find(s);
+        if (it == g_streams.end()) return hipErrorInvalidValue;
+        p = std::move(it->second);
+        g_streams.erase(it);
     }
-    delete s;
+    p->sync();  // its queued work completes; the object goes with its last holder
     return hipSuccess;
 }
 
