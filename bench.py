@@ -325,15 +325,39 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
         out["sealed_ahead_of_demand"] = {"us_per_layer": round(med[True] * 1e6 / L, 1),
                                          "GB_s": round(algo_layer * L / med[True] / 1e9, 2),
                                          "prefetch_stats": si.transfer_prefetch_stats()}
+        # The same steps with each layer's causal groups merged into one
+        # launch (NativeTransfer merge_groups: same swaps, same tickets; one
+        # layer prefetch and one DMA when sealed ahead).
+        nt.merge_groups = True
+        cache.zero_()
+        merged = {}
+        for ahead in (False, True):
+            times = []
+            for _ in range(steps):
+                good, t = step(ahead)
+                ok &= good
+                times.append(t)
+            merged[ahead] = float(np.median(times))
+        if truth is not None:
+            got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
+            ok &= bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
+        nt.merge_groups = False
+        out["merged_layer_launch"] = {
+            "on_demand_us_per_layer": round(merged[False] * 1e6 / L, 1),
+            "sealed_ahead_us_per_layer": round(merged[True] * 1e6 / L, 1),
+            "sealed_ahead_GB_s": round(algo_layer * L / merged[True] / 1e9, 2)}
         ledger = os.environ.get("SECURE_INFER_H2D_PROFILE")
         if ledger:
             si.pause_h2d_profile(False)
             split = {}
-            for ahead, name in ((False, "on_demand"), (True, "sealed_ahead_of_demand")):
+            for ahead, merge, name in ((False, False, "on_demand"), (True, False, "sealed_ahead_of_demand"),
+                                       (True, True, "merged_sealed_ahead_of_demand")):
                 si.drain_h2d_profile_after_job()
                 if Path(ledger).exists():
                     Path(ledger).write_text(Path(ledger).read_text().splitlines()[0] + "\n")
+                nt.merge_groups = merge
                 good, t = step(ahead)
+                nt.merge_groups = False
                 ok &= good
                 si.drain_h2d_profile_after_job()
                 split[name] = ledger_split(Path(ledger), 1)

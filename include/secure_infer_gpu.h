@@ -344,6 +344,23 @@ int secure_infer_gcm_replay_reserve(uint64_t transfer_ticket);
  * here (this library has no address predictor to reset). */
 void secure_infer_retire_transfer_prefetches(void);
 void secure_infer_invalidate_transfer_prefetches(void);
+/* No reference counterpart (a layer-wide form of secure_infer_h2d_prefetch_group
+ * for callers that bracket a whole layer in one layer group): seals the K and
+ * V swaps of `ngroups` causal groups of one layer -- group g is rows
+ * [group_start[g], group_start[g] + group_rows[g]) of `mapping`, taken in
+ * the order given -- into one pinned buffer laid out as the device layout of
+ * a launch of exactly those swaps: [every group's K records][every group's V
+ * records][IV words][slot ids].  Tickets follow the swaps' order (group 0's
+ * K, its V, group 1's K, ...), the order the reference's grouped loading
+ * assigns them (native_layerwise.py:96-129), so the records are the ones the
+ * swaps would seal on demand.  The swaps, issued inside one layer group in
+ * that order, then go to the device as one DMA and one launch.  0, or -1
+ * (bad argument, an id outside the host pool, or the prefetch budget
+ * SECURE_INFER_PREFETCH_MB spent: the swaps then seal on demand). */
+int secure_infer_h2d_prefetch_layer(si_session* session, const void* k_base, const void* v_base,
+                                    uint64_t host_block_bytes, uint64_t host_nblocks, const int64_t* mapping,
+                                    const uint32_t* group_start, const uint32_t* group_rows, uint32_t ngroups,
+                                    uint32_t layer, uint32_t codec_bits, uint32_t heads, uint32_t head_dim);
 /* secure_infer.cpp:817-830: swaps served from prefetched records that were
  * ready / that had to wait for their sealing to finish / swaps sealed on
  * demand (the reference's ready / busy_fallback / missing_fallback; a busy

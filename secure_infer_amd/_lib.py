@@ -90,6 +90,7 @@ SIGNATURES = {
     "secure_infer_count_ready_unconsumed_gcm_tickets": ([], _u64),
     "secure_infer_h2d_prefetch": ([_v, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32, _u32, _u32], _i),
     "secure_infer_h2d_prefetch_group": ([_v, _v, _v, _u64, _u64, _v, _u32, _u32, _u32, _u32, _u32], _i),
+    "secure_infer_h2d_prefetch_layer": ([_v, _v, _v, _u64, _u64, _v, _v, _v, _u32, _u32, _u32, _u32, _u32], _i),
     "secure_infer_flush_completed_h2d_profile": ([], None),
     "secure_infer_drain_h2d_profile_after_job": ([], None),
     "secure_infer_pause_h2d_profile": ([ct.c_int], None),

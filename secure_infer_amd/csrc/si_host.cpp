@@ -610,6 +610,11 @@ struct Prefetch {
     // both halves], so one DMA can carry the group's launch.
     const uint8_t* group_ids = nullptr;
     uint32_t group_records = 0;
+    // A layer prefetch (its first K part owns the buffer): [every group's K
+    // records][every group's V records][IV words][slot ids], the device
+    // layout of a launch of exactly the layer's swaps, so one DMA carries it.
+    const uint8_t* layer_tail = nullptr;
+    uint32_t layer_records = 0;
     std::mutex m;
     std::condition_variable cv;
     uint32_t tasks = 0, done = 0;
@@ -853,7 +858,10 @@ void seal_record(const si_internal::SessionKeys& keys, const uint8_t* src, uint6
 // One swap's records within a launch.
 struct H2DPart {
     const uint8_t* src = nullptr;  // its sealed records: ring slot rows or a prefetch buffer
-    uint32_t r0 = 0, n = 0;        // rows [r0, r0 + n) of the launch
+    uint32_t r0 = 0, n = 0;        // host rows [r0, r0 + n) of the slot (swap order)
+    uint32_t kind = 0;
+    uint32_t dev_r0 = 0;           // first record on the device (K parts, then V parts)
+    size_t ids0 = 0;               // its slot ids in the launch's slot_ids (swap order)
     uint64_t t0 = 0;               // ticket of its first record
     uint32_t source = 0;           // 0 sealed on demand, 1 prefetched, 2 prefetch waited for
     double seal_us = 0;
@@ -862,11 +870,13 @@ struct H2DPart {
 };
 
 // The records of consecutive swaps that go to the device as one copy
-// sequence and one reload launch: K swaps before V swaps, all of one stream,
-// session, layer and geometry, in one ring slot laid out as
-// [cap wire records][iv words, n x 16][slot ids, n x 8].  Inside a layer
-// group the swaps accumulate until the group ends (or the next swap does not
-// fit), as the reference batches a group's swaps
+// sequence and one reload launch: all of one stream, session, layer and
+// geometry.  On the host a ring slot holds them in swap order; on the device
+// the launch is laid out [cap wire records: K parts, then V parts, each in
+// swap order][iv words, n x 16][slot ids, n x 8], so K and V swaps may come
+// in any order (a layer group around several causal groups takes K1 V1 K2
+// V2 ...).  Inside a layer group the swaps accumulate until the group ends
+// (or the next swap does not fit), as the reference batches a group's swaps
 // (enqueue_h2d_gcm_batch_task, flushed by secure_infer_h2d_layer_group_end,
 // secure_infer.cpp:5862-5904); outside a group every swap is a launch of
 // its own.
@@ -971,9 +981,22 @@ int flush_launch()
     Mirror& sl = *L->ring->slots[L->slot];
     const bool prof = profile_on();
     const size_t wire_cap = size_t(L->cap) * L->stride;
-    bool contiguous = true;  // tickets t0 .. t0 + n - 1 in record order
-    for (size_t i = 1; i < L->parts.size(); ++i)
-        contiguous = contiguous && L->parts[i].t0 == L->parts[i - 1].t0 + L->parts[i - 1].n;
+    // Device order: the K parts, then the V parts, each in swap order.
+    std::vector<size_t> order;
+    order.reserve(L->parts.size());
+    for (uint32_t kind = 0; kind < 2; ++kind)
+        for (size_t i = 0; i < L->parts.size(); ++i)
+            if (L->parts[i].kind == kind) order.push_back(i);
+    {
+        uint32_t r = 0;
+        for (size_t i : order) {
+            L->parts[i].dev_r0 = r;
+            r += L->parts[i].n;
+        }
+    }
+    bool contiguous = true;  // tickets t0 .. t0 + n - 1 in device order
+    for (size_t k = 1; k < order.size(); ++k)
+        contiguous = contiguous && L->parts[order[k]].t0 == L->parts[order[k - 1]].t0 + L->parts[order[k - 1]].n;
     const size_t iv_bytes = contiguous ? 0 : size_t(L->n) * 16;
     uint8_t* tail = sl.host + wire_cap;
     if (!contiguous) {
@@ -983,14 +1006,17 @@ int flush_launch()
         for (const H2DPart& p : L->parts)
             for (uint32_t r = 0; r < p.n; ++r) {
                 const uint64_t c = L->keys.nonce + p.t0 + r;
-                uint32_t* o = w + 4 * size_t(p.r0 + r);
+                uint32_t* o = w + 4 * size_t(p.dev_r0 + r);
                 o[0] = salt;
                 o[1] = uint32_t(c >> 32);
                 o[2] = uint32_t(c);
                 o[3] = 2;
             }
     }
-    memcpy(tail + iv_bytes, L->slot_ids.data(), size_t(L->n) * 8);
+    int64_t* ids = reinterpret_cast<int64_t*>(tail + iv_bytes);
+    for (const H2DPart& p : L->parts) memcpy(ids + p.dev_r0, L->slot_ids.data() + p.ids0, size_t(p.n) * 8);
+    for (H2DPart& p : L->parts)
+        if (p.ob) p.ob->status_off = p.dev_r0;  // the kernel stores statuses in device order
 
     bool launched = false;
     // On failure nothing is registered; copies still queued are waited for
@@ -1005,32 +1031,43 @@ int flush_launch()
     };
     if (prof && hipEventRecord(sl.p_c0, L->ring->copy) != hipSuccess) return fail();
     // A launch of exactly one group prefetch (its K half, then its V half, as
-    // large as the launch and with one ticket run): the prefetch buffer holds
-    // the slot ids right after the records, the device layout of this
-    // launch, so one copy carries all of it.
-    const Prefetch* gk = L->parts.size() == 2 ? L->parts[0].pf.get() : nullptr;
-    const bool one_copy = gk && gk->group_records == L->n && L->cap == L->n && contiguous && L->parts[0].r0 == 0 &&
-                          L->parts[1].pf && L->parts[1].pf->owner.get() == gk &&
-                          L->parts[1].src == L->parts[0].src + size_t(L->parts[0].n) * L->stride &&
-                          memcmp(gk->group_ids, L->slot_ids.data(), size_t(L->n) * 8) == 0;
+    // large as the launch and with one ticket run), or of exactly one layer
+    // prefetch: the prefetch buffer holds the records in device order
+    // followed by the launch's tail (slot ids; a layer prefetch's IV words
+    // first), so one copy carries all of it.
+    const Prefetch* first = L->parts[order[0]].pf.get();
+    bool one_copy = false;
+    if (first && L->cap == L->n) {
+        const Prefetch* owner = first->owner ? first->owner.get() : first;
+        bool same_buffer = true;
+        for (size_t i : order) {
+            const Prefetch* pf = L->parts[i].pf.get();
+            same_buffer = same_buffer && pf && (pf == owner || pf->owner.get() == owner) &&
+                          L->parts[i].src == owner->host + size_t(L->parts[i].dev_r0) * L->stride;
+        }
+        if (same_buffer && owner->group_records == L->n && contiguous)
+            one_copy = memcmp(owner->group_ids, ids, size_t(L->n) * 8) == 0;
+        else if (same_buffer && owner->layer_records == L->n && !contiguous)
+            one_copy = memcmp(owner->layer_tail, tail, iv_bytes + size_t(L->n) * 8) == 0;
+    }
     if (one_copy) {
-        if (hipMemcpyAsync(sl.dev, L->parts[0].src, size_t(L->n) * (L->stride + 8), hipMemcpyHostToDevice,
-                           L->ring->copy) != hipSuccess)
+        if (hipMemcpyAsync(sl.dev, L->parts[order[0]].src, size_t(L->n) * L->stride + iv_bytes + size_t(L->n) * 8,
+                           hipMemcpyHostToDevice, L->ring->copy) != hipSuccess)
             return fail();
     } else {
-        // One copy per run of parts whose sealed records sit back to back,
-        // then the IV words and slot ids.
-        for (size_t i = 0; i < L->parts.size();) {
-            const uint8_t* src = L->parts[i].src;
-            const uint32_t r0 = L->parts[i].r0;
-            uint32_t rows = L->parts[i].n;
-            size_t j = i + 1;
-            for (; j < L->parts.size() && L->parts[j].src == src + size_t(rows) * L->stride; ++j)
-                rows += L->parts[j].n;
-            if (hipMemcpyAsync(sl.dev + size_t(r0) * L->stride, src, size_t(rows) * L->stride,
+        // One copy per run of parts (in device order) whose sealed records sit
+        // back to back, then the IV words and slot ids.
+        for (size_t k = 0; k < order.size();) {
+            const H2DPart& p0 = L->parts[order[k]];
+            const uint8_t* src = p0.src;
+            uint32_t rows = p0.n;
+            size_t j = k + 1;
+            for (; j < order.size() && L->parts[order[j]].src == src + size_t(rows) * L->stride; ++j)
+                rows += L->parts[order[j]].n;
+            if (hipMemcpyAsync(sl.dev + size_t(p0.dev_r0) * L->stride, src, size_t(rows) * L->stride,
                                hipMemcpyHostToDevice, L->ring->copy) != hipSuccess)
                 return fail();
-            i = j;
+            k = j;
         }
         if (hipMemcpyAsync(sl.dev + wire_cap, tail, iv_bytes + size_t(L->n) * 8, hipMemcpyHostToDevice,
                            L->ring->copy) != hipSuccess)
@@ -1047,7 +1084,7 @@ int flush_launch()
     d.nrec = L->n;
     d.n_k = L->n_k;
     d.iv_words = contiguous ? nullptr : reinterpret_cast<const uint32_t*>(sl.dev + wire_cap);
-    d.ticket_base = contiguous ? L->parts[0].t0 : 0;
+    d.ticket_base = contiguous ? L->parts[order[0]].t0 : 0;
     d.cache_k = L->cache[0] ? L->cache[0] : L->cache[1];
     d.cache_v = L->cache[1] ? L->cache[1] : L->cache[0];
     d.slot_bytes = L->slot_bytes;
@@ -1113,8 +1150,7 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     if (L && !(L->stream == stream && L->s == s && L->ds == ds && L->layer == layer && L->codec == codec_bits &&
                L->heads == heads && L->dim == head_dim && L->bytes == bytes && L->slot_bytes == slot_bytes &&
                L->nslots == nslots && L->fail_count == fail_count && L->observe == observe &&
-               (L->cache[kind] == nullptr || L->cache[kind] == dev_cache) && !(kind == 0 && L->n > L->n_k) &&
-               L->n + n <= L->cap)) {
+               (L->cache[kind] == nullptr || L->cache[kind] == dev_cache) && L->n + n <= L->cap)) {
         if (flush_launch() != 0) return -1;
         L = nullptr;
     }
@@ -1179,6 +1215,8 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     H2DPart part;
     part.r0 = L->n;
     part.n = n;
+    part.kind = kind;
+    part.ids0 = L->slot_ids.size();
     part.source = source;
     if (pf) {
         part.src = pf->host;
@@ -1811,6 +1849,78 @@ int secure_infer_h2d_prefetch_group(si_session* s, const void* k_base, const voi
     std::vector<std::function<void()>> tasks;
     queue_seals(pk, tasks);
     queue_seals(pv, tasks);
+    Pool::get().submit_all(tasks);
+    return 0;
+}
+
+int secure_infer_h2d_prefetch_layer(si_session* s, const void* k_base, const void* v_base, uint64_t host_block_bytes,
+                                    uint64_t host_nblocks, const int64_t* mapping, const uint32_t* group_start,
+                                    const uint32_t* group_rows, uint32_t ngroups, uint32_t layer, uint32_t codec_bits,
+                                    uint32_t heads, uint32_t head_dim)
+{
+    if (!s || !k_base || !v_base || !mapping || !group_start || !group_rows || ngroups == 0 || host_nblocks == 0)
+        return -1;
+    uint64_t bytes = 0;
+    if (!valid_geometry(codec_bits, heads, head_dim, host_block_bytes, bytes)) return -1;
+    uint64_t total = 0;
+    for (uint32_t g = 0; g < ngroups; ++g) {
+        if (group_rows[g] == 0) return -1;
+        for (uint32_t r = 0; r < group_rows[g]; ++r) {
+            const int64_t hb = mapping[2 * (uint64_t(group_start[g]) + r)];
+            if (hb < 0 || uint64_t(hb) >= host_nblocks) return -1;
+        }
+        total += group_rows[g];
+    }
+    if (total > UINT32_MAX / 4) return -1;
+    const uint32_t N = uint32_t(total);
+    const si_internal::SessionKeys keys = si_internal::session_keys(s);
+    if (bytes > keys.max_record_bytes) return -1;
+    const uint64_t stride = secure_infer_wire_stride(bytes);
+    const size_t wire = size_t(2) * N * stride;
+    size_t cap = 0;
+    uint8_t* buf = take_pf_buffer(wire + size_t(2) * N * (16 + 8), cap);
+    if (!buf) return -1;
+    // Tickets in the order the swaps take them (each group's K, then its V):
+    // the records keep the reference's tickets while the buffer holds every K
+    // record before every V record, with explicit IV words.
+    const uint64_t t0 = si_internal::reserve_tickets(2 * N);
+    if (!si_internal::replay_reserve_range(t0, 2 * uint64_t(N))) return -1;
+    uint32_t* ivw = reinterpret_cast<uint32_t*>(buf + wire);
+    int64_t* ids = reinterpret_cast<int64_t*>(buf + wire + size_t(2) * N * 16);
+    const uint32_t salt = (uint32_t(keys.salt[0]) << 24) | (uint32_t(keys.salt[1]) << 16) |
+                          (uint32_t(keys.salt[2]) << 8) | uint32_t(keys.salt[3]);
+    std::vector<std::shared_ptr<Prefetch>> parts;
+    uint32_t off = 0;  // K rows of the groups before this one
+    for (uint32_t g = 0; g < ngroups; ++g) {
+        const uint32_t n = group_rows[g];
+        const int64_t* map = mapping + 2 * uint64_t(group_start[g]);
+        for (uint32_t kind = 0; kind < 2; ++kind) {
+            const uint32_t row = kind * N + off;  // device row of the part's first record
+            auto pf = new_prefetch(s, keys, kind ? v_base : k_base, host_block_bytes, map, n, kind, layer, codec_bits,
+                                   heads, head_dim, bytes, buf + size_t(row) * stride);
+            pf->t0 = t0 + 2 * uint64_t(off) + uint64_t(kind) * n;
+            for (uint32_t r = 0; r < n; ++r) {
+                const uint64_t c = keys.nonce + pf->t0 + r;
+                uint32_t* o = ivw + 4 * size_t(row + r);
+                o[0] = salt;
+                o[1] = uint32_t(c >> 32);
+                o[2] = uint32_t(c);
+                o[3] = 2;
+                ids[row + r] = map[2 * r + 1];
+            }
+            if (parts.empty()) {
+                pf->cap = cap;
+                pf->layer_tail = buf + wire;
+                pf->layer_records = 2 * N;
+            } else {
+                pf->owner = parts.front();
+            }
+            parts.push_back(std::move(pf));
+        }
+        off += n;
+    }
+    std::vector<std::function<void()>> tasks;
+    for (auto& pf : parts) queue_seals(pf, tasks);
     Pool::get().submit_all(tasks);
     return 0;
 }

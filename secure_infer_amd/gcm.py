@@ -553,12 +553,14 @@ class NativeTransfer:
     """
 
     def __init__(self, session: GcmSession, shape: LayerShape, stream=None, streams=None,
-                 causal_group_blocks: int = 0, pipeline_seal: bool = True, stripe: bool = False):
+                 causal_group_blocks: int = 0, pipeline_seal: bool = True, stripe: bool = False,
+                 merge_groups: bool = False):
         self.session = session
         self.shape = shape
         self.stream = stream
         self.streams = list(streams) if streams else [stream]
         self.stripe = bool(stripe)
+        self.merge_groups = bool(merge_groups)
         self.causal_group_blocks = int(causal_group_blocks)
         self.pipeline_seal = pipeline_seal
         self.layer = 0
@@ -635,7 +637,13 @@ class NativeTransfer:
         L = lib()
         swap, h = L.secure_infer_h2d_swap, self.session._h
         heads, dim, layer = self.shape.heads, self.shape.head_dim, self.layer
-        for k, parts in plan:
+        # merge_groups: one layer group around every causal group of the layer
+        # (same swaps, same order, same tickets), so the layer goes to the
+        # device as one launch; otherwise one per causal group, the
+        # reference's grouping (native_layerwise.py:96-112).
+        brackets = [(sum(k for k, _ in plan), [p for _, parts in plan for p in parts])] if self.merge_groups \
+            else plan
+        for k, parts in brackets:
             _check(L.secure_infer_h2d_layer_group_begin(2 * k), "h2d_layer_group_begin")
             try:
                 for kind, j, part, rows in parts:
@@ -670,7 +678,19 @@ class NativeTransfer:
         # are sealed together into one buffer, which the group's launch
         # copies in one DMA (same tickets as two prefetches: K, then V).
         paired = (len(self.streams) == 1 or not self.stripe) and pools[0][1:] == pools[1][1:]
-        for _, parts in self._plan(mapping):
+        plan = self._plan(mapping)
+        if paired and self.merge_groups and len(plan) > 1:
+            # The whole layer in one buffer, in the device layout of its one
+            # launch: one DMA per layer.
+            base = mapping.data_ptr()
+            starts = (ct.c_uint32 * len(plan))(*[(parts[0][2].value - base) // 16 for _, parts in plan])
+            rows = (ct.c_uint32 * len(plan))(*[parts[0][3] for _, parts in plan])
+            sp, sbb, sn = pools[0]
+            ok = L.secure_infer_h2d_prefetch_layer(h, sp, pools[1][0], sbb, sn, ct.c_void_p(base), starts, rows,
+                                                   len(plan), layer, bits, heads, dim) == 0
+            self._prefetched.add(layer)
+            return ok
+        for _, parts in plan:
             if paired:
                 (_, _, part, rows), _ = parts
                 sp, sbb, sn = pools[0]

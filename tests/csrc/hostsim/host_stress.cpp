@@ -26,6 +26,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <string>
 #include <memory>
 #include <mutex>
 #include <random>
@@ -34,6 +36,8 @@
 
 #include "secure_infer_gpu.h"
 #include "si_oracle.h"
+
+extern "C" size_t hostsim_reload_log(uint32_t layer, uint64_t* out, size_t cap);
 
 namespace {
 
@@ -130,8 +134,12 @@ std::vector<uint8_t>& kept(std::vector<uint8_t> v)
 // tamper: this thread (alone) arms the H2D fault injection for its own
 // layers (it matches layer, kind and host block, so no other thread's
 // records are hit).
+// merge: each layer's two causal groups (tail first, as the reference's
+// grouped loading submits them) go inside one layer group, K1 V1 K2 V2, so
+// the launch packs K before V on the device; odd layers are sealed ahead as
+// one layer buffer (secure_infer_h2d_prefetch_layer).
 void reload_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t layers, uint32_t bits, uint32_t seed,
-                   bool tamper)
+                   bool tamper, bool merge)
 {
     std::mt19937 rng(seed);
     hipStream_t stream;
@@ -140,10 +148,12 @@ void reload_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t la
     const uint64_t rb = record_bytes(bits);
     for (uint32_t l = 0; l < layers; ++l) {
         const uint32_t layer = first_layer + l;
-        std::vector<std::vector<uint8_t>> pools;
-        for (uint32_t kind = 0; kind < 2; ++kind) pools.push_back(host_pool(blocks(rng, nhost), nhost, bits, kind, layer));
+        // The pools stay allocated for the round: their host ranges stay
+        // registered until then, and a range found first names the record.
+        std::vector<uint8_t>* pools[2];
+        for (uint32_t kind = 0; kind < 2; ++kind) pools[kind] = &kept(host_pool(blocks(rng, nhost), nhost, bits, kind, layer));
         for (uint32_t kind = 0; kind < 2; ++kind)
-            secure_infer_register_host_range_ex(pools[kind].data(), pools[kind].size(), layer, kind, rb);
+            secure_infer_register_host_range_ex(pools[kind]->data(), pools[kind]->size(), layer, kind, rb);
         std::vector<uint8_t> cache[2];
         for (auto& c : cache) c.assign(nslots * kBlock, 0x3c);
         std::vector<int64_t> slots(nslots);
@@ -158,16 +168,32 @@ void reload_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t la
         const int mode = tamper ? int(l % 4) : 0;  // 1: corrupted once, 2: corrupted twice
         if (mode == 1 || mode == 2) secure_infer_test_tamper_h2d(int32_t(layer), 1, victim, uint32_t(mode));
         stage(slot, "reload: prefetch", layer);
-        if (l % 2 == 1)
-            CHECK(secure_infer_h2d_prefetch_group(sess, pools[0].data(), pools[1].data(), rb, nhost, map.data(),
+        // causal groups, tail first: rows [n/2, n) then [0, n/2)
+        const uint32_t gstart[2] = {uint32_t(n / 2), 0}, grows[2] = {uint32_t(n - n / 2), uint32_t(n / 2)};
+        if (l % 2 == 1 && merge)
+            CHECK(secure_infer_h2d_prefetch_layer(sess, pools[0]->data(), pools[1]->data(), rb, nhost, map.data(), gstart,
+                                                  grows, 2, layer, bits, kHeads, kDim) == 0,
+                  "prefetch_layer layer %u", layer);
+        else if (l % 2 == 1)
+            CHECK(secure_infer_h2d_prefetch_group(sess, pools[0]->data(), pools[1]->data(), rb, nhost, map.data(),
                                                   uint32_t(n), layer, bits, kHeads, kDim) == 0,
                   "prefetch_group layer %u", layer);
         stage(slot, "reload: swaps", layer);
         CHECK(secure_infer_h2d_layer_group_begin(2 * n) == 0, "group_begin");
-        for (uint32_t kind = 0; kind < 2; ++kind)
-            CHECK(secure_infer_h2d_swap(stream, sess, pools[kind].data(), rb, nhost, cache[kind].data(), kBlock, nslots,
-                                        map.data(), uint32_t(n), kind, layer, bits, kHeads, kDim, nullptr) == 0,
-                  "h2d_swap layer %u kind %u", layer, kind);
+        if (merge) {
+            for (int g = 0; g < 2; ++g)
+                for (uint32_t kind = 0; kind < 2; ++kind)
+                    CHECK(secure_infer_h2d_swap(stream, sess, pools[kind]->data(), rb, nhost, cache[kind].data(), kBlock,
+                                                nslots, map.data() + 2 * gstart[g], grows[g], kind, layer, bits, kHeads,
+                                                kDim, nullptr) == 0,
+                          "h2d_swap layer %u group %d kind %u", layer, g, kind);
+        } else {
+            for (uint32_t kind = 0; kind < 2; ++kind)
+                CHECK(secure_infer_h2d_swap(stream, sess, pools[kind]->data(), rb, nhost, cache[kind].data(), kBlock,
+                                            nslots, map.data(), uint32_t(n), kind, layer, bits, kHeads, kDim,
+                                            nullptr) == 0,
+                      "h2d_swap layer %u kind %u", layer, kind);
+        }
         stage(slot, "reload: group_end", layer);
         CHECK(secure_infer_h2d_layer_group_end() == 0, "group_end");
         stage(slot, "reload: wait_layer", layer);
@@ -175,6 +201,40 @@ void reload_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t la
         stage(slot, "reload: stream sync", layer);
         hipStreamSynchronize(stream);
         stage(slot, "reload: check", layer);
+        {
+            // Tickets rise along the reference's submission order: each causal
+            // group's K records, then its V records (native_layerwise.py:96-112),
+            // whether a group was its own layer group or part of a merged one,
+            // sealed on demand or ahead of demand (a retry's fresh ticket is
+            // later; the first ticket of each record counts).
+            std::vector<uint64_t> log(3 * 4 * n * 2);
+            const size_t got = hostsim_reload_log(layer, log.data(), log.size() / 3);
+            std::map<std::pair<uint64_t, uint64_t>, uint64_t> first;
+            for (size_t i = 0; i < std::min(got, log.size() / 3); ++i) {
+                const auto key = std::make_pair(log[3 * i], log[3 * i + 1]);
+                auto it = first.find(key);
+                if (it == first.end() || log[3 * i + 2] < it->second) first[key] = log[3 * i + 2];
+            }
+            std::vector<uint64_t> seq;
+            const int ngroups = merge ? 2 : 1;
+            for (int g = 0; g < ngroups; ++g) {
+                const uint32_t r0 = merge ? gstart[g] : 0, rows = merge ? grows[g] : uint32_t(n);
+                for (uint64_t kind = 0; kind < 2; ++kind)
+                    for (uint32_t r = r0; r < r0 + rows; ++r) {
+                        auto it = first.find(std::make_pair(kind, uint64_t(map[2 * r])));
+                        seq.push_back(it == first.end() ? 0 : it->second);
+                    }
+            }
+            bool rising = seq.size() == 2 * n && seq[0] != 0;
+            for (size_t i = 1; i < seq.size(); ++i) rising = rising && seq[i] > seq[i - 1];
+            if (!rising) {
+                std::string t;
+                for (auto v : seq) t += " " + std::to_string(v);
+                fprintf(stderr, "[host_stress] layer %u got %zu log rows, tickets:%s\n", layer, got, t.c_str());
+            }
+            CHECK(rising, "layer %u (merge %d, prefetched %d): tickets not in the reference's order", layer, int(merge),
+                  int(l % 2 == 1));
+        }
         CHECK(rc == (mode == 2 ? -1 : 0), "layer %u mode %d wait rc %d", layer, mode, rc);
         for (uint32_t kind = 0; kind < 2; ++kind)
             for (size_t i = 0; i < n; ++i) {
@@ -185,7 +245,7 @@ void reload_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t la
                     CHECK(zero, "layer %u: the persistently corrupted record is not zeroed", layer);
                     continue;
                 }
-                const auto want = expect_slot(pools[kind].data() + uint64_t(map[2 * i]) * rb, bits, kind);
+                const auto want = expect_slot(pools[kind]->data() + uint64_t(map[2 * i]) * rb, bits, kind);
                 CHECK(memcmp(slot, want.data(), kBlock) == 0, "layer %u kind %u record %zu differs", layer, kind, i);
             }
         if (tamper) secure_infer_test_tamper_h2d(-1, -1, -1, 0);
@@ -207,7 +267,7 @@ void store_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t lay
     const uint64_t rb = record_bytes(bits);
     struct Layer {
         std::vector<uint16_t> cache[2];
-        std::vector<uint8_t> pool[2];
+        std::vector<uint8_t>* pool[2];
         std::vector<int64_t> map;
     };
     std::vector<Layer> ls(layers);
@@ -218,8 +278,8 @@ void store_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t lay
         Layer& L = ls[l];
         for (uint32_t kind = 0; kind < 2; ++kind) {
             L.cache[kind] = blocks(rng, nslots);
-            L.pool[kind].assign(nhost * rb, 0);
-            secure_infer_register_host_range_ex(L.pool[kind].data(), L.pool[kind].size(), first_layer + l, kind, rb);
+            L.pool[kind] = &kept(std::vector<uint8_t>(nhost * rb, 0));  // registered until the round ends
+            secure_infer_register_host_range_ex(L.pool[kind]->data(), L.pool[kind]->size(), first_layer + l, kind, rb);
         }
         L.map.resize(2 * n);
         for (size_t i = 0; i < n; ++i) {
@@ -228,7 +288,7 @@ void store_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t lay
         }
         for (uint32_t kind = 0; kind < 2; ++kind) {
             CHECK(secure_infer_d2h_group_begin(n) == 1, "d2h group_begin");
-            CHECK(secure_infer_d2h_swap(stream, sess, L.cache[kind].data(), kBlock, nslots, L.pool[kind].data(), rb,
+            CHECK(secure_infer_d2h_swap(stream, sess, L.cache[kind].data(), kBlock, nslots, L.pool[kind]->data(), rb,
                                         nhost, L.map.data(), uint32_t(n), kind, first_layer + l, bits, kHeads,
                                         kDim) == 0,
                   "d2h_swap");
@@ -246,7 +306,7 @@ void store_thread(int slot, si_session* sess, uint32_t first_layer, uint32_t lay
         Layer& L = ls[l];
         for (uint32_t kind = 0; kind < 2; ++kind)
             for (size_t i = 0; i < n; ++i) {
-                const uint8_t* got = L.pool[kind].data() + uint64_t(L.map[2 * i + 1]) * rb;
+                const uint8_t* got = L.pool[kind]->data() + uint64_t(L.map[2 * i + 1]) * rb;
                 std::vector<uint8_t> want(rb);
                 const uint16_t* blk = L.cache[kind].data() + uint64_t(L.map[2 * i]) * kBlock / 2;
                 if (bits) si_or_codec_encode(blk, kHeads, kDim, bits, kind, first_layer + l, want.data());
@@ -322,8 +382,8 @@ void destroy_during_prefetch(int slot, uint32_t layer, uint32_t seed)
     std::mt19937 rng(seed);
     si_session* s = new_session(900 + seed);
     const size_t nhost = 16, n = 16;
-    auto k = host_pool(blocks(rng, nhost), nhost, 0, 0, layer);
-    auto v = host_pool(blocks(rng, nhost), nhost, 0, 1, layer);
+    auto& k = kept(host_pool(blocks(rng, nhost), nhost, 0, 0, layer));
+    auto& v = kept(host_pool(blocks(rng, nhost), nhost, 0, 1, layer));
     secure_infer_register_host_range_ex(k.data(), k.size(), layer, 0, kBlock);
     secure_infer_register_host_range_ex(v.data(), v.size(), layer, 1, kBlock);
     std::vector<int64_t> map(2 * n);
@@ -344,7 +404,7 @@ void destroy_refused_while_held(uint32_t layer, uint32_t seed)
 {
     std::mt19937 rng(seed);
     si_session* s = new_session(1700 + seed);
-    auto pool = host_pool(blocks(rng, 4), 4, 0, 0, layer);
+    auto& pool = kept(host_pool(blocks(rng, 4), 4, 0, 0, layer));
     secure_infer_register_host_range_ex(pool.data(), pool.size(), layer, 0, kBlock);
     std::vector<uint8_t> cache(4 * kBlock, 0);
     std::atomic<int> step{0};
@@ -411,11 +471,12 @@ int main(int argc, char** argv)
         const uint32_t base = 1000u * uint32_t(round + 1);
         for (int i = 0; i < kSlots; ++i) g_stage[i].store(nullptr);
         std::vector<std::thread> ts;
-        ts.emplace_back(reload_thread, 0, sess, base + 0, 8, 0u, 11u + round, true);
-        ts.emplace_back(reload_thread, 1, sess, base + 100, 8, 4u, 12u + round, false);
-        ts.emplace_back(reload_thread, 2, sess, base + 200, 6, 0u, 13u + round, false);
+        ts.emplace_back(reload_thread, 0, sess, base + 0, 8, 0u, 11u + round, true, false);
+        ts.emplace_back(reload_thread, 1, sess, base + 100, 8, 4u, 12u + round, false, false);
+        ts.emplace_back(reload_thread, 2, sess, base + 200, 6, 0u, 13u + round, false, false);
         ts.emplace_back(store_thread, 3, sess, base + 300, 5, 0u, 14u + round, false);
         ts.emplace_back(store_thread, 4, sess, base + 400, 4, 8u, 15u + round, false);
+        ts.emplace_back(reload_thread, 11, sess, base + 650, 8, 4u, 22u + round, false, true);
         ts.emplace_back(exit_inside_group, 5, sess, base + 600, 17u + round);
         ts.emplace_back(exit_inside_batch, 6, sess, base + 700, 18u + round);
         ts.emplace_back(destroy_during_prefetch, 7, base + 800, 19u + round);
@@ -423,7 +484,7 @@ int main(int argc, char** argv)
         // The D2H fault injection hits any record: the tampered store runs
         // with no other store in flight, beside more reloads.
         stage(10, "main: tampered store phase");
-        std::thread tr(reload_thread, 8, sess, base + 250, 4, 4u, 21u + round, false);
+        std::thread tr(reload_thread, 8, sess, base + 250, 8, 0u, 21u + round, true, true);
         store_thread(9, sess, base + 500, 3, 0u, 16u + round, true);
         tr.join();
         stage(10, "main: destroy_refused_while_held");

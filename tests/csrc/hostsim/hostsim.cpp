@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 #include <openssl/evp.h>
 
+#include <array>
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
@@ -440,6 +441,20 @@ void ctr(const uint8_t key[16], const uint8_t iv12[12], const uint8_t* in, size_
 
 bool gated(const uint32_t* gate) { return gate && __atomic_load_n(gate, __ATOMIC_SEQ_CST) == 0u; }
 
+// (layer, kind, block id, ticket) of every reload record, read from its AAD
+// (secure_infer_build_gcm_aad: kind at byte 6, layer BE32 at 8, block id BE64
+// at 12, ticket BE64 at 36), so the stress driver can check the order in
+// which tickets were assigned.
+std::mutex g_log_m;
+std::vector<std::array<uint64_t, 4>>& g_log = *new std::vector<std::array<uint64_t, 4>>();
+
+uint64_t be(const uint8_t* p, int n)
+{
+    uint64_t v = 0;
+    for (int i = 0; i < n; ++i) v = (v << 8) | p[i];
+    return v;
+}
+
 // Layer batches: 0 verify + decrypt (output zeroed on failure), 1 encrypt +
 // tag (a bad slot id gets the complement of its tag), 2 verify only.
 void layer_kernel(int mode, const GcmCtx* ctx, const RecBatch& b, const Sched& s)
@@ -459,6 +474,10 @@ void layer_kernel(int mode, const GcmCtx* ctx, const RecBatch& b, const Sched& s
                 if (b.fail_count) add_u32(b.fail_count, 1);
             }
             continue;
+        }
+        {
+            std::lock_guard<std::mutex> g(g_log_m);
+            g_log.push_back({be(v.aad + 8, 4), v.aad[6], be(v.aad + 12, 8), be(v.aad + 36, 8)});
         }
         uint8_t tag[16];
         memcpy(tag, v.tag, 16);
@@ -607,3 +626,28 @@ hipError_t launch_blake2b_test(hipStream_t, const uint8_t*, uint32_t, const uint
 }
 
 }  // namespace si
+
+// Takes the reload log of one layer out of the log (layer numbers come back
+// in later rounds): rows of (kind, block id, ticket); returns the count (at
+// most cap rows written).
+extern "C" size_t hostsim_reload_log(uint32_t layer, uint64_t* out, size_t cap)
+{
+    std::lock_guard<std::mutex> g(si::g_log_m);
+    size_t n = 0;
+    auto keep = si::g_log.begin();
+    for (auto it = si::g_log.begin(); it != si::g_log.end(); ++it) {
+        const auto e = *it;
+        if (e[0] != layer) {
+            *keep++ = e;
+            continue;
+        }
+        if (n < cap) {
+            out[3 * n] = e[1];
+            out[3 * n + 1] = e[2];
+            out[3 * n + 2] = e[3];
+        }
+        ++n;
+    }
+    si::g_log.erase(keep, si::g_log.end());
+    return n;
+}

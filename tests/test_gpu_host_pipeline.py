@@ -607,6 +607,110 @@ def test_group_prefetch_tamper_is_retried():
         si.clear_host_ranges()
 
 
+def _codec_layers(rng, nlayers, ncpu, heads, dim, bits):
+    """Per layer, host packet pools [ncpu, width] (uint8) encoded by the
+    oracle codec from random bf16 blocks, and those blocks."""
+    out = []
+    for layer in range(nlayers):
+        blocks = [W.bf16_blocks(rng, ncpu, heads, dim) for _ in range(2)]
+        packets = [torch.from_numpy(np.stack([O.codec_encode(blocks[k][i], bits, k, layer)
+                                              for i in range(ncpu)])).contiguous() for k in range(2)]
+        si.register_host_range(packets[0], layer, 0)
+        si.register_host_range(packets[1], layer, 1)
+        out.append((packets, blocks))
+    return out
+
+
+@pytest.mark.parametrize("bits", [0, 4])
+@pytest.mark.parametrize("ahead", [True, False], ids=["sealed_ahead", "on_demand"])
+def test_merged_layer_launch(bits, ahead):
+    """merge_groups: a 41-block layer in 16-block causal groups goes to the
+    device as one launch (one layer group around the groups' swaps, K1 V1 K2
+    V2 K3 V3; sealed ahead it is one layer prefetch and one DMA).  Each layer
+    spends exactly 2 x 41 tickets, every swap is served by the prefetch when
+    sealed ahead, and the caches end bit-exact (bf16), or equal to the oracle
+    codec's decode of the packets (int4).  The order the tickets follow is
+    pinned on the CPU by the host runtime's sanitizer stress test, which logs
+    every record's AAD."""
+    rng = np.random.default_rng(150 + bits + int(ahead))
+    heads, dim, ncpu, nslots, nlayers = 2, 128, 41, 64, 3
+    shape = si.LayerShape(heads, dim, bits)
+    sess = si.GcmSession(KEY, SALT, 10 + bits, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        if bits:
+            layers = _codec_layers(rng, nlayers, ncpu, heads, dim, bits)
+            host_layers = [packets for packets, _ in layers]
+        else:
+            host_layers = _layers(rng, nlayers, ncpu, heads, dim)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16, pipeline_seal=ahead, merge_groups=True)
+        slot_ids = rng.permutation(nslots)[:ncpu]
+        mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
+        before = si.transfer_prefetch_stats()
+        caches_l = [caches(nslots, heads, dim) for _ in range(nlayers)]
+        for layer in range(nlayers):
+            t0 = si.new_transfer_ticket()
+            nt.single_layer_kv_transfer((host_layers[layer], mapping), caches_l[layer])
+            assert si.new_transfer_ticket() == t0 + 2 * ncpu + 1
+        after = si.transfer_prefetch_stats()
+        served = (after["ready"] - before["ready"]) + (after["busy_fallback"] - before["busy_fallback"])
+        missing = after["missing_fallback"] - before["missing_fallback"]
+        assert (served, missing) == ((nlayers * 6, 0) if ahead else (0, nlayers * 6))
+        assert int(_lib.load().secure_infer_count_ready_unconsumed_gcm_tickets()) == 0
+        idx = torch.from_numpy(slot_ids.astype(np.int64)).to(DEV)
+        for layer in range(nlayers):
+            assert nt.wait_layer(layer) == 0
+            ck, cv = caches_l[layer]
+            got = [ck.index_select(0, idx).cpu().numpy(), cv.index_select(0, idx).cpu().numpy()]
+            for k in range(2):
+                if bits:
+                    packets = host_layers[layer][k].numpy()
+                    for i in range(ncpu):
+                        assert np.array_equal(got[k][i].view(np.uint16),
+                                              O.codec_decode(packets[i], heads, dim, bits, k)), (layer, k, i)
+                else:
+                    assert np.array_equal(got[k], host_layers[layer][k].numpy()), (layer, k)
+            untouched = np.setdiff1d(np.arange(nslots), slot_ids)
+            assert (host(ck)[untouched].view(np.uint8) == 0x3C).all()
+    finally:
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()
+
+
+@pytest.mark.parametrize("shots", [1, 2], ids=["repaired", "final"])
+def test_merged_layer_tamper(shots):
+    """A V record of the middle causal group of a merged, sealed-ahead layer
+    corrupted once is re-sealed by the strict retry and the layer
+    authenticates; corrupted twice, the layer fails, that slot reads as
+    zeros, and every other slot is still bit-exact."""
+    rng = np.random.default_rng(160 + shots)
+    heads, dim, ncpu, nslots, layer = 2, 128, 41, 48, 0
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 20 + shots, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        (hk, hv), = _layers(rng, 1, ncpu, heads, dim)
+        slot_ids = rng.permutation(nslots)[:ncpu]
+        mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
+        victim = 17  # in the group [9, 25)
+        si.inject_h2d_tamper(layer=layer, kind=1, host_block=victim, shots=shots)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16, merge_groups=True)
+        ck, cv = caches(nslots, heads, dim)
+        nt.single_layer_kv_transfer(((hk, hv), mapping), (ck, cv))
+        assert nt.wait_layer(layer) == (0 if shots == 1 else -1)
+        kk, vv = host(ck), host(cv)
+        for c, sl in enumerate(slot_ids):
+            assert np.array_equal(kk[sl], hk[c].numpy())
+            if shots == 2 and c == victim:
+                assert (vv[sl] == 0).all()
+            else:
+                assert np.array_equal(vv[sl], hv[c].numpy()), c
+    finally:
+        si.inject_h2d_tamper(shots=0)
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()
+
+
 def test_job_authentication_spans_layers():
     """secure_infer_recovery_wait_job_authentication (secure_infer.cpp:7336-7372):
     every record of the job on every layer, no retry; 1 / 0 / -1."""
@@ -656,6 +760,47 @@ assert nt.wait_layer(0) == 0 and nt.wait_layer(1) == 0
 si.drain_h2d_profile_after_job()
 print("done")
 """
+
+
+MERGED_LEDGER_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import secure_infer_amd as si
+heads, dim, n = 2, 128, 41
+shape = si.LayerShape(heads, dim)
+sess = si.GcmSession(bytes(16), b"abcd", 0, max_record_bytes=shape.record_bytes)
+hk = torch.zeros((n, 128, heads, dim), dtype=torch.int16)
+hv = torch.ones((n, 128, heads, dim), dtype=torch.int16)
+ck = torch.zeros((64, 128, heads, dim), dtype=torch.int16, device="cuda")
+cv = torch.zeros_like(ck)
+m = torch.stack((torch.arange(n), torch.arange(n) + 20), 1).to(torch.int64).contiguous()
+ahead = si.NativeTransfer(sess, shape, causal_group_blocks=16, merge_groups=True)
+ahead.single_layer_kv_transfer(((hk, hv), m), (ck, cv))
+late = si.NativeTransfer(sess, shape, causal_group_blocks=16, merge_groups=True, pipeline_seal=False)
+late.layer = 1
+late.single_layer_kv_transfer(((hk, hv), m), (ck, cv))
+assert ahead.wait_layer(0) == 0 and late.wait_layer(1) == 0
+assert torch.equal(cv[20:20 + n].cpu(), hv) and torch.equal(ck[20:20 + n].cpu(), hk)
+si.drain_h2d_profile_after_job()
+print("done")
+"""
+
+
+def test_merged_layer_is_one_launch(tmp_path):
+    """With merge_groups a 41-block layer in three causal groups is one row
+    of the H2D ledger (one launch of 82 records), sealed ahead or on demand."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    csv = tmp_path / "h2d.csv"
+    env = dict(os.environ, SECURE_INFER_H2D_PROFILE=str(csv))
+    out = subprocess.run([sys.executable, "-c", MERGED_LEDGER_SCRIPT, str(Path(__file__).resolve().parent.parent)],
+                         env=env, capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0 and "done" in out.stdout, out.stderr[-2000:]
+    rows = [l.split(",") for l in csv.read_text().strip().splitlines()[1:]]
+    src = sorted((r[0], r[1], r[2], r[4].replace("prefetch_waited", "prefetched")) for r in rows)
+    assert src == [("0", "2", "82", "prefetched"), ("1", "2", "82", "sealed")]
 
 
 def test_h2d_profile_ledger(tmp_path):

@@ -9,7 +9,9 @@ the allocation-free entry's scratch ownership).  tests/csrc/hostsim/host_stress.
 then drives, concurrently: reload threads on their own streams through layer
 groups (sealed on demand and ahead of demand, a record corrupted once and
 repaired by the strict retry, one corrupted twice whose layer fails and whose
-slot reads as zeros, bf16 and int4), D2H store batches spanning layers (bf16
+slot reads as zeros, bf16 and int4; a layer's causal groups merged into one
+launch, sealed on demand or as one layer prefetch, with the tickets checked to
+rise in the reference's K1 V1 K2 V2 order), D2H store batches spanning layers (bf16
 and int8, batch_end racing the pool's verification, a corrupted record that
 fails its batch), threads that end inside a layer group and inside a D2H
 batch, a session destroyed while its prefetches are still being sealed, and a

@@ -73,16 +73,26 @@ class Recorder:
         return self.secure_infer_h2d_prefetch(sess, v_base, host_block_bytes, host_nblocks, mapping_ptr, n, 1,
                                               layer, bits, heads, dim)
 
+    def secure_infer_h2d_prefetch_layer(self, sess, k_base, v_base, host_block_bytes, host_nblocks, mapping_ptr,
+                                        starts, rows, ngroups, layer, bits, heads, dim):
+        import ctypes as ct
+        groups = []
+        for g in range(ngroups):
+            arr = (ct.c_int64 * (2 * rows[g])).from_address(mapping_ptr.value + 16 * starts[g])
+            groups.append((starts[g], [(arr[2 * i], arr[2 * i + 1]) for i in range(rows[g])]))
+        self.calls.append(("prefetch_layer", layer, bits, groups))
+        return 0
+
 
 def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False,
-                 pipeline_seal=True, stripe=False):
+                 pipeline_seal=True, stripe=False, merge_groups=False):
     rec = Recorder()
     parent = FakeStream("parent")
     shape = shape or si.LayerShape(2, 64)
     sess = mock.Mock()
     sess._h = None
     nt = si.NativeTransfer(sess, shape, streams=streams or None, causal_group_blocks=group,
-                           pipeline_seal=pipeline_seal, stripe=stripe)
+                           pipeline_seal=pipeline_seal, stripe=stripe, merge_groups=merge_groups)
     nt.layer = layer
     host = [torch.zeros((nblocks, 4), dtype=torch.int16), torch.zeros((nblocks, 4), dtype=torch.int16)]
     dest = [torch.zeros((nslots or nblocks + 100, 4), dtype=torch.int16) for _ in range(2)]
@@ -210,3 +220,31 @@ def test_layer_seals_are_queued_in_swap_order():
 def test_unpipelined_layers_are_sealed_on_demand():
     _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True, pipeline_seal=False)
     assert not [c for c in rec.calls if c[0] == "prefetch"]
+
+
+def test_merged_groups_keep_the_swaps_and_their_order():
+    """merge_groups: one layer group of 2 * 41 records around the same swaps,
+    in the same order (so the same tickets) as one group per causal group;
+    the layer is sealed ahead as one layer prefetch naming every group (tail
+    first) before the first swap."""
+    _, rec_g, _ = run_transfer(41, 16, None, layer=3)
+    _, rec, _ = run_transfer(41, 16, None, layer=3, keep_prefetch=True, merge_groups=True)
+    swaps = [c for c in rec.calls if c[0] == "swap"]
+    assert [c[2:] for c in swaps] == [c[2:] for c in rec_g.calls if c[0] == "swap"]  # stream handles differ
+    kinds = [c[0] if c[0] != "swap" else ("K", "V")[c[2]] for c in rec.calls if not c[0].startswith("prefetch")]
+    assert kinds == ["begin"] + ["K", "V"] * 3 + ["end"]
+    assert [c[1] for c in rec.calls if c[0] == "begin"] == [82]
+    order = [(c[2], h) for c in swaps for h, _ in c[5]]
+    assert order == gcm.reference_ticket_order(41, 16)
+    pre = [c for c in rec.calls if c[0].startswith("prefetch")]
+    assert len(pre) == 1 and pre[0][0] == "prefetch_layer" and pre[0][1:3] == (3, 0)
+    groups = pre[0][3]
+    assert [(start, len(pairs)) for start, pairs in groups] == [(25, 16), (9, 16), (0, 9)]
+    assert [p for _, pairs in groups for p in pairs] == [p for c in swaps if c[2] == 0 for p in c[5]]
+    assert rec.calls.index(pre[0]) < next(i for i, c in enumerate(rec.calls) if c[0] == "swap")
+
+
+def test_merged_single_group_is_a_group_prefetch():
+    _, rec, _ = run_transfer(10, 16, None, keep_prefetch=True, merge_groups=True)
+    assert [c[0] for c in rec.calls if c[0].startswith("prefetch")] == [
+        "prefetch", "prefetch_group_pairs_with_previous", "prefetch"]
