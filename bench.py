@@ -15,8 +15,9 @@ Prints ONE JSON line.  `value` is GB/s of algorithmic bytes over the timed
 region (reload, per record: ciphertext read + bf16 write + tag + AAD + status;
 writeback: bf16 read + ciphertext write + tag + AAD).  `roofline.achieved` is
 the same bytes over `roofline.kernel_us`, the median kernel time of one
-layer's launch sequence measured in this run (HIP events around each launch
-of one more pass after the timed region).  `roofline.traffic` and `issue`
+layer's launch sequence measured in this run (one more back-to-back pass
+after the timed region whose kernels stamp the device clock at the start and
+end of every wave).  `roofline.traffic` and `issue`
 (VALU / LDS issue fractions of the GCM kernel) come from the committed
 rocprofv3 counter summaries under profiles/.
 """
@@ -58,6 +59,43 @@ DEFAULT = "reload_bf16_llama3_8b_6144tok"
 # RUNTIME_LOAD_CHUNK of the reference's reuse connectors (connector.py:21, 288):
 # a layer's reload is submitted in groups of 2048 / 128 = 16 blocks, tail first.
 LOAD_CHUNK_BLOCKS = 2048 // 128
+
+
+class Range:
+    """A named ROCTx range (rocprofiler-sdk's roctx library) around one part
+    of the run -- a workload, its timed region, its per-launch kernel pass --
+    so that a kernel trace of this same command taken with --marker-trace
+    splits per workload and phase.  Costs a library call per range; does
+    nothing where the library is absent."""
+    _fns = None
+
+    def __init__(self, name: str):
+        self.name = name.encode()
+
+    @classmethod
+    def _load(cls):
+        if cls._fns is None:
+            import ctypes as ct
+            try:
+                lib = ct.CDLL("librocprofiler-sdk-roctx.so.1")
+                lib.roctxRangePushA.argtypes, lib.roctxRangePushA.restype = [ct.c_char_p], ct.c_int
+                lib.roctxRangePop.argtypes, lib.roctxRangePop.restype = [], ct.c_int
+                cls._fns = (lib.roctxRangePushA, lib.roctxRangePop)
+            except (OSError, AttributeError):
+                cls._fns = ()
+        return cls._fns
+
+    def __enter__(self):
+        fns = self._load()
+        if fns:
+            fns[0](self.name)
+        return self
+
+    def __exit__(self, *exc):
+        fns = self._load()
+        if fns:
+            fns[1]()
+        return False
 
 
 def aad_bytes(direction: int, kind: int, layer: int, block_id: int, nbytes: int, ticket: int) -> bytes:
@@ -486,24 +524,70 @@ def run_workload(name: str, args, torch, si, steps: int, warmup: int, with_cpu: 
             step(layer)
     torch.cuda.synchronize()
     fails.zero_()
+    # Clock stamps of the kernel pass that follows the timed region (made
+    # now, so that the pass starts as soon as the region ends).
+    import ctypes as ct
+    lib = si._lib.load()
+    words = 1 << 17  # per layer: two words per wave of its kernels
+    stamps = torch.empty((L, words), dtype=torch.int64, device=dev)
+    stamps[:, 0::2] = torch.iinfo(torch.int64).max
+    stamps[:, 1::2] = 0
+    khz = ct.c_uint64()
+    if lib.secure_infer_gpu_clock_rate_khz(ct.byref(khz)) != 0:
+        raise RuntimeError("secure_infer_gpu_clock_rate_khz failed")
+
     # Timed region: K steps of one launch per layer on one stream, nothing
     # else queued; the average launch duration is the region over K*L.
     stream = torch.cuda.current_stream()
     t_start, t_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t_start.record(stream)
-    for _ in range(steps):
-        for layer in range(L):
-            step(layer)
-    t_stop.record(stream)
-    torch.cuda.synchronize()
+    with Range(f"timed:{name}"):
+        t_start.record(stream)
+        for _ in range(steps):
+            for layer in range(L):
+                step(layer)
+        t_stop.record(stream)
+        torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_stop)
     ms_per_step = total_ms / steps
     us_launch = total_ms * 1e3 / (steps * L)
 
+    # The kernel time per launch, measured in this run: one more pass of the
+    # same prepared launches right after the timed region (at the clocks the
+    # region's sustained load has reached; the correctness checks come after
+    # it, on the failure counts the region left), back to back as in the
+    # region (same results: reloads rewrite the same plaintext, writebacks the
+    # same ciphertext).  Every wave of each layer's kernels writes the
+    # device's constant-rate clock when it starts and when it ends
+    # (secure_infer_gpu_clock_next_layers, armed once for all layers so the
+    # host issues exactly the timed region's calls); a layer's kernel time is
+    # its last wave end minus its first wave start.  (HIP events recorded by
+    # the launch itself, hipExtLaunchKernel, lengthened each launch they timed
+    # by 3-4 us in a kernel trace; arming layer by layer left host gaps of
+    # ~9 us, after which a kernel ran ~3 us longer.)  roofline.frac derives
+    # from the median; `value` and us_per_layer stay the timed region's
+    # figures.
+    fails_timed = fails.clone()
+    torch.cuda.synchronize()
+    if lib.secure_infer_gpu_clock_next_layers(ct.c_void_p(stamps.data_ptr()), words, L) != 0:
+        raise RuntimeError("secure_infer_gpu_clock_next_layers failed")
+    with Range(f"kernel_pass:{name}"):
+        for layer in range(L):
+            step(layer)
+        torch.cuda.synchronize()
+    used_c = (ct.c_uint64 * L)()
+    if lib.secure_infer_gpu_clock_layers_used(used_c, L) != 0:
+        raise RuntimeError("a kernel's clock stamps did not fit")
+    used = list(used_c)
+    if len(set(used)) != 1 or used[0] == 0:
+        raise RuntimeError(f"clocked layers took different stamp counts: {sorted(set(used))}")
+    starts, ends = stamps[:, 0:used[0]:2], stamps[:, 1:used[0]:2]
+    if bool((starts == torch.iinfo(torch.int64).max).any()) or bool((ends == 0).any()):
+        raise RuntimeError("a wave of a clocked layer wrote no stamp")
+
     # correctness of what was timed: every layer on the device (bf16 reload),
     # sampled layers against the oracle (every workload)
-    nfail = int(fails.sum().item()) if op == "reload" else 0
+    nfail = int(fails_timed.sum().item()) if op == "reload" else 0
     exact = True
     if op == "reload" and bits == 0:
         got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
@@ -518,28 +602,8 @@ def run_workload(name: str, args, torch, si, steps: int, warmup: int, with_cpu: 
         zeroed = all(bool((cache[l, r // NB, slots[l, r % NB]] == 0).all()) for l, r in tampered)
         tamper_ok = nfail == len(tampered) * steps and zeroed
 
-    # The kernel time per launch, measured in this run: one more pass of the
-    # same prepared launches after the timed region (same results: reloads
-    # rewrite the same plaintext, writebacks the same ciphertext), each
-    # layer's launch sequence timed by HIP events that its first and last
-    # kernels record at their own dispatch start and end
-    # (secure_infer_gpu_time_next_layer: hipExtLaunchKernel events, the
-    # interval a kernel trace reports; events recorded between the launches
-    # would also count a launch gap each).  roofline.frac derives from the
-    # median; `value` and us_per_layer stay the timed region's figures.
-    lib = si._lib.load()
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
-    for a, b in pairs:  # torch creates its events at their first record
-        a.record(stream)
-        b.record(stream)
-    torch.cuda.synchronize()
-    for layer in range(L):
-        a, b = pairs[layer]
-        if lib.secure_infer_gpu_time_next_layer(a.cuda_event, b.cuda_event) != 0:
-            raise RuntimeError("secure_infer_gpu_time_next_layer failed")
-        step(layer)
-    torch.cuda.synchronize()
-    per_launch_us = np.array([a.elapsed_time(b) * 1e3 for a, b in pairs])
+    ticks = (ends.max(1).values - starts.min(1).values).cpu().numpy()
+    per_launch_us = ticks.astype(np.float64) * 1e3 / khz.value
     kernel_us = float(np.median(per_launch_us))
 
     algo_layer = nrec * algorithmic_bytes_per_record(op, nbytes, block_bytes)
@@ -579,9 +643,10 @@ def run_workload(name: str, args, torch, si, steps: int, warmup: int, with_cpu: 
                      "traffic": load_traffic(name),
                      "kernel_us": round(kernel_us, 3),
                      "kernel_us_range": [round(float(per_launch_us.min()), 3), round(float(per_launch_us.max()), 3)],
-                     "kernel_us_source": (f"median over {L} layers of one pass after the timed region: HIP events "
-                                          "at the dispatch start of each layer's first kernel and the end of its "
-                                          "last (hipExtLaunchKernel)"),
+                     "kernel_us_source": (f"median over {L} layers of one back-to-back pass after the timed region: "
+                                          "per layer, the device clock (wall_clock64, "
+                                          f"{khz.value // 1000} MHz) at the end of its kernels' last wave minus "
+                                          "the start of their first"),
                      "region_us_per_launch": round(us_launch, 3)},
         "issue": load_issue(name),
     }
@@ -606,9 +671,10 @@ def run_workload(name: str, args, torch, si, steps: int, warmup: int, with_cpu: 
             # read by the library at the first H2D swap, which comes later
             import tempfile
             os.environ["SECURE_INFER_H2D_PROFILE"] = os.path.join(tempfile.mkdtemp(), "h2d_ledger.csv")
-        res["end_to_end"] = end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer,
-                                       e2e_steps, truth if (op == "reload" and bits == 0) else None,
-                                       max(1, min(args.slice_streams, 8)), args.stripe)
+        with Range(f"end_to_end:{name}"):
+            res["end_to_end"] = end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo_layer,
+                                           e2e_steps, truth if (op == "reload" and bits == 0) else None,
+                                           max(1, min(args.slice_streams, 8)), args.stripe)
     return res
 
 
@@ -661,8 +727,10 @@ def main():
                           "copy_read_plus_write_GB_s": round(2 * n / dt / 1e9, 1)}), flush=True)
         return
 
-    res = run_workload(args.config, args, torch, si, args.steps, args.warmup, not args.no_cpu, args.cpu_budget,
-                       args.e2e_steps)
+    with Range(f"workload:{args.config}"):
+        res = run_workload(args.config, args, torch, si, args.steps, args.warmup, not args.no_cpu,
+                           args.cpu_budget, args.e2e_steps)
+    print(f"[bench] {args.config}: {res['us_per_layer']} us/layer", file=sys.stderr, flush=True)
     if args.config == DEFAULT and not args.single:
         # The other workloads in the same run, so one driver run times all of
         # them: same device measurement and checks, a short CPU leg, no
@@ -671,8 +739,10 @@ def main():
         for name in sorted(CONFIGS):
             if name == DEFAULT:
                 continue
-            r = run_workload(name, args, torch, si, min(args.steps, 10), min(args.warmup, 2), not args.no_cpu,
-                             min(args.cpu_budget, 2.0), 0)
+            with Range(f"workload:{name}"):
+                r = run_workload(name, args, torch, si, min(args.steps, 10), min(args.warmup, 2), not args.no_cpu,
+                                 min(args.cpu_budget, 2.0), 0)
+            print(f"[bench] {name}: {r['us_per_layer']} us/layer", file=sys.stderr, flush=True)
             others[name] = {k: r[k] for k in ("us_per_layer", "value", "hbm_frac", "ms_per_step", "steps", "warmup",
                                               "bit_exact", "bit_exact_checked", "tamper_fail_closed",
                                               "failed_records_per_step")}

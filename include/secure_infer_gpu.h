@@ -278,6 +278,31 @@ int secure_infer_gpu_reload_layer_noalloc(hipStream_t stream, si_session* sessio
  * if both are NULL. */
 int secure_infer_gpu_time_next_layer(hipEvent_t start, hipEvent_t stop);
 
+/* Kernel clock of the calling thread's next `layers` layer calls (no
+ * reference counterpart, as above): lane 0 of every wave of the kernels of
+ * each of the next `layers` secure_infer_gpu_reload_layer,
+ * _reload_layer_noalloc or _writeback_layer calls writes the device's
+ * constant-rate clock (wall_clock64; rate from
+ * secure_infer_gpu_clock_rate_khz) when the wave starts and when it ends
+ * into `stamps` (device memory): layer call l (in call order) takes words
+ * [l * words_per_layer, (l + 1) * words_per_layer), two per wave (start,
+ * end), its kernels one after another.  A layer's kernel time is the latest
+ * end minus the earliest start of the words it wrote.  Unlike the events
+ * above it adds nothing to the launches (a hipExtLaunchKernel event pair
+ * lengthens each launch it times), and arming every layer at once leaves the
+ * calls back to back.  Words a launch does not reach keep their contents;
+ * arming again drops what was armed.  0, or -1 on NULL / 0 / overflow. */
+int secure_infer_gpu_clock_next_layers(uint64_t* stamps, uint64_t words_per_layer, uint32_t layers);
+
+/* Words each of the first `layers` clocked calls wrote, into words_used[l]
+ * (may be NULL); -1 if fewer calls were clocked since the arming, or a
+ * kernel of one of them did not fit in words_per_layer (that kernel wrote no
+ * stamps). */
+int secure_infer_gpu_clock_layers_used(uint64_t* words_used, uint32_t layers);
+
+/* Rate of that clock on the current device, in kHz.  0, or -1. */
+int secure_infer_gpu_clock_rate_khz(uint64_t* khz);
+
 /* One layer of writeback: record r gathers cache[kind] + slots[r]*slot_bytes,
  * optionally quantises it with the transport codec, encrypts it and writes the
  * ciphertext and tag into its wire record (the AAD must already be there).

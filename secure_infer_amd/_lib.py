@@ -63,6 +63,9 @@ SIGNATURES = {
     "secure_infer_gpu_reload_layer_noalloc": ([_v, _v, ct.POINTER(SiReloadDesc)], _i),
     "secure_infer_gpu_writeback_layer": ([_v, _v, ct.POINTER(SiWritebackDesc)], _i),
     "secure_infer_gpu_time_next_layer": ([_v, _v], _i),
+    "secure_infer_gpu_clock_next_layers": ([_v, _u64, _u32], _i),
+    "secure_infer_gpu_clock_layers_used": ([_v, _u32], _i),
+    "secure_infer_gpu_clock_rate_khz": ([_v], _i),
     "secure_infer_codec_width": ([_u32, _u32, _u32], _u64),
     "secure_infer_wire_stride": ([_u64], _u64),
     "secure_infer_new_transfer_ticket": ([], _u64),

@@ -1036,11 +1036,18 @@ static int reload_checks(const si_session* s, const si_reload_desc* d, const voi
 // Events armed by secure_infer_gpu_time_next_layer for the calling thread's
 // next layer launch (one shot).
 thread_local si::LaunchEvents t_layer_events;
+// Clock probes armed by secure_infer_gpu_clock_next_layers for the calling
+// thread's next layer launches, one per layer in launch order; each keeps the
+// words its launch used and its overflow flag for
+// secure_infer_gpu_clock_layers_used.
+thread_local std::vector<si::ClockProbe> t_clock_layers;
+thread_local size_t t_clock_next = 0;
 
 static si::LaunchEvents take_layer_events()
 {
-    const si::LaunchEvents ev = t_layer_events;
+    si::LaunchEvents ev = t_layer_events;
     t_layer_events = si::LaunchEvents();
+    if (t_clock_next < t_clock_layers.size()) ev.clock = &t_clock_layers[t_clock_next++];
     return ev;
 }
 
@@ -1091,6 +1098,7 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
     // A timed layer: start at the first kernel, stop at the layer's last kernel.
     const si::LaunchEvents ev = take_layer_events();
     si::LaunchEvents ev_rec = ev, ev_rel, ev_dq;
+    ev_rel.clock = ev_dq.clock = ev.clock;
     if (strict) {
         ev_rec.stop = nullptr;
         ev_rel.stop = codec ? nullptr : ev.stop;
@@ -1212,6 +1220,38 @@ int secure_infer_gpu_time_next_layer(hipEvent_t start, hipEvent_t stop)
     return 0;
 }
 
+int secure_infer_gpu_clock_next_layers(uint64_t* stamps, uint64_t words_per_layer, uint32_t layers)
+{
+    if (!stamps || words_per_layer == 0 || layers == 0 || words_per_layer > UINT64_MAX / layers) return -1;
+    t_clock_layers.assign(layers, si::ClockProbe());
+    for (uint32_t l = 0; l < layers; ++l) {
+        t_clock_layers[l].stamps = stamps + uint64_t(l) * words_per_layer;
+        t_clock_layers[l].words = words_per_layer;
+    }
+    t_clock_next = 0;
+    return 0;
+}
+
+int secure_infer_gpu_clock_layers_used(uint64_t* words_used, uint32_t layers)
+{
+    if (layers == 0 || layers > t_clock_next) return -1;
+    for (uint32_t l = 0; l < layers; ++l) {
+        if (t_clock_layers[l].overflow) return -1;
+        if (words_used) words_used[l] = t_clock_layers[l].used;
+    }
+    return 0;
+}
+
+int secure_infer_gpu_clock_rate_khz(uint64_t* khz)
+{
+    int dev = 0, rate = 0;
+    if (!khz || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, dev) != hipSuccess || rate <= 0)
+        return -1;
+    *khz = uint64_t(rate);
+    return 0;
+}
+
 int secure_infer_test_strict_phases(int n)
 {
     if (n < 0) return -1;
@@ -1260,6 +1300,7 @@ int secure_infer_gpu_writeback_layer(hipStream_t stream, si_session* s, const si
     // A timed layer: start at the layer's first kernel, stop at the record kernel.
     const si::LaunchEvents ev = take_layer_events();
     si::LaunchEvents ev_q, ev_rec = ev;
+    ev_q.clock = ev.clock;
     if (codec) {
         ev_q.start = ev.start;
         ev_rec.start = nullptr;

@@ -18,6 +18,7 @@
 // gives the bf16 NaN 0x7fc0.  The bit patterns of NaN parameters are not
 // specified.
 #include "si_codec_math.h"
+#include "si_clock.h"
 #include "si_kernels.h"
 
 namespace si {
@@ -66,7 +67,7 @@ __device__ __forceinline__ float nonfinite(float x)
 // row of 16 elements shares one (t, h, dim-group) pair.  Per token the thread
 // reads 16 (int8) or 8 (int4) packet bytes and writes 32 bytes of bf16, and a
 // wave covers 1 KiB of consecutive packet columns.
-__global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint32_t tpt)
+__device__ __forceinline__ void dequant_scatter_body(const CodecBatch& b, uint32_t tpt)
 {
     // An allocation-free call that does not own the GPU's scratch (whose
     // staging this reads) touches nothing; its records are failed closed
@@ -148,6 +149,13 @@ __global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint
         dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
         dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
     }
+}
+
+__global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint32_t tpt)
+{
+    clock_stamp(b.clock, 0);
+    dequant_scatter_body(b, tpt);
+    clock_stamp(b.clock, 1);
 }
 
 // Another lane's value by a DPP move: 0xb1 swaps lanes 2i / 2i+1, 0x4e swaps
@@ -439,6 +447,7 @@ __device__ __forceinline__ void quant_v_block(const CodecBatch& b, uint32_t r, u
 template <uint32_t kBits>
 __global__ __launch_bounds__(256) void quant_kernel(CodecBatch b, uint32_t kx, uint32_t vx)
 {
+    clock_stamp(b.clock, 0);
     const uint32_t nkb = kx * b.n_k;
     if (blockIdx.x < nkb) {
         quant_k_block<kBits>(b, blockIdx.x / kx, blockIdx.x % kx);
@@ -446,6 +455,7 @@ __global__ __launch_bounds__(256) void quant_kernel(CodecBatch b, uint32_t kx, u
         const uint32_t v = blockIdx.x - nkb;
         quant_v_block<kBits>(b, b.n_k + v / vx, v % vx);
     }
+    clock_stamp(b.clock, 1);
 }
 
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev)
@@ -460,10 +470,12 @@ hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b, const
     while (tpt > 1 && wg1 / tpt < 1024u) tpt >>= 1;
     const uint32_t per_rec = (128u / tpt) * (b.heads * b.dim / 16u);
     const dim3 grid((per_rec + 255u) / 256u, b.nrec);
+    CodecBatch bb = b;
+    bb.clock = ev.clock ? ev.clock->take(uint64_t(grid.x) * grid.y * 4u) : nullptr;
     if (ev.start || ev.stop)
-        hipExtLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, b, tpt);
+        hipExtLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, bb, tpt);
     else
-        hipLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, b, tpt);
+        hipLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, bb, tpt);
     return hipGetLastError();
 }
 
@@ -474,15 +486,17 @@ hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b, const La
     const uint32_t kx = (2u * hd + 255u) / 256u, vx = (4u * hd + 255u) / 256u;
     if (b.n_k + nv) {
         const dim3 grid(kx * b.n_k + vx * nv);
+        CodecBatch bb = b;
+        bb.clock = ev.clock ? ev.clock->take(uint64_t(grid.x) * 4u) : nullptr;
         if (ev.start || ev.stop) {
-            if (b.bits == 8)
-                hipExtLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, b, kx, vx);
+            if (bb.bits == 8)
+                hipExtLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, bb, kx, vx);
             else
-                hipExtLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, b, kx, vx);
-        } else if (b.bits == 8) {
-            hipLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, b, kx, vx);
+                hipExtLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, bb, kx, vx);
+        } else if (bb.bits == 8) {
+            hipLaunchKernelGGL(quant_kernel<8>, grid, dim3(256), 0, stream, bb, kx, vx);
         } else {
-            hipLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, b, kx, vx);
+            hipLaunchKernelGGL(quant_kernel<4>, grid, dim3(256), 0, stream, bb, kx, vx);
         }
     }
     return hipGetLastError();

@@ -30,6 +30,7 @@
 #include <mutex>
 
 #include "si_device.h"
+#include "si_clock.h"
 #include "si_kernels.h"
 
 namespace si {
@@ -611,9 +612,8 @@ __device__ __forceinline__ RecView get_view(const uint4* src)
 //      accumulator and add the segment's rows to its row count; the
 //      workgroup that completes R rows finalises the record.
 template <int kMode, bool kAligned, bool kWT>
-__global__ __launch_bounds__(SI_NT) __attribute__((amdgpu_waves_per_eu(SI_U, SI_U)))
-void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sch,
-                        RecAcc* __restrict__ acc)
+__device__ __forceinline__ void gcm_records_body(const GcmCtx* __restrict__ ctx, const RecBatch& batch,
+                                                 const Sched& sch, RecAcc* __restrict__ acc)
 {
     // 160 KiB, in 16-byte words.  During the rows:
     //   [0, 1024)      H^UT, H^2UT tables (row steps; below 64 KiB, so every
@@ -898,6 +898,16 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
     }
 }
 
+template <int kMode, bool kAligned, bool kWT>
+__global__ __launch_bounds__(SI_NT) __attribute__((amdgpu_waves_per_eu(SI_U, SI_U)))
+void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sch,
+                        RecAcc* __restrict__ acc)
+{
+    clock_stamp(sch.clock, 0);
+    gcm_records_body<kMode, kAligned, kWT>(ctx, batch, sch, acc);
+    clock_stamp(sch.clock, 1);
+}
+
 // Verify-before-release, second launch: record r (grid y) was verified by a
 // MODE_VERIFY launch that wrote its status word; workgroup x decrypts blocks
 // [x*chunk, (x+1)*chunk) of it into its destination (slot, or the codec
@@ -907,9 +917,8 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
 // A slot id out of range with no staging touches nothing.  Threads take
 // blocks 256 apart, so the counter-mode cache of rounds 1-2 applies while
 // counter bytes 12..13 stay fixed over the workgroup's range.
-__global__ __launch_bounds__(SI_RELEASE_THREADS) void release_kernel(const GcmCtx* __restrict__ ctx, RecBatch b,
-                                                                     uint64_t bytes, uint32_t chunk, int aligned,
-                                                                     const uint32_t* gate)
+__device__ __forceinline__ void release_body(const GcmCtx* __restrict__ ctx, const RecBatch& b, uint64_t bytes,
+                                             uint32_t chunk, int aligned, const uint32_t* gate)
 {
     __shared__ uint32_t s_aes[256 * 64];
     if (gate && *gmem(gate) == 0u) return;
@@ -955,6 +964,15 @@ __global__ __launch_bounds__(SI_RELEASE_THREADS) void release_kernel(const GcmCt
             else store_block<false>(v.dst + 16 * k, valid, o);
         }
     }
+}
+
+__global__ __launch_bounds__(SI_RELEASE_THREADS) void release_kernel(const GcmCtx* __restrict__ ctx, RecBatch b,
+                                                                     uint64_t bytes, uint32_t chunk, int aligned,
+                                                                     const uint32_t* gate, uint64_t* clock)
+{
+    clock_stamp(clock, 0);
+    release_body(ctx, b, bytes, chunk, aligned, gate);
+    clock_stamp(clock, 1);
 }
 
 __global__ __launch_bounds__(SI_T) void ctr_kernel(const GcmCtx* __restrict__ ctx,
@@ -1193,6 +1211,14 @@ static hipError_t launch_mode(hipStream_t stream, const GcmCtx* ctx, const RecBa
 {
     if (s.nwg == 0) return hipSuccess;
     const dim3 grid(s.nwg), block(SI_NT);
+    if (ev.clock) {
+        // a measured launch: the same schedule with this kernel's stamps
+        Sched sm = s;
+        sm.clock = ev.clock->take(uint64_t(s.nwg) * (SI_NT / 64));
+        LaunchEvents e2 = ev;
+        e2.clock = nullptr;
+        return launch_mode<kMode>(stream, ctx, b, sm, acc, aligned, e2);
+    }
     if (aligned && s.bytes % 16 == 0)
         launch_records<kMode, true, true>(grid, block, stream, ev, ctx, b, s, acc);
     else if (aligned)
@@ -1223,11 +1249,13 @@ hipError_t launch_release(hipStream_t stream, const GcmCtx* ctx, const RecBatch&
     const uint64_t nb = (bytes + 15) / 16;
     const uint32_t chunk = 8u * SI_RELEASE_THREADS;
     const dim3 grid(uint32_t((nb + chunk - 1) / chunk), nrec), block(SI_RELEASE_THREADS);
+    uint64_t* clock = ev.clock ? ev.clock->take(uint64_t(grid.x) * grid.y * (SI_RELEASE_THREADS / 64)) : nullptr;
     if (ev.start || ev.stop)
         hipExtLaunchKernelGGL(release_kernel, grid, block, 0, stream, ev.start, ev.stop, 0, ctx, b, bytes, chunk,
-                              aligned ? 1 : 0, gate);
+                              aligned ? 1 : 0, gate, clock);
     else
-        hipLaunchKernelGGL(release_kernel, grid, block, 0, stream, ctx, b, bytes, chunk, aligned ? 1 : 0, gate);
+        hipLaunchKernelGGL(release_kernel, grid, block, 0, stream, ctx, b, bytes, chunk, aligned ? 1 : 0, gate,
+                           clock);
     return hipGetLastError();
 }
 

@@ -71,6 +71,7 @@ struct Sched {
     const uint32_t* gate;  // optional: when *gate == 0 every workgroup returns
                            // at once (an allocation-free call that does not own
                            // the GPU's scratch; see noalloc_finish)
+    uint64_t* clock;       // optional: clock stamps of a measured launch (ClockProbe)
 };
 // Scratch of the allocation-free reload (secure_infer_gpu_reload_layer_noalloc):
 // one device array per GPU, [control words][accumulators of up to
@@ -118,12 +119,39 @@ hipError_t launch_noalloc_finish(hipStream_t stream, const NoallocFinish& f);
 // Test hook: hold (1) or release (0) the scratch with SI_NOALLOC_TEST_TOKEN.
 hipError_t launch_noalloc_test_hold(hipStream_t stream, uint32_t* ctrl, int hold);
 
+// Clock stamps of a measured layer: lane 0 of every wave of the layer's
+// kernels writes the device's constant-rate clock (wall_clock64) when the
+// wave starts and when it ends, two words per wave (wave w of a kernel:
+// words 2w, 2w + 1 of that kernel's share), the kernels' shares one after
+// another from `stamps`.  The layer's kernel time is the last end minus the
+// first start.  A kernel whose share does not fit in `words` stamps nothing
+// and sets `overflow`.
+struct ClockProbe {
+    uint64_t* stamps = nullptr;  // device memory
+    uint64_t words = 0;
+    uint64_t used = 0;
+    bool overflow = false;
+
+    uint64_t* take(uint64_t waves)
+    {
+        if (!stamps || used + 2 * waves > words) {
+            overflow = overflow || stamps != nullptr;
+            return nullptr;
+        }
+        uint64_t* p = stamps + used;
+        used += 2 * waves;
+        return p;
+    }
+};
+
 // Events a timed launch records at its kernel's dispatch start and end
 // (hipExtLaunchKernel: the interval a kernel trace reports, without the
-// launch gaps an event recorded between kernels adds).  Null: a plain launch.
+// launch gaps an event recorded between kernels adds), and the clock probe
+// of a measured launch.  Null: a plain launch.
 struct LaunchEvents {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
+    ClockProbe* clock = nullptr;
 };
 
 hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const RecBatch& b,
@@ -171,6 +199,7 @@ struct CodecBatch {
     uint64_t staging_stride;
     uint64_t qbytes, sbytes, width;
     const uint32_t* gate;   // as Sched::gate (dequantiser only)
+    uint64_t* clock;        // as Sched::clock
 };
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev = LaunchEvents());
 hipError_t launch_gather_quant(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev = LaunchEvents());

@@ -29,7 +29,10 @@ typedef enum hipMemcpyKind {
     hipMemcpyDefault = 4,
 } hipMemcpyKind;
 
-typedef enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 1 } hipDeviceAttribute_t;
+typedef enum hipDeviceAttribute_t {
+    hipDeviceAttributeMultiprocessorCount = 1,
+    hipDeviceAttributeWallClockRate = 2
+} hipDeviceAttribute_t;
 
 #define hipStreamDefault 0u
 #define hipStreamNonBlocking 1u

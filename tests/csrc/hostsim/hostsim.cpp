@@ -160,6 +160,10 @@ hipError_t hipSetDevice(int dev) { return dev == 0 ? hipSuccess : hipErrorInvali
 
 hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int)
 {
+    if (a == hipDeviceAttributeWallClockRate) {
+        *v = 100000;  // kHz
+        return hipSuccess;
+    }
     if (a != hipDeviceAttributeMultiprocessorCount) return hipErrorInvalidValue;
     *v = 256;
     return hipSuccess;

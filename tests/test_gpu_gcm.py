@@ -418,6 +418,113 @@ def test_native_transfer_wait_layer():
 
 
 @pytest.mark.parametrize("bits", [0, 4])
+def test_clocked_layer_launch(bits):
+    """secure_infer_gpu_clock_next_layers: armed for two layer calls, every
+    wave of each call's kernels (a reload, then a writeback) writes the device
+    clock at its start and end into that call's words -- two words per wave,
+    each start at or before its end, the reload's span positive and within
+    the host's wall time -- the results are unchanged, and a third call is not
+    clocked.  Stamps that do not fit leave the launch unstamped and are
+    reported (-1), nothing is written past the words given, and the results
+    are still right."""
+    import ctypes as ct
+    import time
+    rng = np.random.default_rng(71 + bits)
+    heads, dim, nb, nslots, layer, t0 = 4, 128, 6, 16, 3, 31000 + bits
+    blocks = W.bf16_blocks(rng, 2 * nb, heads, dim)
+    kinds = [0] * nb + [1] * nb
+    if bits:
+        payloads = [O.codec_encode(blocks[r], bits, kinds[r], layer) for r in range(2 * nb)]
+        want = np.stack([O.codec_decode(payloads[r], heads, dim, bits, kinds[r]) for r in range(2 * nb)])
+    else:
+        payloads = [blocks[r].view(np.uint8).reshape(-1) for r in range(2 * nb)]
+        want = blocks
+    n = payloads[0].size
+    wire = dev(W.build_wire(KEY, SALT, payloads, kinds, layer, list(range(nb)) * 2, t0))
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=n)
+    ck, cv = make_caches(nslots, heads, dim)
+    slot_ids = rng.permutation(nslots)[:nb].astype(np.int64)
+    slots = dev(np.concatenate([slot_ids, slot_ids]))
+    staging = torch.zeros(2 * nb * W.align32(n), dtype=torch.uint8, device=DEV) if bits else None
+    fail = torch.zeros(1, dtype=torch.int32, device=DEV)
+    wb = dev(W.wire_aads(KEY, SALT, n, kinds, layer, list(range(nb)) * 2, t0 + 100))
+    L = si._lib.load()
+    khz = ct.c_uint64()
+    assert L.secure_infer_gpu_clock_rate_khz(ct.byref(khz)) == 0 and khz.value > 0
+    words = 1 << 15
+    big = torch.iinfo(torch.int64).max
+    stamps = torch.zeros(2 * words + 64, dtype=torch.int64, device=DEV)
+    ptr = ct.c_void_p(stamps.data_ptr())
+
+    def arm(nwords, layers):
+        stamps[0::2] = big
+        stamps[1::2] = 0
+        assert L.secure_infer_gpu_clock_next_layers(ptr, nwords, layers) == 0
+
+    def used(layers):
+        u = (ct.c_uint64 * layers)()
+        return L.secure_infer_gpu_clock_layers_used(u, layers), list(u)
+
+    def reload():
+        sess.reload_layer(wire, n, 2 * nb, nb, ck, cv, slots, ticket_base=t0, codec_bits=bits, heads=heads,
+                          head_dim=dim, layer=layer, staging=staging, fail_count=fail)
+
+    def writeback():
+        sess.writeback_layer(wb, n, 2 * nb, nb, ck, cv, slots, ticket_base=t0 + 100, codec_bits=bits, heads=heads,
+                             head_dim=dim, layer=layer, staging=staging)
+
+    def check_reload():
+        assert int(fail.item()) == 0
+        idx = dev(slot_ids)
+        assert torch.equal(ck.index_select(0, idx), dev(want[:nb].view(np.int16)))
+        assert torch.equal(cv.index_select(0, idx), dev(want[nb:].view(np.int16)))
+
+    assert L.secure_infer_gpu_clock_next_layers(None, 16, 1) == -1
+    assert L.secure_infer_gpu_clock_next_layers(ptr, 0, 1) == -1
+    assert L.secure_infer_gpu_clock_next_layers(ptr, 16, 0) == -1
+    arm(words, 2)
+    assert used(1)[0] == -1  # nothing clocked yet
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    reload()
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - w0) * 1e6
+    check_reload()
+    writeback()
+    torch.cuda.synchronize()
+    rc, u = used(2)
+    assert rc == 0 and all(0 < x <= words and x % 2 == 0 for x in u)
+    assert used(3)[0] == -1
+    got = stamps.cpu().numpy()
+    for l in range(2):
+        seg = got[l * words:(l + 1) * words]
+        st, en = seg[0:u[l]:2], seg[1:u[l]:2]
+        assert (st != big).all() and (en != 0).all() and (st <= en).all()
+        assert (seg[u[l]::2] == big).all() and (seg[u[l] + 1::2] == 0).all()  # nothing past its waves
+    seg = got[:words]
+    span_us = (seg[1:u[0]:2].max() - seg[0:u[0]:2].min()) * 1e3 / khz.value
+    assert 0 < span_us <= wall_us
+    expect = W.build_wire(KEY, SALT, payloads, kinds, layer, list(range(nb)) * 2, t0 + 100, direction=2)
+    g = host(wb).reshape(2 * nb, W.stride(n))
+    ex = expect.reshape(2 * nb, W.stride(n))
+    assert np.array_equal(g[:, :n], ex[:, :n])
+    # the arming covered two calls: a third leaves the stamps alone
+    before = stamps.clone()
+    reload()
+    torch.cuda.synchronize()
+    assert torch.equal(stamps, before)
+    # too few words: the kernels that do not fit stamp nothing; reported
+    arm(2, 1)
+    ck.zero_()
+    cv.zero_()
+    reload()
+    torch.cuda.synchronize()
+    assert used(1)[0] == -1
+    assert (stamps[0::2] == big).all() and (stamps[1::2] == 0).all()
+    check_reload()
+
+
+@pytest.mark.parametrize("bits", [0, 4])
 def test_timed_layer_launch(bits):
     """secure_infer_gpu_time_next_layer: the next layer call (reload, then
     writeback) launches its first and last kernels with the caller's events;
