@@ -61,22 +61,22 @@ __device__ __forceinline__ float nonfinite(float x)
 }
 
 // One thread -> 16 consecutive columns (h, d) of `tpt` consecutive tokens
-// (tpt divides 64); grid (x, record).  A K thread loads its 16 (scale, low)
-// pairs once for its tokens (they depend on the column and the 64-token group
-// only); a V token
-// row of 16 elements shares one (t, h, dim-group) pair.  Per token the thread
-// reads 16 (int8) or 8 (int4) packet bytes and writes 32 bytes of bf16, and a
-// wave covers 1 KiB of consecutive packet columns.
-__device__ __forceinline__ void dequant_scatter_body(const CodecBatch& b, uint32_t tpt)
+// (tpt divides 64) of record r; workgroup x of the record.  A K thread loads
+// its 16 (scale, low) pairs once for its tokens (they depend on the column
+// and the 64-token group only), so K takes more tokens per thread than V
+// (whose pair changes with the token); a V token row of 16 elements shares
+// one (t, h, dim-group) pair.  Per token the thread reads 16 (int8) or 8
+// (int4) packet bytes and writes 32 bytes of bf16, and a wave covers 1 KiB of
+// consecutive packet columns.
+__device__ __forceinline__ void dequant_scatter_body(const CodecBatch& b, uint32_t r, uint32_t x, uint32_t tpt)
 {
     // An allocation-free call that does not own the GPU's scratch (whose
     // staging this reads) touches nothing; its records are failed closed
     // by the call's finishing kernel.
     if (b.gate && *b.gate == 0u) return;
-    const uint32_t r = blockIdx.y;
     const uint32_t hd = b.heads * b.dim;
     const uint32_t nc = hd / 16u;  // column chunks per token
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t idx = x * 256u + threadIdx.x;
     if (idx >= (128u / tpt) * nc) return;
     const int64_t sid = b.slots[r];
     if (sid < 0 || sid >= b.nslots) return;
@@ -151,10 +151,19 @@ __device__ __forceinline__ void dequant_scatter_body(const CodecBatch& b, uint32
     }
 }
 
-__global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint32_t tpt)
+// The kx workgroups of each K record (tk tokens per thread), then the vx of
+// each V record (tv tokens per thread).
+__global__ __launch_bounds__(256) void dequant_scatter_kernel(CodecBatch b, uint32_t kx, uint32_t vx, uint32_t tk,
+                                                              uint32_t tv)
 {
     clock_stamp(b.clock, 0);
-    dequant_scatter_body(b, tpt);
+    const uint32_t nkb = kx * b.n_k;
+    if (blockIdx.x < nkb) {
+        dequant_scatter_body(b, blockIdx.x / kx, blockIdx.x % kx, tk);
+    } else {
+        const uint32_t v = blockIdx.x - nkb;
+        dequant_scatter_body(b, b.n_k + v / vx, v % vx, tv);
+    }
     clock_stamp(b.clock, 1);
 }
 
@@ -458,24 +467,37 @@ __global__ __launch_bounds__(256) void quant_kernel(CodecBatch b, uint32_t kx, u
     clock_stamp(b.clock, 1);
 }
 
+// CUs of an MI355X, the unit of the dequantiser's grid sizing.
+constexpr uint64_t kCus = 256;
+
 hipError_t launch_dequant_scatter(hipStream_t stream, const CodecBatch& b, const LaunchEvents& ev)
 {
-    // Tokens per thread: the most that still leaves >= 1024 workgroups (four
-    // per CU), so K parameters are re-read as little as the chip's width
-    // allows.  Measured on MI355X: Llama-3-8B int8 (1024 columns, 128
-    // records) 10.2 / 9.6 / 9.3 / 11.4 us at 1 / 2 / 4 / 8 tokens per thread;
-    // Qwen2.5-7B int4 (512 columns) 6.4 / 6.0 / 7.1 / 9.9 us.
-    const uint64_t wg1 = uint64_t(b.nrec) * b.heads * b.dim / 32u;  // workgroups at tpt = 1
-    uint32_t tpt = 8;
-    while (tpt > 1 && wg1 / tpt < 1024u) tpt >>= 1;
-    const uint32_t per_rec = (128u / tpt) * (b.heads * b.dim / 16u);
-    const dim3 grid((per_rec + 255u) / 256u, b.nrec);
+    // Tokens per thread (a power of two, 1..16): about one workgroup per CU
+    // for the K records and two for the V records.  Measured on MI355X (layer
+    // time with the record kernel; K, V tokens per thread): int4 Qwen2.5-7B
+    // (512 columns, 64 + 64 records) 24.5 / 24.0 / 25.7 / 30.1 us at
+    // (2,2) / (4,2) / (8,2) / (16,2), 25.4 at (8,4); int8 Llama-3-8B (1024
+    // columns) 40.4 / 39.8 / 39.5 / 41.8 us at (2,2) / (4,2) / (8,2) /
+    // (16,2), 39.5 at (8,4) -- the fastest split is 768 workgroups in both.
+    // More workgroups beat sharing a K thread's (scale, low) loads over more
+    // tokens.
+    const uint32_t nc = b.heads * b.dim / 16u;  // 16-column chunks per token
+    const auto tokens = [nc](uint32_t nrec, uint64_t wgs) {
+        const uint64_t t = uint64_t(128u) * nc * nrec / (wgs * 256u);  // tokens per thread for `wgs` workgroups
+        uint32_t p = 1;
+        while (p < 16u && uint64_t(p) * 2u <= t) p *= 2u;
+        return p;
+    };
+    const uint32_t tk = tokens(b.n_k, kCus), tv = tokens(b.nrec - b.n_k, 2u * kCus);
+    const uint32_t kx = ((128u / tk) * nc + 255u) / 256u, vx = ((128u / tv) * nc + 255u) / 256u;
+    const dim3 grid(kx * b.n_k + vx * (b.nrec - b.n_k));
     CodecBatch bb = b;
-    bb.clock = ev.clock ? ev.clock->take(uint64_t(grid.x) * grid.y * 4u) : nullptr;
+    bb.clock = ev.clock ? ev.clock->take(uint64_t(grid.x) * 4u) : nullptr;
     if (ev.start || ev.stop)
-        hipExtLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, bb, tpt);
+        hipExtLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, ev.start, ev.stop, 0, bb, kx, vx,
+                              tk, tv);
     else
-        hipLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, bb, tpt);
+        hipLaunchKernelGGL(dequant_scatter_kernel, grid, dim3(256), 0, stream, bb, kx, vx, tk, tv);
     return hipGetLastError();
 }
 
