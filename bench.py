@@ -327,10 +327,17 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
         out["stripe"] = bool(stripe)
         lib = si._lib.load()
 
-        def step(ahead):
+        layers_in = [(hosts[l], mapping_rl[l]) for l in range(L)]
+        layers_out = [(cache[l, 0], cache[l, 1]) for l in range(L)]
+
+        def step(mode):
+            """One reload of every layer: "on_demand" (each layer sealed as its
+            transfer comes), "sealed_ahead" (every layer sealed before the
+            step), "layer_ahead" (reload_layers: layer l + 1 seals while
+            layer l copies)."""
             nt.layer = 0
-            if ahead:
-                queued = [nt.prefetch_kv_transfer((hosts[l], mapping_rl[l]), l) for l in range(L)]
+            if mode == "sealed_ahead":
+                queued = [nt.prefetch_kv_transfer(layers_in[l], l) for l in range(L)]
                 if not all(queued):
                     raise RuntimeError("prefetch budget (SECURE_INFER_PREFETCH_MB) too small for every layer")
                 deadline = time.perf_counter() + 120
@@ -339,62 +346,81 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
                         raise RuntimeError("prefetched records not sealed within 120 s")
                     time.sleep(0.0005)
             t0 = time.perf_counter()
-            for l in range(L):
-                nt.single_layer_kv_transfer((hosts[l], mapping_rl[l]), (cache[l, 0], cache[l, 1]))
+            if mode == "layer_ahead":
+                nt.reload_layers(layers_in, layers_out, lookahead=1)
+            else:
+                for l in range(L):
+                    nt.single_layer_kv_transfer(layers_in[l], layers_out[l])
             good = all(nt.wait_layer(l) == 0 for l in range(L))
             torch.cuda.synchronize()
             return good, time.perf_counter() - t0
+
+        def timed(mode, merge):
+            """Median step of `steps` and the prefetch counters they moved
+            (busy_fallback: swaps that waited for their records' sealing)."""
+            nonlocal ok
+            nt.merge_groups = merge
+            s0 = si.transfer_prefetch_stats()
+            times = []
+            with Range(f"e2e:{mode}{':merged' if merge else ''}"):
+                for _ in range(steps):
+                    good, t = step(mode)
+                    ok &= good
+                    times.append(t)
+            s1 = si.transfer_prefetch_stats()
+            nt.merge_groups = False
+            return float(np.median(times)), {k: s1[k] - s0[k] for k in s1}
+
+        def matches_truth():
+            if truth is None:
+                return True
+            got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
+            return bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
+
         # Timed steps run with the ledger paused (its timing events cost the
         # host ~10 us per launch); one more step of each mode records it.
         si.pause_h2d_profile(True)
-        ok, _ = step(False)
-        med = {}
-        for ahead in (False, True):
-            times = []
-            for _ in range(steps):
-                good, t = step(ahead)
-                ok &= good
-                times.append(t)
-            med[ahead] = float(np.median(times))
-        dt = med[False]
-        if truth is not None:
-            got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
-            ok &= bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
-        out["sealed_ahead_of_demand"] = {"us_per_layer": round(med[True] * 1e6 / L, 1),
-                                         "GB_s": round(algo_layer * L / med[True] / 1e9, 2),
-                                         "prefetch_stats": si.transfer_prefetch_stats()}
+        ok, _ = step("on_demand")
+        med, stats = {}, {}
+        for mode in ("on_demand", "sealed_ahead", "layer_ahead"):
+            med[mode], stats[mode] = timed(mode, False)
+        dt = med["on_demand"]
+        ok &= matches_truth()
+        out["on_demand_prefetch_stats"] = stats["on_demand"]
+        out["sealed_ahead_of_demand"] = {"us_per_layer": round(med["sealed_ahead"] * 1e6 / L, 1),
+                                         "GB_s": round(algo_layer * L / med["sealed_ahead"] / 1e9, 2),
+                                         "prefetch_stats": stats["sealed_ahead"]}
+        out["sealed_one_layer_ahead"] = {"us_per_layer": round(med["layer_ahead"] * 1e6 / L, 1),
+                                         "GB_s": round(algo_layer * L / med["layer_ahead"] / 1e9, 2),
+                                         "prefetch_stats": stats["layer_ahead"]}
         # The same steps with each layer's causal groups merged into one
         # launch (NativeTransfer merge_groups: same swaps, same tickets; one
         # layer prefetch and one DMA when sealed ahead).
-        nt.merge_groups = True
         cache.zero_()
         merged = {}
-        for ahead in (False, True):
-            times = []
-            for _ in range(steps):
-                good, t = step(ahead)
-                ok &= good
-                times.append(t)
-            merged[ahead] = float(np.median(times))
-        if truth is not None:
-            got = torch.stack([cache[l][:, slots[l]] for l in range(L)])
-            ok &= bool(torch.equal(got.view(torch.int16), truth.view(torch.int16)))
-        nt.merge_groups = False
+        for mode in ("on_demand", "sealed_ahead", "layer_ahead"):
+            merged[mode], stats["merged_" + mode] = timed(mode, True)
+        ok &= matches_truth()
         out["merged_layer_launch"] = {
-            "on_demand_us_per_layer": round(merged[False] * 1e6 / L, 1),
-            "sealed_ahead_us_per_layer": round(merged[True] * 1e6 / L, 1),
-            "sealed_ahead_GB_s": round(algo_layer * L / merged[True] / 1e9, 2)}
+            "on_demand_us_per_layer": round(merged["on_demand"] * 1e6 / L, 1),
+            "sealed_ahead_us_per_layer": round(merged["sealed_ahead"] * 1e6 / L, 1),
+            "sealed_ahead_GB_s": round(algo_layer * L / merged["sealed_ahead"] / 1e9, 2),
+            "one_layer_ahead_us_per_layer": round(merged["layer_ahead"] * 1e6 / L, 1),
+            "one_layer_ahead_GB_s": round(algo_layer * L / merged["layer_ahead"] / 1e9, 2),
+            "one_layer_ahead_prefetch_stats": stats["merged_layer_ahead"]}
         ledger = os.environ.get("SECURE_INFER_H2D_PROFILE")
         if ledger:
             si.pause_h2d_profile(False)
             split = {}
-            for ahead, merge, name in ((False, False, "on_demand"), (True, False, "sealed_ahead_of_demand"),
-                                       (True, True, "merged_sealed_ahead_of_demand")):
+            for mode, merge, name in (("on_demand", False, "on_demand"),
+                                      ("sealed_ahead", False, "sealed_ahead_of_demand"),
+                                      ("sealed_ahead", True, "merged_sealed_ahead_of_demand"),
+                                      ("layer_ahead", True, "merged_one_layer_ahead")):
                 si.drain_h2d_profile_after_job()
                 if Path(ledger).exists():
                     Path(ledger).write_text(Path(ledger).read_text().splitlines()[0] + "\n")
                 nt.merge_groups = merge
-                good, t = step(ahead)
+                good, t = step(mode)
                 nt.merge_groups = False
                 ok &= good
                 si.drain_h2d_profile_after_job()

@@ -594,6 +594,18 @@ class NativeTransfer:
         return plan
 
     @staticmethod
+    def _check_mapping(host, mapping: torch.Tensor, destination) -> None:
+        """The swaps refuse ids outside either pool before sealing anything;
+        sealing ahead must not spend tickets on a mapping they refuse.
+        (numpy: a torch reduction would wake torch's CPU thread pool, whose
+        spinning threads then compete with the sealing workers.)"""
+        m = mapping.numpy()
+        lo, hi = m.min(0), m.max(0)
+        if (lo[0] < 0 or hi[0] >= min(host[0].shape[0], host[1].shape[0]) or lo[1] < 0
+                or hi[1] >= min(destination[0].shape[0], destination[1].shape[0])):
+            raise RuntimeError("h2d_swap refused: a mapping entry lies outside its pool")
+
+    @staticmethod
     def _host_pool(src: torch.Tensor) -> torch.Tensor:
         if src.is_cuda or not src.is_contiguous():
             raise ValueError("host pools must be contiguous CPU tensors")
@@ -609,15 +621,7 @@ class NativeTransfer:
         if self.layer in self._prefetched:
             self._prefetched.discard(self.layer)
         elif self.pipeline_seal and (len(plan) > 1 or len(plan[0][1]) > 1):
-            # The swaps refuse ids outside either pool before sealing anything;
-            # sealing ahead must not spend tickets on a mapping they refuse.
-            # (numpy: a torch reduction would wake torch's CPU thread pool,
-            # whose spinning threads then compete with the sealing workers)
-            m = mapping.numpy()
-            lo, hi = m.min(0), m.max(0)
-            if (lo[0] < 0 or hi[0] >= min(host[0].shape[0], host[1].shape[0]) or lo[1] < 0
-                    or hi[1] >= min(destination[0].shape[0], destination[1].shape[0])):
-                raise RuntimeError("h2d_swap refused: a mapping entry lies outside its pool")
+            self._check_mapping(host, mapping, destination)
             self.prefetch_kv_transfer(payload, self.layer)
             self._prefetched.discard(self.layer)
         bits = self.shape.bits_for(self.layer)
@@ -741,6 +745,33 @@ class NativeTransfer:
                                                        ct.c_void_p(fail.data_ptr())),
                "recovery_track_layer")
         self.layer += 1
+
+    def reload_layers(self, payloads, destinations, lookahead: int = 1) -> None:
+        """Every layer of a stored prefix in order, through
+        single_layer_kv_transfer, with the host sealing ahead: before layer
+        l's swaps the records of layers l .. l + lookahead are queued for
+        sealing (prefetch_kv_transfer, in layer order, so tickets keep the
+        reference's (layer, group, kind, block) order), so layer l + 1 seals
+        while layer l copies.  The reference keeps a window of predicted
+        records sealing ahead of the swaps (schedule_linear_prefetches,
+        secure_infer.cpp:1696-1740); here the window is `lookahead` whole
+        layers, named by the caller instead of predicted from addresses.  A
+        prefetch over the SECURE_INFER_PREFETCH_MB budget leaves that layer
+        to seal on demand.  Layers are numbered from the driver's current
+        layer."""
+        n = len(payloads)
+        if len(destinations) != n:
+            raise ValueError("one destination per payload")
+        base = self.layer
+        maps = [m.to(device="cpu", dtype=torch.int64).contiguous() for _, m in payloads]
+        for (host, _), m, dst in zip(payloads, maps, destinations):
+            if m.shape[0]:
+                self._check_mapping(host, m, dst)
+        for l in range(n):
+            for a in range(l, min(n, l + 1 + max(0, int(lookahead)))):
+                if base + a not in self._prefetched and maps[a].shape[0]:
+                    self.prefetch_kv_transfer((payloads[a][0], maps[a]), base + a)
+            self.single_layer_kv_transfer((payloads[l][0], maps[l]), destinations[l])
 
     def wait_layer(self, layer: int) -> int:
         """0 if every record of `layer` authenticated, -1 otherwise."""

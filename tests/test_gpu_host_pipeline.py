@@ -445,6 +445,41 @@ def test_prefetched_records_serve_the_swaps():
         si.clear_host_ranges()
 
 
+@pytest.mark.parametrize("merge", [False, True], ids=["per_group", "merged"])
+def test_reload_layers_one_layer_ahead(merge):
+    """reload_layers with lookahead 1 (layer l + 1 sealing while layer l
+    copies): 4 layers of 41 blocks in 16-block causal groups, every swap
+    served by a prefetch, nothing left unconsumed, exactly 2 x 41 tickets per
+    layer, every layer authenticated and bit-exact."""
+    rng = np.random.default_rng(147 + int(merge))
+    heads, dim, ncpu, nslots, nlayers = 2, 128, 41, 64, 4
+    shape = si.LayerShape(heads, dim)
+    sess = si.GcmSession(KEY, SALT, 12, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        host_layers = _layers(rng, nlayers, ncpu, heads, dim)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16, merge_groups=merge)
+        slot_ids = rng.permutation(nslots)[:ncpu]
+        mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
+        caches_l = [caches(nslots, heads, dim) for _ in range(nlayers)]
+        before = si.transfer_prefetch_stats()
+        t0 = si.new_transfer_ticket()
+        nt.reload_layers([(host_layers[l], mapping) for l in range(nlayers)], caches_l, lookahead=1)
+        assert si.new_transfer_ticket() == t0 + nlayers * 2 * ncpu + 1
+        after = si.transfer_prefetch_stats()
+        served = (after["ready"] - before["ready"]) + (after["busy_fallback"] - before["busy_fallback"])
+        assert served == nlayers * 6 and after["missing_fallback"] == before["missing_fallback"]
+        idx = torch.from_numpy(slot_ids.astype(np.int64)).to(DEV)
+        for layer in range(nlayers):
+            assert nt.wait_layer(layer) == 0
+            (hk, hv), (ck, cv) = host_layers[layer], caches_l[layer]
+            assert torch.equal(ck.index_select(0, idx).cpu(), hk) and torch.equal(cv.index_select(0, idx).cpu(), hv)
+        assert int(_lib.load().secure_infer_count_ready_unconsumed_gcm_tickets()) == 0
+    finally:
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()
+
+
 def test_retired_prefetch_falls_back_to_sealing_on_demand():
     rng = np.random.default_rng(142)
     heads, dim, ncpu, nslots = 2, 128, 4, 8

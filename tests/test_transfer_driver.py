@@ -248,3 +248,56 @@ def test_merged_single_group_is_a_group_prefetch():
     _, rec, _ = run_transfer(10, 16, None, keep_prefetch=True, merge_groups=True)
     assert [c[0] for c in rec.calls if c[0].startswith("prefetch")] == [
         "prefetch", "prefetch_group_pairs_with_previous", "prefetch"]
+
+
+@pytest.mark.parametrize("lookahead", [0, 1, 2])
+def test_reload_layers_seals_ahead_in_layer_order(lookahead):
+    """reload_layers: before layer l's swaps, layers l .. l + lookahead are
+    queued for sealing, each once and in layer order (so tickets keep the
+    (layer, group, kind, block) order); every layer's swaps then consume
+    them, and a mapping outside its pool is refused before anything is
+    sealed."""
+    rec = Recorder()
+    parent = FakeStream("parent")
+    shape = si.LayerShape(2, 64)
+    sess = mock.Mock()
+    sess._h = None
+    nt = si.NativeTransfer(sess, shape, causal_group_blocks=16)
+    nt.layer = 5
+    nb, nlayers = 20, 4
+    payloads, dests = [], []
+    for _ in range(nlayers):
+        host = [torch.zeros((nb, 4), dtype=torch.int16), torch.zeros((nb, 4), dtype=torch.int16)]
+        payloads.append((host, torch.stack((torch.arange(nb), torch.arange(nb) + 3), dim=1)))
+        dests.append([torch.zeros((nb + 3, 4), dtype=torch.int16) for _ in range(2)])
+    with mock.patch.object(gcm, "lib", return_value=rec), \
+         mock.patch.object(gcm, "_dev", lambda t, name: None), \
+         mock.patch.object(gcm.torch.cuda, "current_stream", return_value=parent):
+        nt.reload_layers(payloads, dests, lookahead=lookahead)
+        assert nt.layer == 5 + nlayers
+        events = []
+        for c in rec.calls:
+            if c[0] == "prefetch" and c[1] == 0 and (not events or events[-1] != ("P", c[2])):
+                events.append(("P", c[2]))
+            elif c[0] == "swap" and (not events or events[-1] != ("S", c[3])):
+                events.append(("S", c[3]))
+        want = []
+        queued = set()
+        for l in range(nlayers):
+            for a in range(l, min(nlayers, l + 1 + lookahead)):
+                if a not in queued:
+                    queued.add(a)
+                    want.append(("P", 5 + a))
+            want.append(("S", 5 + l))
+        assert events == want
+        # the prefetched parts are exactly the swapped ones, layer by layer
+        pre = [(c[1], c[2], c[4]) for c in rec.calls if c[0] == "prefetch"]
+        sw = [(c[2], c[3], c[5]) for c in rec.calls if c[0] == "swap"]
+        assert sorted(pre, key=lambda x: x[1]) == sorted(sw, key=lambda x: x[1]) and len(pre) == len(sw)
+        # refused before any sealing
+        rec.calls.clear()
+        bad = list(payloads)
+        bad[2] = (payloads[2][0], torch.stack((torch.arange(nb), torch.arange(nb) + 30), dim=1))
+        with pytest.raises(RuntimeError):
+            nt.reload_layers(bad, dests, lookahead=lookahead)
+        assert not [c for c in rec.calls if c[0] in ("prefetch", "swap")]
