@@ -158,6 +158,30 @@ def test_error_returns_before_any_device_work():
     t.join()
     assert errors == [-1]
     assert L.secure_infer_h2d_layer_group_end() == 0
+    # layer prefetch (a bf16 block of 1 head x 64 is 16,384 B): each call breaks
+    # one argument -- null pools / mapping / group table, no groups, an empty
+    # group, a host block outside the pool, a bad codec -- and is refused
+    # before the (stand-in) session is touched
+    m = (ct.c_int64 * 4)(0, 0, 1, 1)
+    starts, rows, zero = (ct.c_uint32 * 1)(0), (ct.c_uint32 * 1)(2), (ct.c_uint32 * 1)(0)
+    sess, bb = v(1), 16384
+    assert L.secure_infer_h2d_prefetch_layer(sess, None, one, bb, 2, m, starts, rows, 1, 0, 0, 1, 64) == -1
+    assert L.secure_infer_h2d_prefetch_layer(sess, one, one, bb, 2, None, starts, rows, 1, 0, 0, 1, 64) == -1
+    assert L.secure_infer_h2d_prefetch_layer(sess, one, one, bb, 2, m, None, rows, 1, 0, 0, 1, 64) == -1
+    assert L.secure_infer_h2d_prefetch_layer(sess, one, one, bb, 2, m, starts, rows, 0, 0, 0, 1, 64) == -1
+    assert L.secure_infer_h2d_prefetch_layer(sess, one, one, bb, 2, m, starts, zero, 1, 0, 0, 1, 64) == -1
+    assert L.secure_infer_h2d_prefetch_layer(sess, one, one, bb, 1, m, starts, rows, 1, 0, 0, 1, 64) == -1
+    assert L.secure_infer_h2d_prefetch_layer(sess, one, one, bb, 2, m, starts, rows, 1, 0, 3, 1, 64) == -1
+    # kernel clock: null / zero arguments, nothing clocked since arming
+    words = ct.c_uint64()
+    assert L.secure_infer_gpu_clock_next_layers(None, 16, 1) == -1
+    assert L.secure_infer_gpu_clock_next_layers(one, 0, 1) == -1
+    assert L.secure_infer_gpu_clock_next_layers(one, 16, 0) == -1
+    assert L.secure_infer_gpu_clock_next_layers(one, 1 << 62, 8) == -1          # words overflow
+    assert L.secure_infer_gpu_clock_next_layers(one, 16, 2) == 0
+    assert L.secure_infer_gpu_clock_layers_used(ct.byref(words), 1) == -1      # no layer call yet
+    assert L.secure_infer_gpu_clock_layers_used(ct.byref(words), 0) == -1
+    assert L.secure_infer_gpu_clock_rate_khz(None) == -1
     # tracking and tuning
     assert L.secure_infer_recovery_track_layer(0, None, one) == -1
     assert L.secure_infer_gpu_set_chunk_rows(0) == -1
