@@ -136,13 +136,16 @@ def test_full_size_writeback_layer_int4_llama3_70b(heads):
         assert ww[r, toff:toff + 16].tobytes() == tag, f"record {r} tag"
 
 
+@pytest.mark.parametrize("merge", [False, True], ids=["per_group", "merged"])
 @pytest.mark.parametrize("bits,heads,nb", [(0, 8, 48), (4, 4, 64)], ids=["bf16_llama3_8b", "int4_qwen2_5_7b"])
-def test_full_size_layer_through_the_host_pipeline(bits, heads, nb):
+def test_full_size_layer_through_the_host_pipeline(bits, heads, nb, merge):
     """A full-size layer end to end: host pools -> NativeTransfer with the
     reference's 16-block causal groups (host OpenSSL seals, group prefetch,
-    one DMA per group launch) -> fused reload into a 512-slot cache; every
-    slot equals its host block (bf16) or the oracle decode of its packet, and
-    the other slots are untouched."""
+    one DMA per group launch; merged: the layer's groups in one launch from
+    one layer prefetch, with one V record corrupted once and repaired by the
+    strict retry) -> fused reload into a 512-slot cache; every slot equals its
+    host block (bf16) or the oracle decode of its packet, and the other slots
+    are untouched."""
     rng = np.random.default_rng(2000 + bits)
     dim, nslots, layer = 128, 512, 9
     shape = si.LayerShape(heads, dim, bits)
@@ -162,8 +165,10 @@ def test_full_size_layer_through_the_host_pipeline(bits, heads, nb):
     try:
         si.register_host_range(host[0], layer, 0)
         si.register_host_range(host[1], layer, 1)
-        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16, merge_groups=merge)
         nt.layer = layer
+        if merge:
+            si.inject_h2d_tamper(layer=layer, kind=1, host_block=nb // 2 + 1, shots=1)
         nt.single_layer_kv_transfer((host, mapping), caches)
         assert nt.wait_layer(layer) == 0
         torch.cuda.synchronize()
@@ -176,6 +181,8 @@ def test_full_size_layer_through_the_host_pipeline(bits, heads, nb):
             rest = torch.from_numpy(np.setdiff1d(np.arange(nslots), slots).astype(np.int64)).to(DEV)
             assert bool((caches[k].index_select(0, rest).view(torch.uint8) == 0x3C).all())
     finally:
+        si.inject_h2d_tamper(shots=0)
+        si.retire_transfer_prefetches()
         si.clear_host_ranges()
 
 
