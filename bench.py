@@ -351,9 +351,12 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
             else:
                 for l in range(L):
                     nt.single_layer_kv_transfer(layers_in[l], layers_out[l])
+            issue[mode] = issue.get(mode, []) + [time.perf_counter() - t0]
             good = all(nt.wait_layer(l) == 0 for l in range(L))
             torch.cuda.synchronize()
             return good, time.perf_counter() - t0
+
+        issue = {}  # host time to issue every layer (the transfer calls' return), per mode
 
         def timed(mode, merge):
             """Median step of `steps` and the prefetch counters they moved
@@ -361,6 +364,7 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
             nonlocal ok
             nt.merge_groups = merge
             s0 = si.transfer_prefetch_stats()
+            issue.pop(mode, None)
             times = []
             with Range(f"e2e:{mode}{':merged' if merge else ''}"):
                 for _ in range(steps):
@@ -369,7 +373,10 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
                     times.append(t)
             s1 = si.transfer_prefetch_stats()
             nt.merge_groups = False
+            issued[mode + (":merged" if merge else "")] = round(float(np.median(issue[mode])) * 1e6 / L, 1)
             return float(np.median(times)), {k: s1[k] - s0[k] for k in s1}
+
+        issued = {}  # median host issue time per layer, per mode
 
         def matches_truth():
             if truth is None:
@@ -408,6 +415,10 @@ def end_to_end(si, torch, sess, op, cfg, cache, slots, nbytes, block_bytes, algo
             "one_layer_ahead_us_per_layer": round(merged["layer_ahead"] * 1e6 / L, 1),
             "one_layer_ahead_GB_s": round(algo_layer * L / merged["layer_ahead"] / 1e9, 2),
             "one_layer_ahead_prefetch_stats": stats["merged_layer_ahead"]}
+        # Host time to issue a layer (the transfer calls until they return; the
+        # copies and kernels they queue run on): a mode whose figure nears its
+        # step time per layer is bound by the host's issue rate.
+        out["host_issue_us_per_layer"] = issued
         ledger = os.environ.get("SECURE_INFER_H2D_PROFILE")
         if ledger:
             si.pause_h2d_profile(False)
