@@ -1884,7 +1884,6 @@ int secure_infer_h2d_prefetch_layer(si_session* s, const void* k_base, const voi
     // the records keep the reference's tickets while the buffer holds every K
     // record before every V record, with explicit IV words.
     const uint64_t t0 = si_internal::reserve_tickets(2 * N);
-    if (!si_internal::replay_reserve_range(t0, 2 * uint64_t(N))) return -1;
     uint32_t* ivw = reinterpret_cast<uint32_t*>(buf + wire);
     int64_t* ids = reinterpret_cast<int64_t*>(buf + wire + size_t(2) * N * 16);
     const uint32_t salt = (uint32_t(keys.salt[0]) << 24) | (uint32_t(keys.salt[1]) << 16) |
@@ -1919,6 +1918,8 @@ int secure_infer_h2d_prefetch_layer(si_session* s, const void* k_base, const voi
         }
         off += n;
     }
+    // (On failure the parts go, and the first returns the buffer to the pool.)
+    if (!si_internal::replay_reserve_range(t0, 2 * uint64_t(N))) return -1;
     std::vector<std::function<void()>> tasks;
     for (auto& pf : parts) queue_seals(pf, tasks);
     Pool::get().submit_all(tasks);
