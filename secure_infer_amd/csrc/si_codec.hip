@@ -23,6 +23,8 @@
 
 namespace si {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t h)
 {
     return __uint_as_float(h << 16);
@@ -145,9 +147,16 @@ __device__ __forceinline__ void dequant_scatter_body(const CodecBatch& b, uint32
                 for (int k = 0; k < 8; ++k) out[k] = dq2<false>(q[2 * k], sv, ov, q[2 * k + 1], sv, ov);
             }
         }
-        uint4* dst = reinterpret_cast<uint4*>(slot + uint64_t(e0) * 2u);
-        dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
-        dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+        // Non-temporal stores: the slots are not read again in this launch,
+        // and a kernel that ends with the layer's bf16 output dirty in L2
+        // holds the next launch back while that is written back (MI355X,
+        // ABBA x 2 on one box, layer time: int4 Qwen2.5-7B 24.2 -> 22.7 us,
+        // int8 Llama-3-8B 39.3 -> 39.5 us; write-through stores of the two
+        // interleaved halves: 32.0 / 56.9 us).
+        u32x4* dst = reinterpret_cast<u32x4*>(slot + uint64_t(e0) * 2u);
+        const u32x4 v0 = {out[0], out[1], out[2], out[3]}, v1 = {out[4], out[5], out[6], out[7]};
+        __builtin_nontemporal_store(v0, dst);
+        __builtin_nontemporal_store(v1, dst + 1);
     }
 }
 
