@@ -564,7 +564,8 @@ int secure_infer_d2h_batch_end(void);
  * thread hands each launch to the pool once its copy is done.  At most 6
  * launches and SECURE_INFER_D2H_INFLIGHT_MB (128) of buffers are in flight
  * per device; an issue beyond that waits.  A failed record is zeroed in the
- * host pool and makes batch_end return -1 (the reference zeroes and aborts).
+ * host pool and makes batch_end return -1 (the reference zeroes and aborts;
+ * SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE=1 aborts too, after the zeroing).
  * Stream order of the source reads: the device reads a swap's slots when its
  * launch is issued, which can be as late as batch_device_barrier (the
  * reference enqueues each swap's read at the call).  So work the caller

@@ -1440,6 +1440,19 @@ uint64_t d2h_batch_launch_cap(const D2HBatch& b, uint64_t stride)
 
 size_t job_bytes(const D2HJob& j, bool ivs) { return size_t(j.n) * (j.stride + (ivs ? 24 : 8)) + 16; }
 
+// SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE=1: a D2H record that fails host
+// authentication zeroes its host block and then aborts the process, as the
+// reference does (secure_infer.cpp:2514-2524, 8550-8555); by default the
+// batch fails instead (batch_end returns -1) and the process goes on.
+bool d2h_abort_on_failure()
+{
+    static const bool a = [] {
+        const char* e = std::getenv("SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE");
+        return e && std::atoi(e) != 0;
+    }();
+    return a;
+}
+
 void verify_records(D2HJob* job, uint32_t r0, uint32_t r1)
 {
     D2HBatch* b = job->batch;
@@ -1469,6 +1482,13 @@ void verify_records(D2HJob* job, uint32_t r0, uint32_t r1)
         }
     }
     if (bad) b->failures.fetch_add(bad);
+    if (bad && d2h_abort_on_failure()) {
+        fprintf(stderr,
+                "[secure_infer] D2H authentication failed: %llu record(s) withheld (host blocks zeroed); "
+                "aborting (SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE)\n",
+                static_cast<unsigned long long>(bad));
+        std::abort();
+    }
     // The decrements and the notification happen under the batch's lock:
     // batch_end may destroy the batch as soon as it sees pending_tasks == 0.
     // The job's buffer goes back to the device's pool after its last task.

@@ -463,6 +463,18 @@ void watchdog(int rounds, int limit)
 
 int main(int argc, char** argv)
 {
+    if (argc > 1 && std::string(argv[1]) == "d2h_failure") {
+        // One store batch with one record corrupted on its way to the host:
+        // the batch fails (batch_end -1, the block zeroed), or, with
+        // SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE=1, the process aborts first.
+        si_session* sess = new_session(4242);
+        store_thread(0, sess, 5000, 1, 0u, 99u, true);
+        CHECK(secure_infer_gpu_session_destroy(sess) == 0, "destroy");
+        hipDeviceSynchronize();
+        if (g_failures.load()) return 1;
+        printf("D2H_FAILURE_REPORTED\n");
+        return 0;
+    }
     const int rounds = argc > 1 ? atoi(argv[1]) : 2;
     const int limit = argc > 2 ? atoi(argv[2]) : 60;
     std::thread dog(watchdog, rounds, limit);

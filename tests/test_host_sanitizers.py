@@ -48,3 +48,25 @@ def test_host_runtime_under_sanitizer(san, env, rounds):
         "LeakSanitizer" not in report, report[-4000:]
     assert r.returncode == 0, report[-4000:]
     assert f"HOST_STRESS_OK rounds={rounds}" in r.stdout
+
+
+@pytest.mark.parametrize("abort", [False, True], ids=["batch_fails", "process_aborts"])
+def test_d2h_authentication_failure_handling(abort):
+    """A D2H record corrupted on its way to the host is zeroed in its host
+    block and fails the batch (batch_end -1) -- or, with
+    SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE=1, the reference's behaviour: the
+    process aborts (secure_infer.cpp:2514-2524).  Host code only, under
+    AddressSanitizer with the HIP stand-in."""
+    exe = build("address")
+    env = {**os.environ, "ASAN_OPTIONS": "halt_on_error=1:detect_leaks=0"}
+    if abort:
+        env["SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE"] = "1"
+    r = subprocess.run([str(exe), "d2h_failure"], capture_output=True, text=True, timeout=300, env=env)
+    report = r.stdout + r.stderr
+    assert "AddressSanitizer" not in report, report[-4000:]
+    if abort:
+        assert r.returncode in (-6, 134), report[-4000:]
+        assert "aborting (SECURE_INFER_D2H_ABORT_ON_AUTH_FAILURE)" in r.stderr
+        assert "D2H_FAILURE_REPORTED" not in r.stdout
+    else:
+        assert r.returncode == 0 and "D2H_FAILURE_REPORTED" in r.stdout, report[-4000:]
