@@ -545,6 +545,16 @@ class NativeTransfer:
       ``wait_layer`` returns the layer's authentication result after at most
       one strict retry per failed record (wait_for_layer_load,
       connector.py:378-410; secure_infer.cpp:7303-7333).
+    * With ``codec_auth_wait`` a codec layer's transfer returns only once the
+      layer has authenticated (``wait_layer``, strict retries included) and
+      raises ``RuntimeError('Packed KV authentication failed')`` otherwise:
+      the reference's codec transfer asserts ``wait_auth(layer) == 0`` before
+      it decodes a layer (transport_codec.py:168-174, pipelined_codec.py:118).
+      Here the device decodes in the same launch sequence, stream-ordered
+      after the verification (a failed record decodes to zeros); with
+      SECURE_INFER_VERIFY_BEFORE_RELEASE=1 it also releases no record's
+      plaintext before that record's tag has been checked.  The transfer is
+      then synchronous per codec layer, as the reference's is.
 
     ``single_layer_wire_transfer((wire, mapping), destination, ticket_base)``
     reloads records already resident on the device (K blocks then V blocks,
@@ -554,13 +564,14 @@ class NativeTransfer:
 
     def __init__(self, session: GcmSession, shape: LayerShape, stream=None, streams=None,
                  causal_group_blocks: int = 0, pipeline_seal: bool = True, stripe: bool = False,
-                 merge_groups: bool = False):
+                 merge_groups: bool = False, codec_auth_wait: bool = False):
         self.session = session
         self.shape = shape
         self.stream = stream
         self.streams = list(streams) if streams else [stream]
         self.stripe = bool(stripe)
         self.merge_groups = bool(merge_groups)
+        self.codec_auth_wait = bool(codec_auth_wait)
         self.causal_group_blocks = int(causal_group_blocks)
         self.pipeline_seal = pipeline_seal
         self.layer = 0
@@ -660,6 +671,11 @@ class NativeTransfer:
             if st != parent:
                 parent.wait_stream(st)
         self.layer += 1
+        self._codec_auth(layer, bits)
+
+    def _codec_auth(self, layer: int, bits: int) -> None:
+        if self.codec_auth_wait and bits and self.wait_layer(layer) != 0:
+            raise RuntimeError("Packed KV authentication failed")
 
     def prefetch_kv_transfer(self, payload, layer: int) -> bool:
         """Seal `layer`'s records on the host worker pool ahead of demand
@@ -745,6 +761,7 @@ class NativeTransfer:
                                                        ct.c_void_p(fail.data_ptr())),
                "recovery_track_layer")
         self.layer += 1
+        self._codec_auth(self.layer - 1, bits)
 
     def reload_layers(self, payloads, destinations, lookahead: int = 1) -> None:
         """Every layer of a stored prefix in order, through

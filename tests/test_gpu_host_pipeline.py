@@ -862,3 +862,44 @@ def test_h2d_profile_ledger(tmp_path):
     for r in rows:
         assert int(r[2]) == 6 and int(r[3]) == 128 * 2 * 128 * 2
         assert float(r[5]) > 0 and float(r[6]) > 0 and float(r[7]) > 0
+
+
+@pytest.mark.parametrize("shots", [1, 2], ids=["repaired", "final"])
+def test_codec_auth_wait(shots):
+    """NativeTransfer(codec_auth_wait=True) over an int4 layer whose V record
+    is corrupted once: the strict retry re-seals it and the transfer returns
+    with every slot bit-exact.  Corrupted twice: the transfer raises 'Packed
+    KV authentication failed' (the reference's assert before decode_into,
+    transport_codec.py:168-174) and that record's slot reads as zeros, every
+    other slot bit-exact."""
+    rng = np.random.default_rng(170 + shots)
+    heads, dim, ncpu, nslots, layer, bits = 2, 128, 20, 32, 0, 4
+    shape = si.LayerShape(heads, dim, bits)
+    sess = si.GcmSession(KEY, SALT, 30 + shots, max_record_bytes=shape.record_bytes)
+    si.clear_host_ranges()
+    try:
+        (packets, _), = _codec_layers(rng, 1, ncpu, heads, dim, bits)
+        slot_ids = rng.permutation(nslots)[:ncpu]
+        mapping = torch.from_numpy(np.stack([np.arange(ncpu), slot_ids], 1).astype(np.int64))
+        victim = 7
+        si.inject_h2d_tamper(layer=layer, kind=1, host_block=victim, shots=shots)
+        nt = si.NativeTransfer(sess, shape, causal_group_blocks=16, codec_auth_wait=True)
+        ck, cv = caches(nslots, heads, dim)
+        if shots == 1:
+            nt.single_layer_kv_transfer((packets, mapping), (ck, cv))
+        else:
+            with pytest.raises(RuntimeError, match="Packed KV authentication failed"):
+                nt.single_layer_kv_transfer((packets, mapping), (ck, cv))
+        assert nt.layer == layer + 1
+        kk, vv = host(ck), host(cv)
+        for c, sl in enumerate(slot_ids):
+            assert np.array_equal(kk[sl].view(np.uint16), O.codec_decode(packets[0][c].numpy(), heads, dim, bits, 0))
+            if shots == 2 and c == victim:
+                assert (vv[sl] == 0).all()
+            else:
+                assert np.array_equal(vv[sl].view(np.uint16),
+                                      O.codec_decode(packets[1][c].numpy(), heads, dim, bits, 1)), c
+    finally:
+        si.inject_h2d_tamper(shots=0)
+        si.retire_transfer_prefetches()
+        si.clear_host_ranges()

@@ -34,8 +34,13 @@ class FakeStream:
 class Recorder:
     """Stands in for libsecure_infer.so: records brackets and swaps."""
 
-    def __init__(self):
+    def __init__(self, auth=0):
         self.calls = []
+        self.auth = auth
+
+    def secure_infer_recovery_wait_layer_authentication(self, layer):
+        self.calls.append(("wait", int(layer)))
+        return self.auth
 
     def secure_infer_h2d_layer_group_begin(self, n):
         self.calls.append(("begin", int(n)))
@@ -85,14 +90,15 @@ class Recorder:
 
 
 def run_transfer(nblocks, group, streams, layer=7, shape=None, nslots=None, keep_prefetch=False,
-                 pipeline_seal=True, stripe=False, merge_groups=False):
-    rec = Recorder()
+                 pipeline_seal=True, stripe=False, merge_groups=False, codec_auth_wait=False, auth=0):
+    rec = Recorder(auth)
     parent = FakeStream("parent")
     shape = shape or si.LayerShape(2, 64)
     sess = mock.Mock()
     sess._h = None
     nt = si.NativeTransfer(sess, shape, streams=streams or None, causal_group_blocks=group,
-                           pipeline_seal=pipeline_seal, stripe=stripe, merge_groups=merge_groups)
+                           pipeline_seal=pipeline_seal, stripe=stripe, merge_groups=merge_groups,
+                           codec_auth_wait=codec_auth_wait)
     nt.layer = layer
     host = [torch.zeros((nblocks, 4), dtype=torch.int16), torch.zeros((nblocks, 4), dtype=torch.int16)]
     dest = [torch.zeros((nslots or nblocks + 100, 4), dtype=torch.int16) for _ in range(2)]
@@ -301,3 +307,24 @@ def test_reload_layers_seals_ahead_in_layer_order(lookahead):
         with pytest.raises(RuntimeError):
             nt.reload_layers(bad, dests, lookahead=lookahead)
         assert not [c for c in rec.calls if c[0] in ("prefetch", "swap")]
+
+
+@pytest.mark.parametrize("auth", [0, -1], ids=["authenticated", "failed"])
+def test_codec_auth_wait(auth):
+    """codec_auth_wait: after a codec layer's swaps (all of its groups) the
+    transfer waits for that layer's authentication and raises on failure, as
+    the reference's codec transfer asserts wait_auth(layer) == 0 before it
+    decodes (transport_codec.py:168-174); the layer index has moved on either
+    way.  A bf16 layer, or the option off, does not wait."""
+    shape = si.LayerShape(2, 64, codec_bits=4)
+    if auth == 0:
+        nt, rec, _ = run_transfer(41, 16, None, layer=5, shape=shape, codec_auth_wait=True, auth=auth)
+        assert rec.calls[-1] == ("wait", 5) and nt.layer == 6
+        assert [c[0] for c in rec.calls].count("wait") == 1
+        assert [c[0] for c in rec.calls[:-1]].count("swap") == 6  # three groups, K and V
+    else:
+        with pytest.raises(RuntimeError, match="Packed KV authentication failed"):
+            run_transfer(41, 16, None, layer=5, shape=shape, codec_auth_wait=True, auth=auth)
+    for sh, on in ((si.LayerShape(2, 64), True), (shape, False)):
+        _, rec, _ = run_transfer(41, 16, None, layer=5, shape=sh, codec_auth_wait=on, auth=-1)
+        assert not any(c[0] == "wait" for c in rec.calls)
