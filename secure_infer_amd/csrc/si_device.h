@@ -418,14 +418,15 @@ __device__ __forceinline__ void be_mulx(uint32_t a[4])
     a[0] = (a[0] >> 1) ^ ((0u - carry) & 0xe1000000u);
 }
 
-// z = x * y for per-lane x, y (memory byte order in and out), shared by three
-// threads: Shoup's 4-bit method with a per-lane table of the multiples v*y in
-// LDS.  Each thread writes its share of the table (entries v = c, c+3, ...
-// for c = 0..2; v = 0 is not stored: entry v >= 1 sits at
+// z = x * y for per-lane x, y (memory byte order in and out), shared by K
+// threads (K = 2 or 3): Shoup's 4-bit method with a per-lane table of the
+// multiples v*y in LDS.  Each thread writes its share of the table (entries
+// v = c, c+K, ... for c = 0..K-1; v = 0 is not stored: entry v >= 1 sits at
 // tbl[(v - 1) * stride + slot] and a shared zero word stands for v = 0), and
-// after a barrier each evaluates the nibbles j = c (mod 3) of x with its own
-// Horner chain (step x^12), then shifts by x^(4c).  XORing the three results
-// gives x * y; each chain is a third as long as one whole product's.
+// after a barrier each evaluates the nibbles j = c (mod K) of x with its own
+// Horner chain (step x^(4K)), then shifts by x^(4c).  XORing the K results
+// gives x * y; each chain is 1/K as long as one whole product's.
+template <int K>
 __device__ __forceinline__ void gh_table_share(const uint32_t y_mem[4], uint32_t c, uint4* tbl,
                                                uint32_t slot, uint32_t stride)
 {
@@ -437,8 +438,8 @@ __device__ __forceinline__ void gh_table_share(const uint32_t y_mem[4], uint32_t
     uint32_t m1[4] = {m2[0], m2[1], m2[2], m2[3]};
     be_mulx(m1);
 #pragma unroll
-    for (uint32_t i = 0; i < 6; ++i) {
-        const uint32_t v = c + 3u * i;
+    for (uint32_t i = 0; i < (16u + K - 1u) / K; ++i) {
+        const uint32_t v = c + uint32_t(K) * i;
         if (v != 0u && v < 16u) {
             const uint32_t s8 = 0u - ((v >> 3) & 1u), s4 = 0u - ((v >> 2) & 1u);
             const uint32_t s2 = 0u - ((v >> 1) & 1u), s1 = 0u - (v & 1u);
@@ -455,7 +456,7 @@ __device__ __forceinline__ void gh_table_share(const uint32_t y_mem[4], uint32_t
 template <int S>
 __device__ __forceinline__ void be_mulx_s(uint32_t a[4])
 {
-    static_assert(S == 4 || S == 12, "reduction fits the top word");
+    static_assert(S == 4 || S == 8 || S == 12, "reduction fits the top word");
     const uint32_t rem = a[3] & ((1u << S) - 1u);
     a[3] = __builtin_amdgcn_alignbit(a[2], a[3], S);
     a[2] = __builtin_amdgcn_alignbit(a[1], a[2], S);
@@ -467,14 +468,14 @@ __device__ __forceinline__ void be_mulx_s(uint32_t a[4])
 // Part C of x * y (C < K) for NS independent products at once (their
 // chains interleave): z[s] = XOR_{j = C mod K} T_s[nibble j of x[s]] * x^(4j),
 // Horner over those nibbles with step x^(4K).  K = 1 is the whole product,
-// K = 3 a third of it (gh_table_share's layout: entry v >= 1 at
+// K = 2 or 3 a half or a third of it (gh_table_share's layout: entry v >= 1 at
 // tbl[(v - 1) * stride + slot], `zero` for v = 0).
 template <int K, int C, int NS>
 __device__ __forceinline__ void gh_mul_part(const uint32_t (&x_mem)[NS][4], const uint4* const (&tbl)[NS],
                                             const uint4* zero, uint32_t slot, uint32_t stride,
                                             uint32_t (&z_mem)[NS][4])
 {
-    static_assert((K == 1 || K == 3) && C < K, "one or three parts");
+    static_assert((K == 1 || K == 2 || K == 3) && C < K, "one, two or three parts");
     constexpr int kTop = C + K * ((31 - C) / K);
     uint32_t xb[NS][4], a[NS][4];
 #pragma unroll

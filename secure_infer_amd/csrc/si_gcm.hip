@@ -16,7 +16,7 @@
 //   * GHASH: Horner with H^768 over the unit's rows (LDS tables), a move onto
 //     the segment's exponent grid (H^256 or H^512), and a placement multiply
 //     by H^((R - qb)*T + T - t) (qb = end row of the segment) shared by the
-//     three threads of position t.
+//     SI_U threads of position t.
 // Partials are XOR-reduced over the workgroup and then across workgroups with
 // device-scope atomics; a row count names the workgroup that completes a
 // record, which compares the tag in constant time, writes the status and, on
@@ -546,6 +546,27 @@ __device__ __forceinline__ RecView get_view(const uint4* src)
     return v;
 }
 
+// The SI_U units' products of position t (xs[u*T + t]) XORed together.
+__device__ __forceinline__ void unit_sum(const uint4* xs, uint32_t t, uint32_t out[4])
+{
+    static_assert(SI_U == 2 || SI_U == 3, "two or three units");
+    const uint4 a = xs[t], b = xs[SI_T + t];
+    const uint4 c = SI_U == 3 ? xs[2 * SI_T + t] : make_uint4(0, 0, 0, 0);
+    out[0] = xor3(a.x, b.x, c.x); out[1] = xor3(a.y, b.y, c.y);
+    out[2] = xor3(a.z, b.z, c.z); out[3] = xor3(a.w, b.w, c.w);
+}
+
+// Thread (u, t)'s part of the placement products of position t (the
+// nibbles j = u mod SI_U; gh_mul_part).
+template <int NS>
+__device__ __forceinline__ void place_part(uint32_t u, const uint32_t (&x)[NS][4], const uint4* const (&tb)[NS],
+                                           const uint4* zero, uint32_t t, uint32_t (&z)[NS][4])
+{
+    if (u == 0) gh_mul_part<SI_U, 0, NS>(x, tb, zero, t, SI_T, z);
+    else if (u == 1 || SI_U == 2) gh_mul_part<SI_U, 1, NS>(x, tb, zero, t, SI_T, z);
+    else gh_mul_part<SI_U, (SI_U == 3 ? 2 : 1), NS>(x, tb, zero, t, SI_T, z);
+}
+
 // Workgroup w owns a contiguous share of the records' concatenated row
 // sequence (laid out by the host so that a share that straddles two records,
 // which pays a second set of boundary rows and placements, takes fewer
@@ -619,12 +640,14 @@ __device__ __forceinline__ void gcm_records_body(const GcmCtx* __restrict__ ctx,
     if (tid < SI_T) {
         aes_fill_lds(aes, ctx->te0, tid);
     } else {
-        const uint32_t i = tid - SI_T;  // 0..511: one entry of each table
-        const uint4 a0 = ctx->gh4u[i], a1 = ctx->gh4u2[i], a2 = ctx->gh4[i], a3 = ctx->gh4b[i];
-        s_lds[i] = a0;
-        s_lds[512 + i] = a1;
-        s_lds[5120 + i] = a2;
-        s_lds[5632 + i] = a3;
+        // one entry of each table per thread (512 entries each)
+        for (uint32_t i = tid - SI_T; i < 512u; i += SI_NT - SI_T) {
+            const uint4 a0 = ctx->gh4u[i], a1 = ctx->gh4u2[i], a2 = ctx->gh4[i], a3 = ctx->gh4b[i];
+            s_lds[i] = a0;
+            s_lds[512 + i] = a1;
+            s_lds[5120 + i] = a2;
+            s_lds[5632 + i] = a3;
+        }
     }
 
     // This workgroup's share of the records' concatenated rows.
@@ -656,7 +679,7 @@ __device__ __forceinline__ void gcm_records_body(const GcmCtx* __restrict__ ctx,
     // segment 1 runs; both tables are built after the rows.
     if (nseg == 1 || pair) {
         const uint32_t z[4] = {zp0.x, zp0.y, zp0.z, zp0.w};
-        gh_table_share(z, u, ptab0, t, SI_T);
+        gh_table_share<SI_U>(z, u, ptab0, t, SI_T);
     } else if (u == 0) {
         s_zp[t] = zp0;
         s_zp[SI_T + t] = zp1;
@@ -733,40 +756,28 @@ __device__ __forceinline__ void gcm_records_body(const GcmCtx* __restrict__ ctx,
     if (pair) xs0[u * SI_T + t] = p0;
     __syncthreads();
     uint32_t w[2][4];
-    {
-        const uint4 a = xs[t], b = xs[SI_T + t], c = xs[2 * SI_T + t];
-        w[1][0] = xor3(a.x, b.x, c.x); w[1][1] = xor3(a.y, b.y, c.y);
-        w[1][2] = xor3(a.z, b.z, c.z); w[1][3] = xor3(a.w, b.w, c.w);
-    }
+    unit_sum(xs, t, w[1]);
     uint32_t q[2][4];
     if (nseg == 1) {  // uniform over the workgroup; the table is ready
         const uint32_t(&x1)[1][4] = reinterpret_cast<const uint32_t(&)[1][4]>(w[1]);
         uint32_t(&o1)[1][4] = reinterpret_cast<uint32_t(&)[1][4]>(q[1]);
         const uint4* const tb[1] = {ptab0};
-        if (u == 0) gh_mul_part<3, 0, 1>(x1, tb, s_zero, t, SI_T, o1);
-        else if (u == 1) gh_mul_part<3, 1, 1>(x1, tb, s_zero, t, SI_T, o1);
-        else gh_mul_part<3, 2, 1>(x1, tb, s_zero, t, SI_T, o1);
+        place_part<1>(u, x1, tb, s_zero, t, o1);
     } else {
         const uint4* const s_w0 = pair ? xs0 : s_p0;
-        {
-            const uint4 a = s_w0[t], b = s_w0[SI_T + t], c = s_w0[2 * SI_T + t];
-            w[0][0] = xor3(a.x, b.x, c.x); w[0][1] = xor3(a.y, b.y, c.y);
-            w[0][2] = xor3(a.z, b.z, c.z); w[0][3] = xor3(a.w, b.w, c.w);
-        }
+        unit_sum(s_w0, t, w[0]);
         if (!pair) {  // uniform over the workgroup
             const uint4 z0 = s_zp[t], z1 = s_zp[SI_T + t];
             __syncthreads();  // s_p0 and s_zp are read; the region takes segment 0's table
             {
                 const uint32_t za[4] = {z0.x, z0.y, z0.z, z0.w}, zb[4] = {z1.x, z1.y, z1.z, z1.w};
-                gh_table_share(za, u, ptab0, t, SI_T);
-                gh_table_share(zb, u, ptab1, t, SI_T);
+                gh_table_share<SI_U>(za, u, ptab0, t, SI_T);
+                gh_table_share<SI_U>(zb, u, ptab1, t, SI_T);
             }
             __syncthreads();
         }
         const uint4* const tb[2] = {ptab0, pair ? ptab0 : ptab1};
-        if (u == 0) gh_mul_part<3, 0, 2>(w, tb, s_zero, t, SI_T, q);
-        else if (u == 1) gh_mul_part<3, 1, 2>(w, tb, s_zero, t, SI_T, q);
-        else gh_mul_part<3, 2, 2>(w, tb, s_zero, t, SI_T, q);
+        place_part<2>(u, w, tb, s_zero, t, q);
         wave_xor4_to63(q[0]);
         if ((tid & 63u) == 63u) s_c0[tid >> 6] = make_uint4(q[0][0], q[0][1], q[0][2], q[0][3]);
     }
