@@ -525,8 +525,12 @@ int secure_infer_h2d_prefetch_group(si_session* session, const void* k_base, con
 /* secure_infer.cpp:6085-6137: the H2D ledger.  With
  * SECURE_INFER_H2D_PROFILE=<path> every launch appends one CSV row (layer,
  * kind -- 0 K, 1 V, 2 both --, records, record_bytes, source, seal_us,
- * h2d_copy_us, kernel_us) once its work is complete; flush writes the rows
- * of completed launches, drain waits for every pending launch first. */
+ * h2d_copy_us, kernel_us) once its work is complete; with
+ * SECURE_INFER_H2D_PROFILE_RECORDS=1 as well, one row per record in the
+ * reference's per-copy columns (secure_infer.cpp:1846-1847): the record's
+ * own seal time and prefetch hit, its launch's enqueue times and device
+ * phases.  Flush writes the rows of completed launches, drain waits for
+ * every pending launch first. */
 void secure_infer_flush_completed_h2d_profile(void);
 void secure_infer_drain_h2d_profile_after_job(void);
 /* No reference counterpart: pauses (1) or resumes (0) the ledger's rows and

@@ -296,12 +296,16 @@ bool tamper_h2d(uint32_t layer, uint32_t kind, int64_t host_block)
 
 struct Prefetch;
 
-// One ledger row of an H2D swap, written once its slot's work is complete.
+// One ledger row of an H2D launch (or, in records mode, one row per record),
+// written once its slot's work is complete.
 struct ProfileRow {
     bool pending = false;
     uint32_t layer = 0, kind = 0, n = 0, source = 0;  // source: 0 sealed on demand, 1 prefetched, 2 waited
-    uint64_t bytes = 0;
+    uint64_t bytes = 0, stride = 0;
     double seal_us = 0;
+    double copy_enqueue_us = 0, kernel_enqueue_us = 0;  // host time issuing the launch's copies / kernels
+    std::vector<float> rec_seal_us;       // records mode: each record's own seal, device order
+    std::vector<uint8_t> rec_prefetched;  // ... and whether it was sealed ahead of demand
 };
 
 // A pinned host buffer mirrored by a device buffer of the same size, plus
@@ -529,6 +533,18 @@ bool g_profile_checked = false;
 
 std::atomic<bool> g_profile_paused{false};
 
+// SECURE_INFER_H2D_PROFILE_RECORDS=1: one row per record in the reference's
+// per-copy column set (secure_infer.cpp:1846-1847, 5649-5690) instead of one
+// row per launch.
+bool profile_records()
+{
+    static const bool on = [] {
+        const char* e = std::getenv("SECURE_INFER_H2D_PROFILE_RECORDS");
+        return e && std::atoi(e) != 0;
+    }();
+    return on;
+}
+
 bool profile_on()
 {
     if (g_profile_paused.load(std::memory_order_relaxed)) return false;
@@ -538,7 +554,12 @@ bool profile_on()
         const char* path = std::getenv("SECURE_INFER_H2D_PROFILE");
         if (path && *path) {
             g_profile = std::fopen(path, "a");
-            if (g_profile)
+            if (g_profile && profile_records())
+                std::fprintf(g_profile,
+                             "direction,bytes,aligned_bytes,total_us,cpu_crypto_us,device_pipeline_us,host_wait_us,"
+                             "copy_enqueue_us,kernel_enqueue_us,h2d_device_us,kernel_execute_us,d2d_device_us,"
+                             "device_total_us,device_timing_valid,crypto_mode,cpu_prediction_hit\n");
+            else if (g_profile)
                 std::fprintf(g_profile, "layer,kind,records,record_bytes,source,seal_us,h2d_copy_us,kernel_us\n");
         }
     }
@@ -550,12 +571,30 @@ void profile_retire(Mirror& sl)
 {
     if (!sl.row.pending) return;
     sl.row.pending = false;
-    float copy_ms = -1.0f, kernel_ms = -1.0f;
-    (void)hipEventElapsedTime(&copy_ms, sl.p_c0, sl.p_c1);
-    (void)hipEventElapsedTime(&kernel_ms, sl.p_k0, sl.p_k1);
+    float copy_ms = -1.0f, kernel_ms = -1.0f, total_ms = -1.0f;
+    const bool valid = hipEventElapsedTime(&copy_ms, sl.p_c0, sl.p_c1) == hipSuccess &&
+                       hipEventElapsedTime(&kernel_ms, sl.p_k0, sl.p_k1) == hipSuccess &&
+                       hipEventElapsedTime(&total_ms, sl.p_c0, sl.p_k1) == hipSuccess;
     static const char* kSource[] = {"sealed", "prefetched", "prefetch_waited"};
     std::lock_guard<std::mutex> g(g_profile_lock);
-    if (g_profile)
+    if (g_profile && profile_records()) {
+        // Per record: its own seal on the host; the launch that carried it
+        // (every record of it alike) for the enqueue times and the device
+        // phases (copy start to copy end, kernel, copy start to kernel end).
+        // No device-to-device stage follows the kernel, and a swap that
+        // finds its records sealed ahead waits on nothing else.
+        auto us = [](double x) { return static_cast<unsigned long long>(x < 0 ? 0 : x + 0.5); };
+        const double dev = valid ? double(total_ms) * 1e3 : 0.0;
+        for (size_t r = 0; r < sl.row.rec_seal_us.size(); ++r) {
+            const double seal = sl.row.rec_seal_us[r];
+            std::fprintf(g_profile, "H2D,%llu,%llu,%llu,%llu,%llu,0,%llu,%llu,%llu,%llu,0,%llu,%d,0,%d\n",
+                         static_cast<unsigned long long>(sl.row.bytes), static_cast<unsigned long long>(sl.row.stride),
+                         us(seal + sl.row.copy_enqueue_us + sl.row.kernel_enqueue_us + dev), us(seal), us(dev),
+                         us(sl.row.copy_enqueue_us), us(sl.row.kernel_enqueue_us),
+                         us(valid ? double(copy_ms) * 1e3 : 0.0), us(valid ? double(kernel_ms) * 1e3 : 0.0), us(dev),
+                         valid ? 1 : 0, int(sl.row.rec_prefetched[r]));
+        }
+    } else if (g_profile)
         std::fprintf(g_profile, "%u,%u,%u,%llu,%s,%.1f,%.1f,%.1f\n", sl.row.layer, sl.row.kind, sl.row.n,
                      static_cast<unsigned long long>(sl.row.bytes), kSource[sl.row.source % 3], sl.row.seal_us,
                      double(copy_ms) * 1e3, double(kernel_ms) * 1e3);
@@ -622,6 +661,7 @@ struct Prefetch {
     bool started = false;
     std::chrono::steady_clock::time_point first_start{};
     double seal_us = 0;  // first sealing task's start to the last one's end
+    std::vector<float> rec_us;  // each record's seal (its own task)
     ~Prefetch();
 };
 
@@ -718,6 +758,7 @@ std::shared_ptr<Prefetch> new_prefetch(si_session* s, const si_internal::Session
     pf->tag_off = tag_offset(bytes);
     pf->host_blocks.resize(n);
     for (uint32_t r = 0; r < n; ++r) pf->host_blocks[r] = mapping[2 * r];
+    pf->rec_us.assign(n, 0.0f);
     pf->host = host;
     return pf;
 }
@@ -742,8 +783,10 @@ void queue_seals(const std::shared_ptr<Prefetch>& pf, std::vector<std::function<
             }
             bool ok = true;
             const int64_t hb = pf->host_blocks[r];
+            const auto ts = std::chrono::steady_clock::now();
             seal_record(pf->keys, pf->host_base + uint64_t(hb) * pf->host_block_bytes, pf->bytes, pf->tag_off,
                         pf->t0 + r, pf->host + uint64_t(r) * pf->stride, pf->layer, pf->kind, hb, ok);
+            pf->rec_us[r] = float(us_since(ts));
             std::lock_guard<std::mutex> g(pf->m);
             if (!ok) pf->failed = true;
             if (++pf->done == pf->tasks) {
@@ -865,6 +908,7 @@ struct H2DPart {
     uint64_t t0 = 0;               // ticket of its first record
     uint32_t source = 0;           // 0 sealed on demand, 1 prefetched, 2 prefetch waited for
     double seal_us = 0;
+    std::vector<float> rec_us;     // ledger records mode: each record's seal
     std::shared_ptr<Prefetch> pf;
     std::shared_ptr<Observed> ob;  // null when not observed
 };
@@ -1030,6 +1074,7 @@ int flush_launch()
         return -1;
     };
     if (prof && hipEventRecord(sl.p_c0, L->ring->copy) != hipSuccess) return fail();
+    const auto t_copy = std::chrono::steady_clock::now();
     // A launch of exactly one group prefetch (its K half, then its V half, as
     // large as the launch and with one ticket run), or of exactly one layer
     // prefetch: the prefetch buffer holds the records in device order
@@ -1073,6 +1118,7 @@ int flush_launch()
                            L->ring->copy) != hipSuccess)
             return fail();
     }
+    const double copy_enqueue_us = us_since(t_copy);
     if ((prof && hipEventRecord(sl.p_c1, L->ring->copy) != hipSuccess) ||
         hipEventRecord(sl.ev_a, L->ring->copy) != hipSuccess || hipStreamWaitEvent(L->stream, sl.ev_a, 0) != hipSuccess)
         return fail();
@@ -1099,7 +1145,9 @@ int flush_launch()
     d.status_out = L->status ? L->status->dev : nullptr;
     d.flags = reload_flags();
     if (prof && hipEventRecord(sl.p_k0, L->stream) != hipSuccess) return fail();
+    const auto t_kernel = std::chrono::steady_clock::now();
     if (secure_infer_gpu_reload_layer(L->stream, L->s, &d) != 0) return fail();
+    const double kernel_enqueue_us = us_since(t_kernel);
     launched = true;
     if ((prof && hipEventRecord(sl.p_k1, L->stream) != hipSuccess) ||
         hipEventRecord(sl.ev_b, L->stream) != hipSuccess ||
@@ -1116,6 +1164,20 @@ int flush_launch()
         sl.row.source = L->parts[0].source;
         sl.row.seal_us = 0;
         for (const H2DPart& p : L->parts) sl.row.seal_us += p.seal_us;
+        sl.row.stride = L->stride;
+        sl.row.copy_enqueue_us = copy_enqueue_us;
+        sl.row.kernel_enqueue_us = kernel_enqueue_us;
+        sl.row.rec_seal_us.clear();
+        sl.row.rec_prefetched.clear();
+        if (profile_records()) {
+            for (size_t i : order) {
+                const H2DPart& p = L->parts[i];
+                for (uint32_t r = 0; r < p.n; ++r) {
+                    sl.row.rec_seal_us.push_back(r < p.rec_us.size() ? p.rec_us[r] : 0.0f);
+                    sl.row.rec_prefetched.push_back(p.source != 0 ? 1 : 0);
+                }
+            }
+        }
     }
     release_slot(L->ring, L->slot, true);
     if (L->observe) {
@@ -1218,10 +1280,12 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
     part.kind = kind;
     part.ids0 = L->slot_ids.size();
     part.source = source;
+    const bool prof_records = profile_records();
     if (pf) {
         part.src = pf->host;
         part.t0 = pf->t0;
         part.seal_us = pf->seal_us;
+        if (prof_records) part.rec_us = pf->rec_us;
         part.pf = pf;
     } else {
         const auto ts = std::chrono::steady_clock::now();
@@ -1234,11 +1298,14 @@ int h2d_swap_impl(hipStream_t stream, si_session* s, const void* host_base, uint
         uint8_t* rows = sl.host + size_t(part.r0) * stride;
         const uint64_t t0 = part.t0;
         std::atomic<int> bad{0};
+        if (prof_records) part.rec_us.assign(n, 0.0f);
         Pool::get().parallel_for(n, [&](size_t r) {
             const int64_t hb = mapping[2 * r];
             bool ok = true;
+            const auto tr = std::chrono::steady_clock::now();
             seal_record(keys, static_cast<const uint8_t*>(host_base) + uint64_t(hb) * host_block_bytes, bytes,
                         tag_off, t0 + r, rows + r * stride, layer, kind, hb, ok);
+            if (prof_records) part.rec_us[r] = float(us_since(tr));
             if (!ok) bad.store(1);
         });
         if (bad.load()) return -1;

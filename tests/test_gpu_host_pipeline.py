@@ -864,6 +864,37 @@ def test_h2d_profile_ledger(tmp_path):
         assert float(r[5]) > 0 and float(r[6]) > 0 and float(r[7]) > 0
 
 
+def test_h2d_profile_ledger_records(tmp_path):
+    """SECURE_INFER_H2D_PROFILE_RECORDS=1: one row per record in the
+    reference's per-copy column set (secure_infer.cpp:1846-1847, 5649-5690):
+    'H2D', payload and wire bytes, the record's own seal time, the enqueue
+    times and device phases of the launch that carried it, and whether it
+    was sealed ahead of demand (cpu_prediction_hit)."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    csv = tmp_path / "h2d_records.csv"
+    env = dict(os.environ, SECURE_INFER_H2D_PROFILE=str(csv), SECURE_INFER_H2D_PROFILE_RECORDS="1")
+    out = subprocess.run([sys.executable, "-c", LEDGER_SCRIPT, str(Path(__file__).resolve().parent.parent)],
+                         env=env, capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0 and "done" in out.stdout, out.stderr[-2000:]
+    lines = csv.read_text().strip().splitlines()
+    assert lines[0] == ("direction,bytes,aligned_bytes,total_us,cpu_crypto_us,device_pipeline_us,host_wait_us,"
+                        "copy_enqueue_us,kernel_enqueue_us,h2d_device_us,kernel_execute_us,d2d_device_us,"
+                        "device_total_us,device_timing_valid,crypto_mode,cpu_prediction_hit")
+    rows = [[int(x) if x.isdigit() else x for x in l.split(",")] for l in lines[1:]]
+    nbytes = 128 * 2 * 128 * 2
+    assert len(rows) == 12  # two layers of 3 K and 3 V records
+    for r in rows:
+        assert r[0] == "H2D" and r[1] == nbytes and r[2] == si.wire_stride(nbytes)
+        assert r[13] == 1 and r[14] == 0 and r[6] == 0 and r[11] == 0
+        assert r[4] > 0 and r[9] > 0 and r[10] > 0 and r[12] >= r[10] and r[5] == r[12]
+        assert r[3] >= r[4] + r[12] - 1  # rounding of the summed parts
+    # layer 0 was sealed ahead of demand, layer 1 on demand
+    assert sorted(r[15] for r in rows) == [0] * 6 + [1] * 6
+
+
 @pytest.mark.parametrize("shots", [1, 2], ids=["repaired", "final"])
 def test_codec_auth_wait(shots):
     """NativeTransfer(codec_auth_wait=True) over an int4 layer whose V record
