@@ -35,12 +35,19 @@ def build(san: str) -> Path:
     return OUT / f"host_stress_{san}"
 
 
-@pytest.mark.parametrize("san,env,rounds", [
-    ("thread", {"TSAN_OPTIONS": "halt_on_error=1 second_deadlock_stack=1"}, 3),
-    ("address", {"ASAN_OPTIONS": "halt_on_error=1:detect_leaks=1"}, 3),
-])
-def test_host_runtime_under_sanitizer(san, env, rounds):
+@pytest.mark.parametrize("san,env,rounds,ledger", [
+    ("thread", {"TSAN_OPTIONS": "halt_on_error=1 second_deadlock_stack=1"}, 3, False),
+    ("address", {"ASAN_OPTIONS": "halt_on_error=1:detect_leaks=1"}, 3, False),
+    # the H2D ledger in records mode on: its rows are retired as ring slots
+    # are reused, from every thread that launches
+    ("thread", {"TSAN_OPTIONS": "halt_on_error=1 second_deadlock_stack=1",
+                "SECURE_INFER_H2D_PROFILE_RECORDS": "1"}, 2, True),
+], ids=["thread", "address", "thread_ledger"])
+def test_host_runtime_under_sanitizer(san, env, rounds, ledger, tmp_path):
     exe = build(san)
+    env = dict(env)
+    if ledger:
+        env["SECURE_INFER_H2D_PROFILE"] = str(tmp_path / "ledger.csv")
     r = subprocess.run([str(exe), str(rounds)], capture_output=True, text=True, timeout=600,
                        env={**os.environ, **env})
     report = r.stdout + r.stderr
@@ -48,6 +55,10 @@ def test_host_runtime_under_sanitizer(san, env, rounds):
         "LeakSanitizer" not in report, report[-4000:]
     assert r.returncode == 0, report[-4000:]
     assert f"HOST_STRESS_OK rounds={rounds}" in r.stdout
+    if ledger:
+        lines = (tmp_path / "ledger.csv").read_text().splitlines()
+        assert lines[0].startswith("direction,bytes,aligned_bytes,total_us,cpu_crypto_us") and len(lines) > 1
+        assert all(l.startswith("H2D,") and len(l.split(",")) == 16 for l in lines[1:])
 
 
 @pytest.mark.parametrize("abort", [False, True], ids=["batch_fails", "process_aborts"])
