@@ -640,14 +640,17 @@ __device__ __forceinline__ void gcm_records_body(const GcmCtx* __restrict__ ctx,
     if (tid < SI_T) {
         aes_fill_lds(aes, ctx->te0, tid);
     } else {
-        // one entry of each table per thread (512 entries each)
-        for (uint32_t i = tid - SI_T; i < 512u; i += SI_NT - SI_T) {
+        // the 512 entries of each table over the other threads
+        auto fill = [&](uint32_t i) {
             const uint4 a0 = ctx->gh4u[i], a1 = ctx->gh4u2[i], a2 = ctx->gh4[i], a3 = ctx->gh4b[i];
             s_lds[i] = a0;
             s_lds[512 + i] = a1;
             s_lds[5120 + i] = a2;
             s_lds[5632 + i] = a3;
-        }
+        };
+        if constexpr (SI_NT - SI_T == 512) fill(tid - SI_T);
+        else
+            for (uint32_t i = tid - SI_T; i < 512u; i += SI_NT - SI_T) fill(i);
     }
 
     // This workgroup's share of the records' concatenated rows.
