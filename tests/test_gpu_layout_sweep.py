@@ -7,7 +7,9 @@ Every reload is checked record by record against OpenSSL-sealed records
 (statuses, fail count, slot bytes, untouched slots); every writeback's
 ciphertext and tags against OpenSSL over the gathered slot bytes.  The
 shapes are run twice in one thread, interleaved, so a layout reused from the
-library's per-thread layout cache must be the one of the current shape.
+library's per-thread layout cache must be the one of the current shape.  A
+seeded random sweep adds shapes and layout knobs (minimum rows per share,
+straddle cost) that no fixed list names.
 Byte and integer work: all comparisons are bit-exact.
 """
 import numpy as np
@@ -109,3 +111,31 @@ def test_layout_sweep_matches_openssl(direction):
             print(f"{direction} rep {rep}: {nrec} records x {n} B", flush=True)
             case(sess, rng, nrec, n, ticket)
             ticket += nrec
+
+
+@pytest.mark.parametrize("direction", ["reload", "writeback"])
+def test_random_layouts_match_openssl(direction):
+    """Seeded random shapes and layout knobs beyond the hand-picked ones:
+    record counts from one to past four per CU, record sizes from one byte
+    to past four rows (most with a partial last block), the minimum rows per
+    share (1 to 8) and the straddle cost (0 to 13), so shares straddle, pair
+    up or run in rounds in combinations no fixed list names.  Each case
+    against OpenSSL as above."""
+    rng = np.random.default_rng(7300 if direction == "reload" else 7400)
+    sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=70000)
+    case = _reload_case if direction == "reload" else _writeback_case
+    ticket = 1
+    try:
+        for i in range(14):
+            nrec = int(rng.choice([1, 2, 7, 64, 255, 300, 511, 640, 1030]))
+            n = int(rng.integers(1, 70000)) if nrec <= 300 else int(rng.integers(1, 9000))
+            chunk, straddle = int(rng.choice([1, 2, 3, 5, 8])), int(rng.choice([0, 2, 6, 13]))
+            print(f"{direction} case {i}: {nrec} records x {n} B, chunk rows {chunk}, straddle {straddle}",
+                  flush=True)
+            si.set_chunk_rows(chunk)
+            si.set_straddle_rows(straddle)
+            case(sess, rng, nrec, n, ticket)
+            ticket += nrec
+    finally:
+        si.set_chunk_rows(si.gcm.DEFAULT_CHUNK_ROWS)
+        si.set_straddle_rows(si.gcm.DEFAULT_STRADDLE_ROWS)
