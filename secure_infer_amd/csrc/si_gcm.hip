@@ -882,9 +882,10 @@ void gcm_records_kernel(const GcmCtx* __restrict__ ctx, RecBatch batch, Sched sc
 // staging row) only if that status is 1, and writes zeros there otherwise:
 // the reference's order, tag first, then masked output
 // (ghash.aicpu:623-648), so no unverified byte reaches the destination.
-// A slot id out of range with no staging touches nothing.  Threads take
-// blocks 256 apart, so the counter-mode cache of rounds 1-2 applies while
-// counter bytes 12..13 stay fixed over the workgroup's range.
+// A slot id out of range with no staging touches nothing.  A thread's
+// blocks lie SI_RELEASE_THREADS apart, a multiple of 256, so its counter's
+// low byte never changes, and the counter-mode cache of rounds 1-2 applies
+// while counter bytes 12..13 stay fixed over the workgroup's range.
 __device__ __forceinline__ void release_body(const GcmCtx* __restrict__ ctx, const RecBatch& b, uint64_t bytes,
                                              uint32_t chunk, int aligned, const uint32_t* gate)
 {
@@ -1213,7 +1214,7 @@ hipError_t launch_release(hipStream_t stream, const GcmCtx* ctx, const RecBatch&
 {
     if (nrec == 0) return hipSuccess;
     // Blocks per workgroup: a multiple of the block stride (the counter-mode
-    // cache needs each thread's blocks 256 apart), at least 8 per thread.
+    // cache needs each thread's blocks a multiple of 256 apart), 8 per thread.
     const uint64_t nb = (bytes + 15) / 16;
     const uint32_t chunk = 8u * SI_RELEASE_THREADS;
     const dim3 grid(uint32_t((nb + chunk - 1) / chunk), nrec), block(SI_RELEASE_THREADS);
