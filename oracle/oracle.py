@@ -1,7 +1,7 @@
 """Python face of the CPU oracle (test infrastructure only).
 
 Loaded by tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` as the checker.  Product code under ``secure_infer_amd/`` never
+``bench.py`` to check results against.  Product code under ``secure_infer_amd/`` never
 imports this module.
 
 * ``lib``      -- ctypes bindings of ``oracle/si_oracle.c`` (FIPS-197 AES-128,

@@ -2,7 +2,7 @@
  * CPU oracle for the authenticated KV reload / writeback path.
  *
  * TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py as the checker.  The product library never
+ * cpu_baseline leg of bench.py, to check results against.  The product library never
  * links or calls it.
  *
  * Written from the specifications (FIPS-197, NIST SP 800-38D) and from the

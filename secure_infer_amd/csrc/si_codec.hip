@@ -150,7 +150,7 @@ __device__ __forceinline__ void dequant_scatter_body(const CodecBatch& b, uint32
         // Non-temporal stores: the slots are not read again in this launch,
         // and a kernel that ends with the layer's bf16 output dirty in L2
         // holds the next launch back while that is written back (MI355X,
-        // ABBA x 2 on one box, layer time: int4 Qwen2.5-7B 24.2 -> 22.7 us,
+        // ABBA x 2 on one GPU, layer time: int4 Qwen2.5-7B 24.2 -> 22.7 us,
         // int8 Llama-3-8B 39.3 -> 39.5 us; write-through stores of the two
         // interleaved halves: 32.0 / 56.9 us).
         u32x4* dst = reinterpret_cast<u32x4*>(slot + uint64_t(e0) * 2u);

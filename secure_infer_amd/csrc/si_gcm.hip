@@ -280,7 +280,7 @@ __device__ __forceinline__ void keystream_block(const uint32_t* aes, AesLane lan
 // keystreams are formed (the hand-pipelined pair step); encrypt hashes the
 // ciphertext it has just made, after its keystreams.  (Encrypt folding each
 // pair's ciphertext into the next pair's pipelined step measured slower on
-// MI355X: 70B int4 writeback 86.2 vs 86.8 us per layer, ABBA on one box.)
+// MI355X: 70B int4 writeback 86.2 vs 86.8 us per layer, ABBA on one GPU.)
 template <int kMode, bool kCached, int kRows>
 __device__ __forceinline__ void rows_body(const RecView& v, __amdgpu_buffer_rsrc_t dst, const uint4* gh,
                                           const uint4* gh2, const uint32_t* aes, AesLane lane,

@@ -538,7 +538,7 @@ class NativeTransfer:
       returns once the work is queued.  With ``pipeline_seal`` (default) the
       layer's seals are queued on the worker pool first, so later parts seal
       while earlier parts are copied (the reference's CPU ciphertext
-      prefetch, secure_infer.cpp:3264-3710; MI355X box, 16 host CPUs, groups
+      prefetch, secure_infer.cpp:3264-3710; one MI355X, 16 host CPUs, groups
       of 16 blocks: 41-KB int4 records 545 -> 406 us per 28-layer-model layer
       end to end, 256-KB bf16 records 831 -> 553 us).  A layer already sealed
       with ``prefetch_kv_transfer`` is not sealed again.

@@ -1,6 +1,6 @@
 """Writes tests/golden/codec_decode_vectors.npz by running the REFERENCE's
 decode (secure_infer/kv_offload/optimized_decode.py:5-26, torch-only) on the
-CPU in this build container.
+CPU of the development container, where the reference's sources are present.
 
 Inputs are packets made by the oracle's restated encoder
 (transport_codec.py:22-42 cannot be imported: its module imports vLLM) from

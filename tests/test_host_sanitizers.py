@@ -18,7 +18,7 @@ batch, a session destroyed while its prefetches are still being sealed, and a
 destroy refused while another thread holds the session.  Every result is
 checked against the host data, and the sanitizers stop at their first report.
 A race planted in a copy of the driver (the cache read before the layer's
-wait) is reported by this build, so a clean run means something."""
+wait) is reported by the sanitizer build, so a clean run means something."""
 import os
 import subprocess
 from pathlib import Path

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/) before results are checked against it.
 
 * FIPS-197 and SP 800-38D / McGrew-Viega published known answers.
 * OpenSSL (the reference's host AES-128-GCM) fixtures in tests/golden/.
