@@ -595,6 +595,18 @@ int secure_infer_gpu_set_chunk_rows(int jmax);
  * shares straddle wherever a record ends inside one.  No reference
  * counterpart; used by the tests to force straddling shares. */
 int secure_infer_gpu_set_straddle_rows(int rows);
+/* Inspection: the share layout a layer launch of nrec records of `bytes`
+ * payload and `aad_bytes` AAD bytes would use on a device with `cus` compute
+ * units (1..768) under the current tuning.  The host computes it alone; no
+ * device call is made.  info_out[0..4]: workgroups W, rows R per record
+ * (256 GHASH blocks each), 1 if the W shares are laid out one by one
+ * (their boundaries in the records' concatenated rows go to starts_out[0..W],
+ * which needs cap >= W + 1) or 0 for W equal shares, 1 if every workgroup
+ * takes two whole records, 1 if a record's first row also holds ciphertext.
+ * Returns 0, or -1 on invalid arguments.  No reference counterpart; used by
+ * the tests to check the layout's invariants over many shapes. */
+int secure_infer_gpu_layout(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, uint32_t cus,
+                            uint32_t* info_out, uint32_t* starts_out, uint32_t cap);
 
 #ifdef __cplusplus
 }

@@ -109,6 +109,7 @@ SIGNATURES = {
     "secure_infer_gpu_version": ([], ct.c_char_p),
     "secure_infer_gpu_set_chunk_rows": ([_i], _i),
     "secure_infer_gpu_set_straddle_rows": ([_i], _i),
+    "secure_infer_gpu_layout": ([_u32, _u64, _u64, _u32, _v, _v, _u32], _i),
 }
 
 _lib: ct.CDLL | None = None

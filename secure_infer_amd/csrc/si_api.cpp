@@ -312,13 +312,14 @@ std::unique_ptr<DevCtx> build_ctx(const uint8_t key[16], const uint8_t h[16], ui
     return out;
 }
 
-int g_min_rows = 3;
+// Layout knobs (set by the tuning calls, read by every launch's layout).
+std::atomic<int> g_min_rows{3};
 // Cost, in rows, of a share that straddles two records (its second set of
 // boundary rows, the second placement table and the two-product shares);
 // MI355X, bf16 Llama-3-8B layer: 35.1 / 34.8 / 32.2 / 32.2 / 32.6 / 32.7 /
 // 33.9 us per layer at 2 / 4 / 6 / 7 / 8 / 10 / 13 (int4 Qwen2.5-7B: 35.8 us
 // at 4, 26.6 at 2 and 6..13; int8 and the 70B writeback flat from 6 to 10).
-uint32_t g_straddle_rows = 6;
+std::atomic<uint32_t> g_straddle_rows{6};
 // Fixed cost of a record-kernel workgroup, in rows (MI355X: set-up ~3.2 us,
 // placement ~1.5 us and finalisation ~0.35 us at ~1 us per row per CU), and
 // whether shares of two whole records may be laid out.
@@ -344,7 +345,8 @@ uint32_t cu_count()
 // The rows cover AAD || C; the length block L, the last block of the GHASH
 // input, adds L * H to every record's sum (the same for the whole batch), and
 // the kernel's placement exponents count one more for it.
-static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes)
+static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, uint64_t cus,
+                                     int min_rows, uint32_t straddle)
 {
     si::Sched s{};
     s.nrec = nrec;
@@ -362,8 +364,7 @@ static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad
     // least nrec of them (rounded to whole rounds of one per CU) so that no
     // share spans more than R rows, i.e. two records at most.
     const uint64_t G = uint64_t(nrec) * s.rows;
-    const uint64_t cus = cu_count();
-    uint64_t w = (G + uint64_t(g_min_rows) - 1) / uint64_t(g_min_rows);
+    uint64_t w = (G + uint64_t(min_rows) - 1) / uint64_t(min_rows);
     if (w > cus) w = cus;
     if (w < nrec) w = (uint64_t(nrec) + cus - 1) / cus * cus;
     if (w > G) w = G;
@@ -374,7 +375,7 @@ static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad
         // continues into the next one only if it still gains rows after
         // paying the straddle cost Z (boundary rows, a second placement);
         // T is the least that fits W shares.
-        const uint32_t R = s.rows, Z = g_straddle_rows;
+        const uint32_t R = s.rows, Z = straddle;
         auto lay = [&](uint32_t T, bool store) -> uint64_t {
             uint64_t n = 0, r = 0, q = 0;
             if (store) s.starts[0] = 0;
@@ -449,8 +450,8 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, DevCtx& 
     k.aad_bytes = aad_bytes;
     k.nrec = nrec;
     k.cus = cu_count();
-    k.min_rows = uint32_t(g_min_rows);
-    k.straddle = g_straddle_rows;
+    k.min_rows = uint32_t(g_min_rows.load(std::memory_order_relaxed));
+    k.straddle = g_straddle_rows.load(std::memory_order_relaxed);
     k.fixed = g_wg_fixed_rows;
     k.pair = g_pair_records ? 1u : 0u;
     if (!cache) cache.reset(new Entry[kEntries]);
@@ -461,7 +462,7 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, DevCtx& 
     if (hit >= 0) {
         s = cache[hit].s;
     } else {
-        s = make_sched_uncached(nrec, bytes, aad_bytes);
+        s = make_sched_uncached(nrec, bytes, aad_bytes, k.cus, int(k.min_rows), k.straddle);
         cache[next].k = k;
         cache[next].s = s;
         next = (next + 1) % kEntries;
@@ -1735,14 +1736,34 @@ int secure_infer_recovery_wait_job_authentication(uint64_t job_id)
 int secure_infer_gpu_set_chunk_rows(int jmax)
 {
     if (jmax < 1 || jmax > 256) return -1;
-    g_min_rows = jmax;
+    g_min_rows.store(jmax, std::memory_order_relaxed);
     return 0;
 }
 
 int secure_infer_gpu_set_straddle_rows(int rows)
 {
     if (rows < 0 || rows > 256) return -1;
-    g_straddle_rows = uint32_t(rows);
+    g_straddle_rows.store(uint32_t(rows), std::memory_order_relaxed);
+    return 0;
+}
+
+int secure_infer_gpu_layout(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, uint32_t cus, uint32_t* info_out,
+                            uint32_t* starts_out, uint32_t cap)
+{
+    if (!info_out || nrec == 0 || bytes == 0 || bytes > SI_MAX_RECORD_BYTES || aad_bytes > SI_MAX_RECORD_BYTES || cus == 0 ||
+        cus > SI_MAX_WG)
+        return -1;
+    const si::Sched s = make_sched_uncached(nrec, bytes, aad_bytes, cus, g_min_rows.load(std::memory_order_relaxed),
+                                            g_straddle_rows.load(std::memory_order_relaxed));
+    info_out[0] = s.nwg;
+    info_out[1] = s.rows;
+    info_out[2] = s.use_starts;
+    info_out[3] = s.pairs;
+    info_out[4] = s.ek_row0;
+    if (s.use_starts) {
+        if (!starts_out || cap < s.nwg + 1) return -1;
+        memcpy(starts_out, s.starts, (size_t(s.nwg) + 1) * sizeof(uint32_t));
+    }
     return 0;
 }
 
