@@ -12,6 +12,8 @@ seeded random sweep adds shapes and layout knobs (minimum rows per share,
 straddle cost) that no fixed list names.
 Byte and integer work: all comparisons are bit-exact.
 """
+import functools
+
 import numpy as np
 import pytest
 import torch
@@ -42,7 +44,7 @@ def _host(t):
     return t.cpu().numpy()
 
 
-def _reload_case(sess, rng, nrec, n, ticket0):
+def _reload_case(sess, rng, nrec, n, ticket0, strict=False):
     n_k = nrec // 2
     kinds = [0] * n_k + [1] * (nrec - n_k)
     payloads = [rng.integers(0, 256, n, dtype=np.uint8) for _ in range(nrec)]
@@ -60,7 +62,8 @@ def _reload_case(sess, rng, nrec, n, ticket0):
     cv = torch.full_like(ck, FILL)
     fail = torch.zeros(1, dtype=torch.int32, device=DEV)
     dw = _dev(wire)
-    sess.reload_layer(dw, n, nrec, n_k, ck, cv, _dev(slots_np), ticket_base=ticket0, fail_count=fail)
+    sess.reload_layer(dw, n, nrec, n_k, ck, cv, _dev(slots_np), ticket_base=ticket0, fail_count=fail,
+                      verify_before_release=strict)
     kk, vv, ww = _host(ck), _host(cv), _host(dw)
     toff = W.align32(n)
     statuses = [int(ww[r * st + toff + 16:r * st + toff + 20].view(np.uint32)[0]) for r in range(nrec)]
@@ -113,17 +116,21 @@ def test_layout_sweep_matches_openssl(direction):
             ticket += nrec
 
 
-@pytest.mark.parametrize("direction", ["reload", "writeback"])
+@pytest.mark.parametrize("direction", ["reload", "reload_verify_first", "writeback"])
 def test_random_layouts_match_openssl(direction):
     """Seeded random shapes and layout knobs beyond the hand-picked ones:
     record counts from one to past four per CU, record sizes from one byte
     to past four rows (most with a partial last block), the minimum rows per
     share (1 to 8) and the straddle cost (0 to 13), so shares straddle, pair
     up or run in rounds in combinations no fixed list names.  Each case
-    against OpenSSL as above."""
-    rng = np.random.default_rng(7300 if direction == "reload" else 7400)
+    against OpenSSL as above; reloads also with verify-before-release (tags
+    first, then decryption released by status)."""
+    rng = np.random.default_rng({"reload": 7300, "reload_verify_first": 7350, "writeback": 7400}[direction])
     sess = si.GcmSession(KEY, SALT, 0, max_record_bytes=70000)
-    case = _reload_case if direction == "reload" else _writeback_case
+    if direction == "writeback":
+        case = _writeback_case
+    else:
+        case = functools.partial(_reload_case, strict=direction == "reload_verify_first")
     ticket = 1
     try:
         for i in range(14):
