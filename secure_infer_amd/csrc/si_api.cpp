@@ -1111,7 +1111,7 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
         // Tags and statuses first (nothing else written), then the release.
         if (si::launch_gcm(2, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) return -1;
         if (phases == 1) return 0;
-        if (si::launch_release(stream, s->ctx->dev, b, d->nrec, d->bytes, al || codec, gate, ev_rel) != hipSuccess)
+        if (si::launch_release(stream, s->ctx->dev, b, d->nrec, d->bytes, al || codec, gate, cu_count(), ev_rel) != hipSuccess)
             return -1;
     } else if (si::launch_gcm(0, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) {
         return -1;

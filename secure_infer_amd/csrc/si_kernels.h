@@ -160,8 +160,10 @@ hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const Rec
 // same batch wrote every status): each record's plaintext to its
 // destination if its status is 1, zeros otherwise.  nrec records of `bytes`.
 #define SI_RELEASE_THREADS 512
+// cus: the device's compute units (the grid's size).
 hipError_t launch_release(hipStream_t stream, const GcmCtx* ctx, const RecBatch& b, uint32_t nrec, uint64_t bytes,
-                          bool aligned, const uint32_t* gate, const LaunchEvents& ev = LaunchEvents());
+                          bool aligned, const uint32_t* gate, uint32_t cus,
+                          const LaunchEvents& ev = LaunchEvents());
 hipError_t launch_ctr(hipStream_t stream, const GcmCtx* ctx, const uint8_t* in, uint8_t* out,
                       uint64_t bytes, const uint32_t iv[4]);
 hipError_t launch_auth_gate(hipStream_t stream, uint8_t* data, const uint32_t* status,

@@ -506,7 +506,7 @@ hipError_t launch_gcm(int mode, hipStream_t stream, const GcmCtx* ctx, const Rec
 }
 
 hipError_t launch_release(hipStream_t stream, const GcmCtx* ctx, const RecBatch& b, uint32_t nrec, uint64_t bytes,
-                          bool, const uint32_t* gate, const LaunchEvents&)
+                          bool, const uint32_t* gate, uint32_t, const LaunchEvents&)
 {
     S(stream)->push([ctx, b, nrec, bytes, gate] {
         if (gated(gate)) return;
