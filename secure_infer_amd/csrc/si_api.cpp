@@ -360,7 +360,7 @@ static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad
         const uint64_t pad = uint64_t(s.rows) * SI_T - m;  // blocks of row 0 before X
         s.ek_row0 = (s.a >= 1 && s.n >= 1 && pad + s.a <= SI_T - 1) ? 1u : 0u;
     }
-    // W workgroups, one per CU, none with fewer than g_min_rows rows, and at
+    // W workgroups, one per CU, none with fewer than min_rows rows, and at
     // least nrec of them (rounded to whole rounds of one per CU) so that no
     // share spans more than R rows, i.e. two records at most.
     const uint64_t G = uint64_t(nrec) * s.rows;
