@@ -35,6 +35,8 @@ MAX_WG = 768
 @pytest.fixture
 def lib():
     L = _lib.load()
+    assert L.secure_infer_gpu_set_chunk_rows(si.gcm.DEFAULT_CHUNK_ROWS) == 0
+    assert L.secure_infer_gpu_set_straddle_rows(si.gcm.DEFAULT_STRADDLE_ROWS) == 0
     yield L
     assert L.secure_infer_gpu_set_chunk_rows(si.gcm.DEFAULT_CHUNK_ROWS) == 0
     assert L.secure_infer_gpu_set_straddle_rows(si.gcm.DEFAULT_STRADDLE_ROWS) == 0
