@@ -471,6 +471,8 @@ def run_workload(name: str, args, torch, si, steps: int, warmup: int, with_cpu: 
     L, H, D, NB, NS, bits = cfg["layers"], cfg["heads"], cfg["dim"], cfg["blocks"], cfg["slots"], cfg["bits"]
     if args.chunk_rows:
         si.set_chunk_rows(args.chunk_rows)
+    if args.straddle_rows >= 0:
+        si.set_straddle_rows(args.straddle_rows)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev).manual_seed(1234)
@@ -722,6 +724,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
     ap.add_argument("--chunk-rows", type=int, default=0)
+    ap.add_argument("--straddle-rows", type=int, default=-1,
+                    help="straddle cost of the record kernel's share layout (default: the library's)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=3,

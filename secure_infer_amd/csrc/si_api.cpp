@@ -431,7 +431,11 @@ static si::Sched make_sched_uncached(uint32_t nrec, uint64_t bytes, uint64_t aad
 // per int4 Qwen2.5-7B layer launch and ~3 us per bf16 Llama-3-8B one on an
 // x86 host core; a cached one, 0.13 us).  The cache holds no key material:
 // the length block's term L * H comes from the context (DevCtx::lh_of).
-si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, DevCtx& c)
+// straddle: the straddle cost to lay out with, or kTunedStraddle for the
+// tuning's (secure_infer_gpu_set_straddle_rows).
+constexpr uint32_t kTunedStraddle = ~0u;
+si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, DevCtx& c,
+                     uint32_t straddle = kTunedStraddle)
 {
     struct Key {
         uint64_t bytes, aad_bytes;
@@ -451,7 +455,7 @@ si::Sched make_sched(uint32_t nrec, uint64_t bytes, uint64_t aad_bytes, DevCtx& 
     k.nrec = nrec;
     k.cus = cu_count();
     k.min_rows = uint32_t(g_min_rows.load(std::memory_order_relaxed));
-    k.straddle = g_straddle_rows.load(std::memory_order_relaxed);
+    k.straddle = straddle == kTunedStraddle ? g_straddle_rows.load(std::memory_order_relaxed) : straddle;
     k.fixed = g_wg_fixed_rows;
     k.pair = g_pair_records ? 1u : 0u;
     if (!cache) cache.reset(new Entry[kEntries]);
@@ -1109,7 +1113,22 @@ static int reload_launch(hipStream_t stream, si_session* s, const si_reload_desc
     if (codec) ev_dq.stop = ev.stop;
     if (strict) {
         // Tags and statuses first (nothing else written), then the release.
-        if (si::launch_gcm(2, stream, s->ctx->dev, b, sc2, acc, al, ev_rec) != hipSuccess) return -1;
+        // The verification hashes without decrypting, so its rows cost
+        // about a third of a decrypting row's time while a straddling
+        // share's second start costs the same: it is laid out without
+        // straddling shares (MI355X, bf16 Llama-3-8B layer 44.7 -> 41.6 us
+        // per layer, ABBA on one GPU).  A layout that pairs records keeps
+        // the caller's, whose parking area is sized for it.
+        si::Sched sv = sc2;
+        if (!sc.pairs) {
+            si::Sched t = make_sched(d->nrec, d->bytes, 64, *s->ctx, 256u);
+            if (!t.pairs) {
+                t.status_out = d->status_out;
+                t.gate = gate;
+                sv = t;
+            }
+        }
+        if (si::launch_gcm(2, stream, s->ctx->dev, b, sv, acc, al, ev_rec) != hipSuccess) return -1;
         if (phases == 1) return 0;
         if (si::launch_release(stream, s->ctx->dev, b, d->nrec, d->bytes, al || codec, gate, cu_count(), ev_rel) != hipSuccess)
             return -1;
